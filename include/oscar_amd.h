@@ -1,0 +1,209 @@
+/*
+ * oscar_amd.h -- C ABI of the MI355X (gfx950) OSCAR INT2 rotated KV-cache path.
+ *
+ * Plain C: device pointers, byte strides, shapes and a HIP stream passed as
+ * void*.  No torch types.  Every entry point validates its arguments on the
+ * host, launches asynchronously on `stream`, allocates nothing (scratch memory
+ * is caller-provided) and returns 0 or a negative errno-style status; the
+ * message for the last failure on the calling thread is returned by
+ * oscar_last_error().
+ *
+ * Reference interfaces replaced (jpl123123/oscar, Python/Triton-Ascend):
+ *   oscar_store_v1       oscar_ascend/kernels/store_kernel.py:54-102 (oscar_store_ref)
+ *                        and :247-279 (oscar_store_triton), fused with
+ *                        oscar_ascend/backend.py:130-148 (_rotate_clip),
+ *                        :151-198 (do_kv_cache_update tag invalidation) and
+ *                        :513-555 (_staging_write window + owner tags), plus the
+ *                        read-path rotations of backend.py:370-373.
+ *   oscar_rotate_v1      oscar_ascend/backend.py:371 (q @ R_k) and :382
+ *                        (out_rot @ R_v^T) -- dense D x D rotation.
+ *   oscar_attn_plan_v1   oscar_ascend/kernels/slab_attention.py:31-92
+ *                        (plan_slabs / slab_steps host planning).
+ *   oscar_attn_decode_v1 oscar_ascend/kernels/slab_attention.py:376-476
+ *                        (slab_attention: history waves + current chunk + LSE merge).
+ *   oscar_attn_prefill_v1 oscar_ascend/kernels/prefill.py:69-72 (oscar_prefill,
+ *                        fresh-only causal prefill) and the long-continuation use of
+ *                        slab_attention (history + causal current chunk).
+ *
+ * A maintainer binds these from the reference's Python backend with ctypes
+ * (see INTEGRATION.md); oscar_amd/_lib.py is that binding.
+ */
+#ifndef OSCAR_AMD_H
+#define OSCAR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OSCAR_ABI_VERSION 1
+
+/* element types of dense inputs/outputs */
+enum oscar_dtype { OSCAR_F32 = 0, OSCAR_F16 = 1, OSCAR_BF16 = 2 };
+
+/* Packed INT2 paged cache pair, addressed as bytes (cache.view(uint8)).
+ * Slot layout (oscar_ascend/format.py:19-38): K slot [0:8] = K scale, K zero,
+ * V scale, V zero (fp16 little endian), [32:32+D/4] = K codes; V slot
+ * [0:D/4] = V codes.  Strides are in bytes: block, token-in-block, kv head. */
+typedef struct oscar_cache_v1 {
+  uint8_t* k;
+  uint8_t* v;
+  int64_t num_blocks;
+  int64_t block_size;
+  int64_t num_kv_heads;
+  int64_t head_dim;
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+} oscar_cache_v1;
+
+/* FP32 sink/recent staging window (backend.py:492-511).  stage_k/stage_v are
+ * contiguous [rows, block_size, num_kv_heads, head_dim] fp32; owner is
+ * contiguous [rows, block_size] int64 (-1 = empty, else physical block id). */
+typedef struct oscar_staging_v1 {
+  float* stage_k;
+  float* stage_v;
+  int64_t* owner;
+  int64_t rows;
+} oscar_staging_v1;
+
+enum oscar_stage_mode {
+  OSCAR_STAGE_NONE = 0,       /* no staging arena: plain INT2 store */
+  OSCAR_STAGE_INVALIDATE = 1, /* standalone KV update: owner[seat] = -1 for written seats */
+  OSCAR_STAGE_WRITE = 2       /* forward: last writer per seat sets owner (keep ? block : -1)
+                                 and kept seats receive the unclipped fp32 rotated K/V */
+};
+
+typedef struct oscar_store_args_v1 {
+  /* new tokens: key/value [num_tokens, num_kv_heads, head_dim], row stride in elements */
+  const void* key;
+  const void* value;
+  int32_t kv_dtype;             /* OSCAR_BF16 / OSCAR_F16 / OSCAR_F32 */
+  int64_t num_tokens;
+  int64_t key_stride_token;
+  int64_t value_stride_token;
+  /* optional query [num_tokens, num_q_heads, head_dim] to rotate for the read path */
+  const void* query;            /* may be NULL */
+  int64_t num_q_heads;
+  int64_t query_stride_token;
+  /* rotations [head_dim, head_dim] fp32 row-major (x_rot = x @ R); NULL = identity */
+  const float* rk;
+  const float* rv;
+  float k_clip_ratio;           /* 0 disables the sort-based clip */
+  float v_clip_ratio;
+  const int64_t* slot_mapping;  /* [num_tokens]; negative = skip */
+  oscar_cache_v1 cache;
+  /* staging */
+  int32_t stage_mode;           /* enum oscar_stage_mode */
+  oscar_staging_v1 staging;
+  const int32_t* query_start_loc; /* [num_reqs + 1] device, clipped to num_tokens */
+  const int32_t* seq_lens;        /* [num_reqs] device */
+  int32_t num_reqs;
+  int32_t recent_tokens;
+  int32_t sink_tokens_eff;        /* (sink // block_size) * block_size */
+  /* optional read-path outputs in kv_dtype, contiguous [num_tokens, H, head_dim] */
+  void* query_rot;              /* x @ R_k for the queries (may be NULL) */
+  void* key_rot;                /* x @ R_k, unclipped (may be NULL) */
+  void* value_rot;              /* x @ R_v, unclipped (may be NULL) */
+  /* scratch: last-writer claims, entries (epoch << 32 | token); zero-initialised once */
+  int64_t* slot_claims;         /* [num_blocks * block_size] */
+  int64_t* seat_claims;         /* [rows * block_size] (stage mode 2) */
+  int64_t epoch;                /* strictly increasing per call on a device, in [1, 2^31) */
+  /* fp32 rotated K/V staging between the two launches, 16-byte aligned,
+   * >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
+  void* workspace;
+  int64_t workspace_bytes;
+} oscar_store_args_v1;
+
+int64_t oscar_store_workspace_bytes_v1(int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim);
+int oscar_store_v1(const oscar_store_args_v1* args, void* stream);
+
+/* y[M, D] = x[M, D] @ R[D, D] (or @ R^T when transpose != 0); fp32 accumulate
+ * of bf16 hi/lo split products (|error| < 2^-16 |x||R|); out in out_dtype. */
+typedef struct oscar_rotate_args_v1 {
+  const void* x;
+  int32_t x_dtype;
+  int64_t rows;
+  int64_t x_stride_row;         /* elements */
+  const float* r;
+  int32_t transpose;
+  void* out;
+  int32_t out_dtype;
+  int64_t out_stride_row;       /* elements */
+  int64_t head_dim;
+} oscar_rotate_args_v1;
+
+int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
+
+/* Work planning for the split-K decode (host function, no device access).
+ * qsl/seqs are host arrays.  Writes up to max_items work items of
+ * OSCAR_WORK_INTS int32 each and returns the item count (or < 0). */
+#define OSCAR_WORK_INTS 8
+typedef struct oscar_plan_v1 {
+  int32_t num_items;
+  int32_t num_groups;           /* request x kv-head groups with queries */
+  int64_t partial_bytes;        /* workspace bytes needed by oscar_attn_decode_v1 */
+} oscar_plan_v1;
+
+int oscar_attn_plan_v1(const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs,
+                       int32_t has_new, int32_t num_kv_heads, int32_t group, int32_t head_dim,
+                       int32_t chunk_tokens, int32_t target_items, int32_t* items,
+                       int32_t max_items, int32_t* groups, int32_t max_groups, oscar_plan_v1* plan);
+
+typedef struct oscar_attn_args_v1 {
+  const void* q;                /* [n, Hq, D] rotated queries, OSCAR_BF16 */
+  int64_t num_tokens;
+  int64_t num_q_heads;
+  int64_t q_stride_token;       /* elements */
+  const void* k_new;            /* [n, Hk, D] rotated current chunk or NULL (cache-only) */
+  const void* v_new;
+  int64_t kv_new_stride_token;
+  oscar_cache_v1 cache;
+  const int32_t* block_table;   /* [num_reqs, max_blocks] */
+  int64_t block_table_stride;
+  const int32_t* query_start_loc; /* device [num_reqs + 1] */
+  const int32_t* seq_lens;        /* device [num_reqs] */
+  int32_t num_reqs;
+  const oscar_staging_v1* staging; /* NULL = no window */
+  float scale;
+  const int32_t* items;         /* device copy of the plan */
+  int32_t num_items;
+  const int32_t* groups;
+  int32_t num_groups;
+  void* workspace;              /* >= plan.partial_bytes */
+  float* out_rot;               /* [n, Hq, D] fp32 rotated output (required) */
+  float* lse;                   /* [n, Hq] natural-log LSE (required) */
+} oscar_attn_args_v1;
+
+int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
+
+typedef struct oscar_prefill_args_v1 {
+  const void* q;                /* [n, Hq, D] bf16 */
+  int64_t q_stride_token;
+  const void* k;                /* [n, Hk, D] bf16 current chunk */
+  const void* v;
+  int64_t kv_stride_token;
+  int64_t num_tokens;
+  int64_t num_q_heads;
+  int64_t num_kv_heads;
+  int64_t head_dim;
+  int64_t history;              /* cached prefix length (0 = fresh-only) */
+  oscar_cache_v1 cache;         /* used when history > 0 */
+  const int32_t* block_table_row; /* [max_blocks] of this request */
+  const oscar_staging_v1* staging;
+  float scale;
+  void* out;                    /* [n, Hq, D]: bf16 when history == 0, else fp32 rotated */
+  int64_t out_stride_token;
+  float* lse;                   /* [n, Hq] or NULL */
+} oscar_prefill_args_v1;
+
+int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream);
+
+const char* oscar_last_error(void);
+int oscar_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OSCAR_AMD_H */

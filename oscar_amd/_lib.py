@@ -1,0 +1,124 @@
+"""ctypes binding of liboscar_amd.so (the C ABI declared in include/oscar_amd.h).
+
+This is the binding a maintainer adds to the reference's Python backend to reach
+the HIP kernels.  Loading fails loudly when the library is missing: there is no
+CPU fallback in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "liboscar_amd.so"
+
+OSCAR_F32, OSCAR_F16, OSCAR_BF16 = 0, 1, 2
+STAGE_NONE, STAGE_INVALIDATE, STAGE_WRITE = 0, 1, 2
+WORK_INTS = 8
+
+vp = C.c_void_p
+i32, i64, f32 = C.c_int32, C.c_int64, C.c_float
+
+
+class Cache(C.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("num_blocks", i64), ("block_size", i64),
+                ("num_kv_heads", i64), ("head_dim", i64), ("k_stride", i64 * 3),
+                ("v_stride", i64 * 3)]
+
+
+class Staging(C.Structure):
+    _fields_ = [("stage_k", vp), ("stage_v", vp), ("owner", vp), ("rows", i64)]
+
+
+class StoreArgs(C.Structure):
+    _fields_ = [
+        ("key", vp), ("value", vp), ("kv_dtype", i32), ("num_tokens", i64),
+        ("key_stride_token", i64), ("value_stride_token", i64),
+        ("query", vp), ("num_q_heads", i64), ("query_stride_token", i64),
+        ("rk", vp), ("rv", vp), ("k_clip_ratio", f32), ("v_clip_ratio", f32),
+        ("slot_mapping", vp), ("cache", Cache),
+        ("stage_mode", i32), ("staging", Staging),
+        ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
+        ("recent_tokens", i32), ("sink_tokens_eff", i32),
+        ("query_rot", vp), ("key_rot", vp), ("value_rot", vp),
+        ("slot_claims", vp), ("seat_claims", vp), ("epoch", i64),
+        ("workspace", vp), ("workspace_bytes", i64),
+    ]
+
+
+class RotateArgs(C.Structure):
+    _fields_ = [("x", vp), ("x_dtype", i32), ("rows", i64), ("x_stride_row", i64),
+                ("r", vp), ("transpose", i32), ("out", vp), ("out_dtype", i32),
+                ("out_stride_row", i64), ("head_dim", i64)]
+
+
+class Plan(C.Structure):
+    _fields_ = [("num_items", i32), ("num_groups", i32), ("partial_bytes", i64)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("q", vp), ("num_tokens", i64), ("num_q_heads", i64), ("q_stride_token", i64),
+        ("k_new", vp), ("v_new", vp), ("kv_new_stride_token", i64),
+        ("cache", Cache), ("block_table", vp), ("block_table_stride", i64),
+        ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
+        ("staging", C.POINTER(Staging)), ("scale", f32),
+        ("items", vp), ("num_items", i32), ("groups", vp), ("num_groups", i32),
+        ("workspace", vp), ("out_rot", vp), ("lse", vp),
+    ]
+
+
+class PrefillArgs(C.Structure):
+    _fields_ = [
+        ("q", vp), ("q_stride_token", i64), ("k", vp), ("v", vp), ("kv_stride_token", i64),
+        ("num_tokens", i64), ("num_q_heads", i64), ("num_kv_heads", i64), ("head_dim", i64),
+        ("history", i64), ("cache", Cache), ("block_table_row", vp),
+        ("staging", C.POINTER(Staging)), ("scale", f32), ("out", vp),
+        ("out_stride_token", i64), ("lse", vp),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/oscar_amd.h
+SIGNATURES = {
+    "oscar_abi_version": (C.c_int, []),
+    "oscar_last_error": (C.c_char_p, []),
+    "oscar_store_workspace_bytes_v1": (i64, [i64, i64, i64]),
+    "oscar_store_v1": (C.c_int, [C.POINTER(StoreArgs), vp]),
+    "oscar_rotate_v1": (C.c_int, [C.POINTER(RotateArgs), vp]),
+    "oscar_attn_plan_v1": (C.c_int, [C.POINTER(i32), C.POINTER(i32), i32, i32, i32, i32, i32,
+                                     i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
+                                     C.POINTER(Plan)]),
+    "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "oscar_attn_prefill_v1": (C.c_int, [C.POINTER(PrefillArgs), vp]),
+}
+
+_LIB = None
+
+
+class OscarLibraryError(RuntimeError):
+    pass
+
+
+def load() -> C.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise OscarLibraryError(
+            f"{LIB_PATH} is missing: build it with `python -m oscar_amd.build` "
+            "(no CPU fallback exists for the OSCAR HIP path)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.oscar_abi_version() != 1:
+        raise OscarLibraryError("liboscar_amd.so ABI version mismatch")
+    _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().oscar_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({status}): {msg}")

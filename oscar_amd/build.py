@@ -1,0 +1,63 @@
+"""Build liboscar_amd.so for gfx950 with hipcc (in-tree, no torch headers).
+
+``python -m oscar_amd.build`` compiles every source under ``oscar_amd/csrc`` into
+``oscar_amd/liboscar_amd.so``.  All HIP code is compiled with packed FP32
+instructions disabled (``-packed-fp32-ops``).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "liboscar_amd.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+SOURCES = ["capi.cpp", "store.hip", "rotate.hip", "attn_decode.hip", "attn_prefill.hip"]
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def sources() -> list[Path]:
+    return [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile each source to an object in oscar_amd/_build/, then link the .so."""
+    out_dir = HERE / "_build"
+    out_dir.mkdir(exist_ok=True)
+    objs = []
+    for src in sources():
+        obj = out_dir / (src.stem + ".o")
+        cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+        if src.suffix == ".cpp":
+            cmd[1:1] = ["-x", "hip"]
+        _run(cmd, verbose)
+        objs.append(str(obj))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,72 @@
+// Shared device/host helpers for the gfx950 OSCAR kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/oscar_amd.h"
+
+namespace oscar {
+
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+typedef __attribute__((ext_vector_type(2))) int i32x2;
+
+// ---------------------------------------------------------------- host errors
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+#define OSCAR_CHECK_LAUNCH(name)                                                   \
+  do {                                                                             \
+    hipError_t e_ = hipGetLastError();                                             \
+    if (e_ != hipSuccess) return ::oscar::fail(-5, "%s launch: %s", name,         \
+                                               hipGetErrorString(e_));            \
+  } while (0)
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_bits_to_f32(unsigned short b) {
+  return __uint_as_float(((unsigned)b) << 16);
+}
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float x) {
+  // round to nearest even; NaN stays NaN (quiet)
+  unsigned u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (unsigned short)(u >> 16);
+}
+__device__ __forceinline__ unsigned short f32_to_f16_bits(float x) {
+  return __half_as_ushort(__float2half_rn(x));
+}
+__device__ __forceinline__ float f16_bits_to_f32(unsigned short b) {
+  return __half2float(__ushort_as_half(b));
+}
+
+// load element i of a dense row in dtype (F32/F16/BF16) as float
+__device__ __forceinline__ float load_elem(const void* base, int32_t dtype, int64_t i) {
+  if (dtype == OSCAR_BF16) return bf16_bits_to_f32(((const unsigned short*)base)[i]);
+  if (dtype == OSCAR_F16) return f16_bits_to_f32(((const unsigned short*)base)[i]);
+  return ((const float*)base)[i];
+}
+__device__ __forceinline__ void store_elem(void* base, int32_t dtype, int64_t i, float x) {
+  if (dtype == OSCAR_BF16) ((unsigned short*)base)[i] = f32_to_bf16_bits(x);
+  else if (dtype == OSCAR_F16) ((unsigned short*)base)[i] = f32_to_f16_bits(x);
+  else ((float*)base)[i] = x;
+}
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ float wave_max(float x) {
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_min(float x) {
+  for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
+  return x;
+}
+
+}  // namespace oscar

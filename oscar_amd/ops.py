@@ -1,0 +1,347 @@
+"""Torch-facing wrappers around the C ABI (include/oscar_amd.h).
+
+PyTorch is used for device memory and streams only; every computation runs in
+liboscar_amd.so.  All functions raise when the library is missing or a launch
+fails; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import (OSCAR_BF16, OSCAR_F16, OSCAR_F32, STAGE_INVALIDATE, STAGE_NONE,
+                   STAGE_WRITE, WORK_INTS)
+
+_DTYPES = {torch.float32: OSCAR_F32, torch.float16: OSCAR_F16, torch.bfloat16: OSCAR_BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(*tensors) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("OSCAR HIP ops need device tensors (no CPU fallback)")
+
+
+def cache_struct(k_cache: torch.Tensor, v_cache: torch.Tensor, head_dim: int) -> _lib.Cache:
+    """Byte view of a packed cache pair [num_blocks, block_size, Hk, D] (int8 or bf16)."""
+    k8, v8 = k_cache.view(torch.uint8), v_cache.view(torch.uint8)
+    if k8.ndim != 4 or v8.ndim != 4 or not k8.is_contiguous() or not v8.is_contiguous():
+        raise ValueError("OSCAR requires contiguous [blocks, tokens, heads, bytes] caches")
+    c = _lib.Cache()
+    c.k, c.v = k8.data_ptr(), v8.data_ptr()
+    c.num_blocks, c.block_size, c.num_kv_heads = k8.shape[0], k8.shape[1], k8.shape[2]
+    c.head_dim = head_dim
+    for i in range(3):
+        c.k_stride[i] = k8.stride(i)
+        c.v_stride[i] = v8.stride(i)
+    return c
+
+
+def staging_struct(stage) -> _lib.Staging | None:
+    if stage is None:
+        return None
+    sk, sv, owner = stage
+    if sk.dtype != torch.float32 or owner.dtype != torch.int64:
+        raise ValueError("staging arena must be fp32 values and int64 owner tags")
+    if not (sk.is_contiguous() and sv.is_contiguous() and owner.is_contiguous()):
+        raise ValueError("Streaming staging tensors must be contiguous")
+    s = _lib.Staging()
+    s.stage_k, s.stage_v, s.owner, s.rows = sk.data_ptr(), sv.data_ptr(), owner.data_ptr(), owner.shape[0]
+    return s
+
+
+class DeviceScratch:
+    """Per-device scratch: last-writer claim tables and growable workspaces."""
+
+    _by_device: dict = {}
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.epoch = 0
+        self.slot_claims = torch.zeros(0, dtype=torch.int64, device=device)
+        self.seat_claims = torch.zeros(0, dtype=torch.int64, device=device)
+        self.store_ws = torch.empty(0, dtype=torch.uint8, device=device)
+        self.attn_ws = torch.empty(0, dtype=torch.uint8, device=device)
+
+    @classmethod
+    def get(cls, device: torch.device) -> "DeviceScratch":
+        key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+        if key not in cls._by_device:
+            cls._by_device[key] = cls(torch.device("cuda", key[1]))
+        return cls._by_device[key]
+
+    def next_epoch(self) -> int:
+        self.epoch += 1
+        if self.epoch >= 2 ** 31 - 1:  # claims are epoch-tagged: restart from zeroed tables
+            self.slot_claims.zero_()
+            self.seat_claims.zero_()
+            self.epoch = 1
+        return self.epoch
+
+    def claims(self, slots: int, seats: int):
+        if self.slot_claims.numel() < slots:
+            self.slot_claims = torch.zeros(slots, dtype=torch.int64, device=self.device)
+        if self.seat_claims.numel() < max(seats, 1):
+            self.seat_claims = torch.zeros(max(seats, 1), dtype=torch.int64, device=self.device)
+        return self.slot_claims, self.seat_claims
+
+    def store_workspace(self, nbytes: int) -> torch.Tensor:
+        if self.store_ws.numel() < nbytes:
+            self.store_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.store_ws
+
+    def attn_workspace(self, nbytes: int) -> torch.Tensor:
+        if self.attn_ws.numel() < nbytes:
+            self.attn_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.attn_ws
+
+
+# ------------------------------------------------------------------------ store
+def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=None,
+          k_clip=0.0, v_clip=0.0, stage=None, stage_mode=STAGE_NONE, qsl_dev=None,
+          seqs_dev=None, num_reqs=0, recent_tokens=0, sink_tokens_eff=0, query=None,
+          query_rot=None, key_rot=None, value_rot=None):
+    """Rotate + clip + INT2 quantize + scatter (+ staging window) in one C call.
+
+    key/value [N, Hk, D] (bf16/fp16/fp32), slot_mapping [N] int64 (negative = skip).
+    rk/rv fp32 [D, D] or None for identity.  Optional query [N, Hq, D] and
+    *_rot outputs receive the unclipped rotated values in the input dtype.
+    """
+    _require_cuda(key, value, k_cache, v_cache, slot_mapping)
+    n = slot_mapping.shape[0]
+    if n == 0:
+        return
+    lib = _lib.load()
+    dev = key.device
+    hk = k_cache.shape[2]
+    if key.dtype not in _DTYPES or value.dtype != key.dtype:
+        raise ValueError("key/value must share a float dtype")
+    key = key[:n].reshape(n, hk, head_dim)
+    value = value[:n].reshape(n, hk, head_dim)
+    if key.stride(2) != 1 or key.stride(1) != head_dim or value.stride(2) != 1 or value.stride(1) != head_dim:
+        key, value = key.contiguous(), value.contiguous()
+    slot_mapping = slot_mapping.to(device=dev, dtype=torch.int64).contiguous()
+    scratch = DeviceScratch.get(dev)
+    cache = cache_struct(k_cache, v_cache, head_dim)
+    st = staging_struct(stage)
+    seats = 0 if st is None else st.rows * cache.block_size
+    slot_claims, seat_claims = scratch.claims(cache.num_blocks * cache.block_size, seats)
+    a = _lib.StoreArgs()
+    a.key, a.value = key.data_ptr(), value.data_ptr()
+    a.kv_dtype = _DTYPES[key.dtype]
+    a.num_tokens = n
+    a.key_stride_token, a.value_stride_token = key.stride(0), value.stride(0)
+    if query is not None:
+        query = query[:n]
+        if query.stride(-1) != 1 or query.stride(-2) != head_dim:
+            query = query.contiguous()
+        a.query, a.num_q_heads, a.query_stride_token = query.data_ptr(), query.shape[1], query.stride(0)
+    for name, r in (("rk", rk), ("rv", rv)):
+        if r is not None:
+            if r.dtype != torch.float32 or not r.is_contiguous() or r.shape != (head_dim, head_dim):
+                raise ValueError(f"{name} must be a contiguous fp32 [{head_dim}, {head_dim}] tensor")
+            setattr(a, name, r.data_ptr())
+    a.k_clip_ratio, a.v_clip_ratio = float(k_clip), float(v_clip)
+    a.slot_mapping = slot_mapping.data_ptr()
+    a.cache = cache
+    a.stage_mode = stage_mode if st is not None else STAGE_NONE
+    if st is not None:
+        a.staging = st
+    if stage_mode == STAGE_WRITE:
+        a.query_start_loc, a.seq_lens = qsl_dev.data_ptr(), seqs_dev.data_ptr()
+        a.num_reqs, a.recent_tokens, a.sink_tokens_eff = num_reqs, recent_tokens, sink_tokens_eff
+    for name, t in (("query_rot", query_rot), ("key_rot", key_rot), ("value_rot", value_rot)):
+        if t is not None:
+            if not t.is_contiguous() or t.dtype != key.dtype:
+                raise ValueError(f"{name} must be contiguous in the key dtype")
+            setattr(a, name, t.data_ptr())
+    a.slot_claims, a.seat_claims = slot_claims.data_ptr(), seat_claims.data_ptr()
+    a.epoch = scratch.next_epoch()
+    need = lib.oscar_store_workspace_bytes_v1(n, hk, head_dim)
+    ws = scratch.store_workspace(need)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(lib.oscar_store_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_store_v1")
+
+
+# ------------------------------------------------------------------------ rotate
+def rotate(x: torch.Tensor, r: torch.Tensor, *, transpose=False, out_dtype=None, out=None):
+    """x [..., D] @ R (or @ R^T) with MFMA hi/lo products; returns out_dtype (default x dtype)."""
+    _require_cuda(x, r)
+    d = x.shape[-1]
+    rows = x.numel() // d
+    x2 = x.reshape(rows, d)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    out_dtype = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty(*x.shape[:-1], d, dtype=out_dtype, device=x.device)
+    o2 = out.reshape(rows, d)
+    a = _lib.RotateArgs()
+    a.x, a.x_dtype, a.rows, a.x_stride_row = x2.data_ptr(), _DTYPES[x2.dtype], rows, x2.stride(0)
+    a.r, a.transpose = r.contiguous().data_ptr(), int(bool(transpose))
+    a.out, a.out_dtype, a.out_stride_row, a.head_dim = o2.data_ptr(), _DTYPES[out_dtype], o2.stride(0), d
+    lib = _lib.load()
+    _lib.check(lib.oscar_rotate_v1(C.byref(a), C.c_void_p(_stream(x.device))), "oscar_rotate_v1")
+    return out
+
+
+# ------------------------------------------------------------------------ decode attention
+@dataclass
+class DecodePlan:
+    items: torch.Tensor      # device int32 [num_items, WORK_INTS]
+    groups: torch.Tensor     # device int32 [num_groups, 4]
+    qsl: torch.Tensor        # device int32 [B + 1]
+    seqs: torch.Tensor       # device int32 [B]
+    num_items: int
+    num_groups: int
+    partial_bytes: int
+    host_items: list
+    host_qsl: list
+    host_seqs: list
+    has_new: bool
+
+
+def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, group: int,
+                head_dim: int, device, target_items: int | None = None,
+                chunk_tokens: int = 8192) -> DecodePlan:
+    """Split-K plan (host): items of whole 32-token tiles, balanced over the CUs."""
+    lib = _lib.load()
+    nreq = len(seqs)
+    qa = (C.c_int32 * (nreq + 1))(*qsl)
+    sa = (C.c_int32 * max(nreq, 1))(*seqs)
+    if target_items is None:
+        target_items = torch.cuda.get_device_properties(device).multi_processor_count
+    plan = _lib.Plan()
+    n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
+                               chunk_tokens, target_items, None, 0, None, 0, C.byref(plan))
+    if n < 0:
+        _lib.check(n, "oscar_attn_plan_v1")
+    items = (C.c_int32 * max(plan.num_items * WORK_INTS, 1))()
+    groups = (C.c_int32 * max(plan.num_groups * 4, 1))()
+    n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
+                               chunk_tokens, target_items, items, plan.num_items, groups,
+                               plan.num_groups, C.byref(plan))
+    if n < 0:
+        _lib.check(n, "oscar_attn_plan_v1")
+    host_items = list(items)[: plan.num_items * WORK_INTS]
+    it = torch.tensor(host_items or [0], dtype=torch.int32).view(-1)
+    gr = torch.tensor(list(groups)[: plan.num_groups * 4] or [0], dtype=torch.int32)
+    return DecodePlan(it.to(device), gr.to(device),
+                      torch.tensor(qsl, dtype=torch.int32).to(device),
+                      torch.tensor(seqs or [0], dtype=torch.int32).to(device),
+                      plan.num_items, plan.num_groups, plan.partial_bytes, host_items,
+                      list(qsl), list(seqs), bool(has_new))
+
+
+def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None:
+    """streaming_attention.py:48-53: the block table must cover every history."""
+    if table.ndim != 2 or table.shape[0] < len(plan.host_seqs):
+        raise ValueError("Missing request block-table rows")
+    for a, b, seq in zip(plan.host_qsl, plan.host_qsl[1:], plan.host_seqs):
+        hist = seq - (b - a) if plan.has_new else seq
+        if b > a and math.ceil(hist / block_size) > table.shape[1]:
+            raise ValueError("Block table cannot cover the history")
+
+
+def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: DecodePlan, scale,
+                     stage=None, *, head_dim, out_rot=None, lse=None):
+    """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32)."""
+    _require_cuda(q, k_cache, v_cache, block_table)
+    if q.dtype != torch.bfloat16:
+        raise ValueError("OSCAR HIP attention requires bf16 queries")
+    n, hq, _ = q.shape
+    dev = q.device
+    if out_rot is None:
+        out_rot = torch.zeros(n, hq, head_dim, dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.full((n, hq), -math.inf, dtype=torch.float32, device=dev)
+    if plan.num_items == 0 or n == 0:
+        return out_rot, lse
+    if q.stride(2) != 1 or q.stride(1) != head_dim:
+        q = q.contiguous()
+    if (k_new is None) != (v_new is None):
+        raise ValueError("Both new K and V must be supplied together")
+    if k_new is not None:
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise ValueError("Current K/V must match the query dtype")
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    table = block_table.to(device=dev, dtype=torch.int32)
+    if table.stride(1) != 1:
+        table = table.contiguous()
+    if plan.has_new != (k_new is not None):
+        raise ValueError("plan and call disagree on the presence of current K/V")
+    _check_table(table, plan, k_cache.shape[1])
+    scratch = DeviceScratch.get(dev)
+    ws = scratch.attn_workspace(plan.partial_bytes)
+    st = staging_struct(stage)
+    a = _lib.AttnArgs()
+    a.q, a.num_tokens, a.num_q_heads, a.q_stride_token = q.data_ptr(), n, hq, q.stride(0)
+    if k_new is not None:
+        a.k_new, a.v_new, a.kv_new_stride_token = k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0)
+    a.cache = cache_struct(k_cache, v_cache, head_dim)
+    a.block_table, a.block_table_stride = table.data_ptr(), table.stride(0)
+    a.query_start_loc, a.seq_lens, a.num_reqs = plan.qsl.data_ptr(), plan.seqs.data_ptr(), plan.seqs.numel()
+    if st is not None:
+        a.staging = C.pointer(st)
+    a.scale = float(scale)
+    a.items, a.num_items = plan.items.data_ptr(), plan.num_items
+    a.groups, a.num_groups = plan.groups.data_ptr(), plan.num_groups
+    a.workspace = ws.data_ptr()
+    a.out_rot, a.lse = out_rot.data_ptr(), lse.data_ptr()
+    lib = _lib.load()
+    _lib.check(lib.oscar_attn_decode_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_attn_decode_v1")
+    return out_rot, lse
+
+
+# ------------------------------------------------------------------------ prefill
+def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_cache=None,
+                      block_table_row=None, stage=None, out=None, lse=None):
+    """Causal GQA prefill of one request.
+
+    history == 0: original-domain fresh-only prefill, returns bf16 [n, Hq, D].
+    history > 0: rotated continuation over the packed history, returns fp32 out_rot
+    (and fills lse [n, Hq] when given).
+    """
+    _require_cuda(q, k, v)
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("OSCAR HIP prefill requires bf16 q/k/v")
+    n, hq, _ = q.shape
+    hk = k.shape[1]
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if out is None:
+        out = torch.empty(n, hq, head_dim, dtype=torch.bfloat16 if history == 0 else torch.float32,
+                          device=q.device)
+    a = _lib.PrefillArgs()
+    a.q, a.q_stride_token, a.k, a.v, a.kv_stride_token = q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0)
+    a.num_tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = n, hq, hk, head_dim
+    a.history = history
+    keep = []
+    if history > 0:
+        a.cache = cache_struct(k_cache, v_cache, head_dim)
+        row = block_table_row.to(device=q.device, dtype=torch.int32).contiguous()
+        if math.ceil(history / k_cache.shape[1]) > row.numel():
+            raise ValueError("Block table cannot cover the history")
+        keep.append(row)
+        a.block_table_row = row.data_ptr()
+        st = staging_struct(stage)
+        if st is not None:
+            keep.append(st)
+            a.staging = C.pointer(st)
+    a.scale = float(scale)
+    a.out, a.out_stride_token = out.data_ptr(), out.stride(0)
+    if lse is not None:
+        a.lse = lse.data_ptr()
+    lib = _lib.load()
+    _lib.check(lib.oscar_attn_prefill_v1(C.byref(a), C.c_void_p(_stream(q.device))), "oscar_attn_prefill_v1")
+    return out

@@ -1,0 +1,194 @@
+"""GPU parity of the INT2 write path (oscar_store_v1) against the CPU oracle.
+
+Bar: bit-exact cache bytes (meta + codes, untouched bytes preserved), owner tags
+and FP32 window values; read-path rotated copies equal the oracle's correctly
+rounded rotation rounded to the input dtype.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cases, fmt
+from oracle.store import Staging, clip, rotate, rotate_f32gemm, store_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(x, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
+
+
+def cache_dev(a):
+    return torch.from_numpy(a.copy()).view(torch.int8).cuda()
+
+
+def slot_mapping(n, capacity, seed, neg=0.05, dup=0.02):
+    """Shuffled distinct slots; `neg` of them -1, `dup` repeat an earlier position."""
+    g = cases.rng(seed)
+    slots = g.permutation(capacity)[:n].astype(np.int64)
+    slots[g.random(n) < neg] = -1
+    dups = np.nonzero(g.random(n) < dup)[0]
+    for i in dups:
+        if i > 0:
+            slots[i] = slots[g.integers(0, i)]
+    return slots
+
+
+def run_store(k, v, caches, slots, d, rk, rv, **kw):
+    from oscar_amd import ops
+
+    k8, v8 = caches
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    ops.store(to_dev(k), to_dev(v), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+              rk=None if rk is None else torch.from_numpy(rk).cuda(),
+              rv=None if rv is None else torch.from_numpy(rv).cuda(), **kw)
+    torch.cuda.synchronize()
+    return kc.view(torch.uint8).cpu().numpy(), vc.view(torch.uint8).cpu().numpy()
+
+
+@pytest.mark.parametrize("d,hk,rot", [(256, 1, "hadamard"), (256, 1, "identity"),
+                                      (128, 2, "qr"), (64, 4, "hadamard")])
+def test_store_bytes_bit_exact(cuda, d, hk, rot):
+    n, bs, nb = 1500, 128, 16
+    k = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 1)
+    v = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 2)
+    rk = {"hadamard": cases.hadamard_rotation(d, 3), "qr": cases.qr_rotation(d, 3),
+          "identity": None}[rot]
+    rv = {"hadamard": cases.hadamard_rotation(d, 4), "qr": cases.qr_rotation(d, 4),
+          "identity": None}[rot]
+    slots = slot_mapping(n, nb * bs, 5)
+    # pre-fill the caches with noise: untouched bytes must survive
+    g = cases.rng(6)
+    k8, v8 = (g.integers(0, 256, (nb, bs, hk, d), dtype=np.uint8) for _ in range(2))
+    got_k, got_v = run_store(k, v, (k8, v8), slots, d, rk, rv)
+    eye = np.eye(d, dtype=np.float32)
+    ek, ev = k8.copy(), v8.copy()
+    store_ref(rotate(k, rk if rk is not None else eye), rotate(v, rv if rv is not None else eye),
+              ek, ev, slots)
+    assert np.array_equal(got_k, ek), f"K cache bytes differ at {np.argwhere(got_k != ek)[:5]}"
+    assert np.array_equal(got_v, ev)
+
+
+def test_store_prerotated_reference_sgemm_bits(cuda):
+    """With R = identity the kernel quantizes the reference's own fp32 sgemm output."""
+    d, n, bs, nb = 256, 800, 128, 8
+    k = cases.kv_outliers(n, 1, d, 11)
+    v = cases.kv_outliers(n, 1, d, 12)
+    r = cases.hadamard_rotation(d, 13)
+    k_rot, v_rot = rotate_f32gemm(k, r), rotate_f32gemm(v, r)
+    slots = slot_mapping(n, nb * bs, 14)
+    k8, v8 = cases.empty_caches(nb, bs, 1, d)
+    from oscar_amd import ops
+
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    ops.store(to_dev(k_rot, torch.float32), to_dev(v_rot, torch.float32), kc, vc,
+              torch.from_numpy(slots).cuda(), head_dim=d)
+    torch.cuda.synchronize()
+    store_ref(k_rot, v_rot, k8, v8, slots)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
+
+
+def test_store_clip_bit_exact(cuda):
+    d, n, bs, nb = 256, 300, 128, 4
+    k = cases.kv_outliers(n, 1, d, 21)
+    v = cases.kv_outliers(n, 1, d, 22)
+    rk, rv = cases.hadamard_rotation(d, 23), cases.hadamard_rotation(d, 24)
+    slots = slot_mapping(n, nb * bs, 25)
+    k8, v8 = cases.empty_caches(nb, bs, 1, d)
+    got_k, got_v = run_store(k, v, (k8, v8), slots, d, rk, rv, k_clip=0.96, v_clip=0.92)
+    store_ref(clip(rotate(k, rk), 0.96), clip(rotate(v, rv), 0.92), k8, v8, slots)
+    assert np.array_equal(got_k, k8)
+    assert np.array_equal(got_v, v8)
+
+
+def test_store_window_tags_values_and_rotated_outputs(cuda):
+    """Forward write: codes + owner tags + FP32 window + rotated q/k/v for the read."""
+    from oscar_amd import ops
+    from oscar_amd._lib import STAGE_WRITE
+
+    d, hk, hq, bs, nb = 256, 1, 6, 128, 32
+    qsl, seqs = [0, 700, 705, 1200, 1200], [700, 2000, 496, 10]  # last request empty
+    n = qsl[-1]
+    k = cases.kv_outliers(n, hk, d, 31)
+    v = cases.kv_outliers(n, hk, d, 32)
+    q = cases.bf16_normal((n, hq, d), 33)
+    rk, rv = cases.hadamard_rotation(d, 34), cases.hadamard_rotation(d, 35)
+    slots = slot_mapping(n, nb * bs, 36)
+    st = Staging(bs, hk, d, 128, 256, 8192)
+    # earlier window contents that the collisions / rewrites must replace
+    st.owner[:] = np.arange(st.rows)[:, None]
+    st.stage_k[:] = 7.0
+    k8, v8 = cases.empty_caches(nb, bs, hk, d)
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
+    q_rot = torch.empty(n, hq, d, dtype=torch.bfloat16, device="cuda")
+    k_rot = torch.empty(n, hk, d, dtype=torch.bfloat16, device="cuda")
+    v_rot = torch.empty_like(k_rot)
+    ops.store(to_dev(k), to_dev(v), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+              rk=torch.from_numpy(rk).cuda(), rv=torch.from_numpy(rv).cuda(),
+              stage=(sk, sv, own), stage_mode=STAGE_WRITE,
+              qsl_dev=torch.tensor(qsl, dtype=torch.int32, device="cuda"),
+              seqs_dev=torch.tensor(seqs, dtype=torch.int32, device="cuda"), num_reqs=len(seqs),
+              recent_tokens=256, sink_tokens_eff=st.sink_eff, query=to_dev(q),
+              query_rot=q_rot, key_rot=k_rot, value_rot=v_rot)
+    torch.cuda.synchronize()
+    kr, vr = rotate(k, rk), rotate(v, rv)
+    store_ref(kr, vr, k8, v8, slots)
+    st.write(kr, vr, slots, qsl, seqs)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
+    assert np.array_equal(own.cpu().numpy(), st.owner)
+    assert np.array_equal(sk.cpu().numpy(), st.stage_k)
+    assert np.array_equal(sv.cpu().numpy(), st.stage_v)
+    assert np.array_equal(q_rot.float().cpu().numpy(), fmt.bf16_round(rotate(q, rk)))
+    assert np.array_equal(k_rot.float().cpu().numpy(), fmt.bf16_round(kr))
+    assert np.array_equal(v_rot.float().cpu().numpy(), fmt.bf16_round(vr))
+
+
+def test_standalone_update_invalidates_written_seats(cuda):
+    from oscar_amd import ops
+    from oscar_amd._lib import STAGE_INVALIDATE
+
+    d, bs, nb = 128, 128, 8
+    st = Staging(bs, 1, d, 64, 256, 1024)
+    st.owner[:] = 5
+    slots = np.array([3, -1, 130, 131, 3, 1000], np.int64)
+    k = cases.kv_outliers(len(slots), 1, d, 41)
+    k8, v8 = cases.empty_caches(nb, bs, 1, d)
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
+    ops.store(to_dev(k), to_dev(k), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+              stage=(sk, sv, own), stage_mode=STAGE_INVALIDATE)
+    torch.cuda.synchronize()
+    st.invalidate(slots)
+    assert np.array_equal(own.cpu().numpy(), st.owner)
+    store_ref(k, k, k8, v8, slots)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+
+
+def test_negative_slots_only_is_a_no_op(cuda):
+    d, bs, nb = 256, 128, 2
+    k = cases.kv_outliers(5, 1, d, 51)
+    g = cases.rng(52)
+    k8, v8 = (g.integers(0, 256, (nb, bs, 1, d), dtype=np.uint8) for _ in range(2))
+    got_k, got_v = run_store(k, k, (k8, v8), np.full(5, -1, np.int64), d, None, None)
+    assert np.array_equal(got_k, k8) and np.array_equal(got_v, v8)
+
+
+def test_legacy_bf16_geometry(cuda):
+    """bf16 caches: 512-byte slots, same packed placement in the first bytes."""
+    from oscar_amd import ops
+
+    d, n, bs, nb = 256, 200, 128, 4
+    k = cases.kv_outliers(n, 1, d, 61)
+    v = cases.kv_outliers(n, 1, d, 62)
+    slots = slot_mapping(n, nb * bs, 63, dup=0.0)
+    k8, v8 = cases.empty_caches(nb, bs, 1, d, legacy=True)
+    kc = torch.from_numpy(k8.copy()).view(torch.bfloat16).cuda()
+    vc = torch.from_numpy(v8.copy()).view(torch.bfloat16).cuda()
+    ops.store(to_dev(k), to_dev(v), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d)
+    torch.cuda.synchronize()
+    store_ref(k, v, k8, v8, slots)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
