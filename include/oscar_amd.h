@@ -106,10 +106,13 @@ typedef struct oscar_store_args_v1 {
   void* query_rot;              /* x @ R_k for the queries (may be NULL) */
   void* key_rot;                /* x @ R_k, unclipped (may be NULL) */
   void* value_rot;              /* x @ R_v, unclipped (may be NULL) */
-  /* scratch: last-writer claims, entries (epoch << 32 | token); zero-initialised once */
+  /* scratch: last-writer claims, entries (epoch << 24 | token), num_tokens < 2^24;
+   * zero-initialised once.
+   * The epoch is (*epoch_counter + 1); the call ends by incrementing the device
+   * counter, so replays of a captured graph always claim with a fresh epoch. */
   int64_t* slot_claims;         /* [num_blocks * block_size] */
   int64_t* seat_claims;         /* [rows * block_size] (stage mode 2) */
-  int64_t epoch;                /* strictly increasing per call on a device, in [1, 2^31) */
+  int64_t* epoch_counter;       /* device int64, zero-initialised once, shared per device */
   /* fp32 rotated K/V staging between the two launches, 16-byte aligned,
    * >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
   void* workspace;
@@ -174,6 +177,8 @@ typedef struct oscar_attn_args_v1 {
   void* workspace;              /* >= plan.partial_bytes */
   float* out_rot;               /* [n, Hq, D] fp32 rotated output (required) */
   float* lse;                   /* [n, Hq] natural-log LSE (required) */
+  int32_t phases;               /* 0 = split-K pass then merge; 1 = split-K pass only;
+                                   2 = merge only (the workspace holds the pass) */
 } oscar_attn_args_v1;
 
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);

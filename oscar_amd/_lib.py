@@ -40,7 +40,7 @@ class StoreArgs(C.Structure):
         ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
         ("recent_tokens", i32), ("sink_tokens_eff", i32),
         ("query_rot", vp), ("key_rot", vp), ("value_rot", vp),
-        ("slot_claims", vp), ("seat_claims", vp), ("epoch", i64),
+        ("slot_claims", vp), ("seat_claims", vp), ("epoch_counter", vp),
         ("workspace", vp), ("workspace_bytes", i64),
     ]
 
@@ -63,7 +63,7 @@ class AttnArgs(C.Structure):
         ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
         ("staging", C.POINTER(Staging)), ("scale", f32),
         ("items", vp), ("num_items", i32), ("groups", vp), ("num_groups", i32),
-        ("workspace", vp), ("out_rot", vp), ("lse", vp),
+        ("workspace", vp), ("out_rot", vp), ("lse", vp), ("phases", i32),
     ]
 
 

@@ -530,10 +530,14 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnParams P) {
 
 template <int D>
 int launch_decode(const AttnParams& p, hipStream_t s) {
-  hipLaunchKernelGGL(attn_main_kernel<D>, dim3(p.a.num_items), dim3(kThreads), 0, s, p);
-  OSCAR_CHECK_LAUNCH("attn_main_kernel");
-  hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, 32), dim3(D), 0, s, p);
-  OSCAR_CHECK_LAUNCH("attn_merge_kernel");
+  if (p.a.phases != 2) {
+    hipLaunchKernelGGL(attn_main_kernel<D>, dim3(p.a.num_items), dim3(kThreads), 0, s, p);
+    OSCAR_CHECK_LAUNCH("attn_main_kernel");
+  }
+  if (p.a.phases != 1) {
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, 32), dim3(D), 0, s, p);
+    OSCAR_CHECK_LAUNCH("attn_merge_kernel");
+  }
   return 0;
 }
 
@@ -640,6 +644,7 @@ extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream
     return fail(-22, "oscar_attn_decode_v1: missing pointer");
   if ((a.k_new == nullptr) != (a.v_new == nullptr))
     return fail(-22, "oscar_attn_decode_v1: both new K and V must be supplied together");
+  if (a.phases < 0 || a.phases > 2) return fail(-22, "oscar_attn_decode_v1: phases must be 0, 1 or 2");
   if (a.cache.num_kv_heads < 1 || a.num_q_heads % a.cache.num_kv_heads)
     return fail(-22, "oscar_attn_decode_v1: Hq must be a multiple of Hk");
   if ((a.cache.k_stride[2] & 15) || (a.cache.v_stride[2] & 15) || (a.cache.k_stride[1] & 15) ||

@@ -40,7 +40,8 @@ struct StoreParams {
 };
 
 __device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
-  return (long long)((epoch << 32) | (token & 0xffffffffll));
+  // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
+  return (long long)((epoch << 24) | (token & 0xffffffll));
 }
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, int64_t bs, int64_t rows) {
@@ -60,17 +61,18 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
 
   // last-writer claims and standalone invalidation, once per token
   if (kind == KIND_K && blockIdx.y == 0) {
+    const int64_t epoch = *a.epoch_counter + 1;
     for (int i = tid; i < TV; i += kThreads) {
       int64_t vec = vec0 + i;
       if (vec >= nvec || vec % heads != 0) continue;
       int64_t t = vec / heads;
       int64_t s = a.slot_mapping[t];
       if (s < 0 || s >= p.capacity) continue;
-      atomicMax((unsigned long long*)&a.slot_claims[s], (unsigned long long)claim_value(a.epoch, t));
+      atomicMax((unsigned long long*)&a.slot_claims[s], (unsigned long long)claim_value(epoch, t));
       if (a.stage_mode == OSCAR_STAGE_NONE) continue;
       int64_t seat = seat_of(s, a.cache.block_size, a.staging.rows);
       if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
-      else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(a.epoch, t));
+      else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
     }
   }
 
@@ -182,6 +184,7 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   const int64_t t = vec / hk, h = vec % hk;
   const int64_t slot = a.slot_mapping[t];
   if (slot < 0 || slot >= p.capacity) return;
+  const int64_t epoch = *a.epoch_counter + 1;
 
   __shared__ float rows[kThreads / 64][D];
   __shared__ float clip_slot[kThreads / 64];
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   const int64_t blk = slot / bs, off = slot % bs;
   if (a.stage_mode == OSCAR_STAGE_WRITE) {
     const int64_t seat = seat_of(slot, bs, a.staging.rows);
-    if ((long long)a.seat_claims[seat] == claim_value(a.epoch, t)) {
+    if ((long long)a.seat_claims[seat] == claim_value(epoch, t)) {
       int r = find_request(a.query_start_loc, a.num_reqs, a.num_tokens, t);
       int64_t seq = a.seq_lens[r], end = a.query_start_loc[r + 1];
       int64_t pos = seq - end + t;
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
       }
     }
   }
-  if ((long long)a.slot_claims[slot] != claim_value(a.epoch, t)) return;
+  if ((long long)a.slot_claims[slot] != claim_value(epoch, t)) return;
 
   const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
   float thr = INFINITY;
@@ -253,6 +256,13 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   }
 }
 
+// Advance the per-device claim epoch once both launches of a call have finished
+// (vector store: the counter is ordinary device memory).
+__global__ void store_epoch_kernel(int64_t* counter) {
+  const int64_t e = *counter + 1;
+  if (e < (1ll << 39) - 1) *counter = e;  // saturates (5e11 calls) instead of wrapping
+}
+
 template <int D>
 int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_t s) {
   const int kinds = q_vec ? 3 : 2;
@@ -269,6 +279,8 @@ int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_
   dim3 qgrid((unsigned)((kv_vec + 3) / 4), 2);
   hipLaunchKernelGGL(store_quant_kernel<D>, qgrid, block, 0, s, p);
   OSCAR_CHECK_LAUNCH("store_quant_kernel");
+  hipLaunchKernelGGL(store_epoch_kernel, dim3(1), dim3(1), 0, s, p.a.epoch_counter);
+  OSCAR_CHECK_LAUNCH("store_epoch_kernel");
   return 0;
 }
 
@@ -309,9 +321,9 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
     return fail(-22, "oscar_store_v1: key/value row stride smaller than heads*D");
   if ((a.rk && (((uintptr_t)a.rk) & 15)) || (a.rv && (((uintptr_t)a.rv) & 15)))
     return fail(-22, "oscar_store_v1: rotations must be 16-byte aligned");
-  if (a.slot_claims == nullptr || a.epoch < 1 || a.epoch >= (1ll << 31))
-    return fail(-22, "oscar_store_v1: slot_claims scratch and epoch in [1, 2^31) required");
-  if (a.num_tokens >= (1ll << 31)) return fail(-22, "oscar_store_v1: too many tokens");
+  if (a.slot_claims == nullptr || a.epoch_counter == nullptr)
+    return fail(-22, "oscar_store_v1: slot_claims scratch and the device epoch counter are required");
+  if (a.num_tokens >= (1ll << 24)) return fail(-22, "oscar_store_v1: more than 2^24 tokens per call");
   if (a.stage_mode != OSCAR_STAGE_NONE) {
     if (a.staging.owner == nullptr || a.staging.rows <= 0)
       return fail(-22, "oscar_store_v1: staging arena required for stage_mode %d", a.stage_mode);

@@ -68,7 +68,8 @@ class DeviceScratch:
 
     def __init__(self, device: torch.device):
         self.device = device
-        self.epoch = 0
+        # claim epoch lives on the device so that captured graphs replay with fresh epochs
+        self.epoch_counter = torch.zeros(1, dtype=torch.int64, device=device)
         self.slot_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.seat_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.store_ws = torch.empty(0, dtype=torch.uint8, device=device)
@@ -81,19 +82,15 @@ class DeviceScratch:
             cls._by_device[key] = cls(torch.device("cuda", key[1]))
         return cls._by_device[key]
 
-    def next_epoch(self) -> int:
-        self.epoch += 1
-        if self.epoch >= 2 ** 31 - 1:  # claims are epoch-tagged: restart from zeroed tables
-            self.slot_claims.zero_()
-            self.seat_claims.zero_()
-            self.epoch = 1
-        return self.epoch
-
     def claims(self, slots: int, seats: int):
-        if self.slot_claims.numel() < slots:
-            self.slot_claims = torch.zeros(slots, dtype=torch.int64, device=self.device)
-        if self.seat_claims.numel() < max(seats, 1):
-            self.seat_claims = torch.zeros(max(seats, 1), dtype=torch.int64, device=self.device)
+        """Claim tables; growing one restarts both tables and the epoch from zero."""
+        grow = self.slot_claims.numel() < slots or self.seat_claims.numel() < max(seats, 1)
+        if grow:
+            self.slot_claims = torch.zeros(max(slots, self.slot_claims.numel()), dtype=torch.int64,
+                                           device=self.device)
+            self.seat_claims = torch.zeros(max(seats, 1, self.seat_claims.numel()), dtype=torch.int64,
+                                           device=self.device)
+            self.epoch_counter.zero_()
         return self.slot_claims, self.seat_claims
 
     def store_workspace(self, nbytes: int) -> torch.Tensor:
@@ -167,7 +164,9 @@ def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=N
                 raise ValueError(f"{name} must be contiguous in the key dtype")
             setattr(a, name, t.data_ptr())
     a.slot_claims, a.seat_claims = slot_claims.data_ptr(), seat_claims.data_ptr()
-    a.epoch = scratch.next_epoch()
+    a.epoch_counter = scratch.epoch_counter.data_ptr()
+    if n >= 1 << 24:
+        raise ValueError("oscar store: at most 2^24 tokens per call")
     need = lib.oscar_store_workspace_bytes_v1(n, hk, head_dim)
     ws = scratch.store_workspace(need)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -255,7 +254,7 @@ def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None
 
 
 def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: DecodePlan, scale,
-                     stage=None, *, head_dim, out_rot=None, lse=None):
+                     stage=None, *, head_dim, out_rot=None, lse=None, phases=0):
     """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32)."""
     _require_cuda(q, k_cache, v_cache, block_table)
     if q.dtype != torch.bfloat16:
@@ -299,6 +298,7 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     a.groups, a.num_groups = plan.groups.data_ptr(), plan.num_groups
     a.workspace = ws.data_ptr()
     a.out_rot, a.lse = out_rot.data_ptr(), lse.data_ptr()
+    a.phases = int(phases)
     lib = _lib.load()
     _lib.check(lib.oscar_attn_decode_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_attn_decode_v1")
     return out_rot, lse
