@@ -108,11 +108,12 @@ typedef struct oscar_store_args_v1 {
   void* value_rot;              /* x @ R_v, unclipped (may be NULL) */
   /* scratch: last-writer claims, entries (epoch << 24 | token), num_tokens < 2^24;
    * zero-initialised once.
-   * The epoch is (*epoch_counter + 1); the call ends by incrementing the device
-   * counter, so replays of a captured graph always claim with a fresh epoch. */
+   * The call's epoch is epoch_counter[0] + 1: the first launch stores it in
+   * epoch_counter[1], the second copies it to epoch_counter[0], so replays of a
+   * captured graph always claim with a fresh epoch (no host round trip). */
   int64_t* slot_claims;         /* [num_blocks * block_size] */
   int64_t* seat_claims;         /* [rows * block_size] (stage mode 2) */
-  int64_t* epoch_counter;       /* device int64, zero-initialised once, shared per device */
+  int64_t* epoch_counter;       /* device int64[2], zero-initialised once, shared per device */
   /* fp32 rotated K/V staging between the two launches, 16-byte aligned,
    * >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
   void* workspace;

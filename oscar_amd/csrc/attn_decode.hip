@@ -12,10 +12,16 @@
 // Work decomposition: the host plan (oscar_attn_plan_v1) cuts every (request,
 // kv-head) key range into items of whole 32-token tiles, interleaved so that all
 // items of a group land on the same XCD.  One 256-thread workgroup (4 waves, one
-// per SIMD) per item; wave w takes tiles w, w+4, ...; the four wave partials are
-// merged in LDS and the item partial (normalised O, natural-log LSE) goes to the
-// workspace; attn_merge_kernel combines the items of each group (FP32 LSE merge,
-// slab_attention.py:341-356) into out_rot / lse.
+// per SIMD) per item; wave w takes tiles w, w+4, ...  Pages hold a multiple of 32
+// tokens, so a tile never straddles a page: its block id, seat row and in-page
+// offset are wave-uniform scalars.  The four wave partials are merged in LDS and
+// the item partial (normalised O in MFMA register order, natural-log LSE) goes to
+// the workspace with coalesced 16-byte stores; attn_merge_kernel combines the items
+// of each group (FP32 LSE merge, slab_attention.py:341-356) into out_rot / lse.
+//
+// Memory pipeline: each wave keeps kDepth tiles of packed data in flight (codes,
+// scales/zeros and owner tags of its next tiles are loaded into registers while the
+// current tile is computed), so HBM latency is paid once per wave, not per tile.
 //
 // Tile math (one wave, 32 tokens x 32 rows, S^T = K Q^T then O^T += V^T P^T):
 //  * QK (bf16 MFMA 32x32x16): the K operand holds exactly the reference's history
@@ -26,10 +32,14 @@
 //    to LDS in their natural layout and come back transposed with ds_read_b64_tr_b8
 //    (8 tokens x 1 byte = 4 codes per lane); one v_perm and one AND per fp16 pair
 //    give the subnormal c*2^(2k-24) for code bits 2k..2k+1, the B operand is
-//    P' = p*s_V (fp16) and sum_t p*z_V accumulates on the VALU (affine folded).
-//  * slow tiles (staged tokens, current chunk, causal boundary, ragged end) are
-//    deferred; the PV accumulators are then converted to value units and the
-//    tiles are evaluated from full values rounded as the reference does.
+//    P' = p*s_V (fp16, round to nearest) and sum_t p*z_V accumulates on the VALU.
+//  * slow tiles (staged tokens, current chunk, causal boundary, ragged end, or a
+//    score max far above the wave's reference max) are deferred until the fast
+//    tiles are done and the accumulators are in value units.  Their K/V values
+//    (rounded as the reference does) are built from the codes, the FP32 staged rows
+//    (loaded in batched rounds) and the current chunk (copied to LDS once per
+//    workgroup); V goes through LDS and is read transposed with ds_read_b64_tr_b16;
+//    P is split into bf16 hi + lo parts.
 #include "common.h"
 
 namespace oscar {
@@ -39,15 +49,28 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 32;
+constexpr int kDepth = 3;            // tiles of packed data in flight per wave
+constexpr int kMaxCur = 32;          // current-chunk tokens of a request (rows <= 32)
+constexpr int kMaxItemTokens = 8192; // keys per item (64 tiles per wave)
+constexpr int kMaxPages = kMaxItemTokens / kTile + 2;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazy = 8.f;         // max drift (log2 units) before O is rescaled
+typedef short __attribute__((ext_vector_type(4))) i16x4;
+typedef _Float16 __attribute__((ext_vector_type(2))) f16x2;
+typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
+typedef float __attribute__((ext_vector_type(2))) f32x2;
 
 template <int D>
 struct Cfg {
   static constexpr int KSTEPS = D / 16;  // QK contraction steps
-  static constexpr int KDW = D / 32;     // K code dwords per lane (its half of D)
+  static constexpr int NQ = D / 128;     // 16-byte code vectors per lane half (D/8 bytes)
+  static constexpr int NCH = D / 32;     // 16-element chunks per lane half
   static constexpr int NB = D / 4;       // code bytes per token
   static constexpr int MBLK = D / 32;    // PV output blocks (32 d each)
+  static constexpr int VROW = D + 8;     // bf16 per row of the slow-tile V buffer
+  static constexpr int CPR = 2;          // chunks per staged-row load round
+  static constexpr int NV = MBLK * 4 * 64;  // f32x4 of one item partial (register order)
 };
 
 struct AttnParams {
@@ -55,7 +78,7 @@ struct AttnParams {
   oscar_staging_v1 st;
   int has_stage;
   int group;     // Hq / Hk
-  float* part_o;   // [num_items][32][D]
+  float* part_o;   // [num_items][32 * D] in MFMA register order
   float* part_lse; // [num_items][32]
 };
 
@@ -69,92 +92,172 @@ __device__ __forceinline__ float swap_halves(float x) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-__device__ __forceinline__ float round_hist(float x) {
-  // reference history rounding: fp16 then bf16 (streaming_attention.py:124)
-  float h = __half2float(__float2half_rn(x));
-  return bf16_bits_to_f32(f32_to_bf16_bits(h));
+// reference history rounding, fp16 then bf16 (streaming_attention.py:124), of a
+// pair (a -> low half, b -> high half) with the packed RNE conversions
+// v_cvt_pk_f16_f32 / v_cvt_f32_f16 / v_cvt_pk_bf16_f32
+__device__ __forceinline__ unsigned hist_pair(float a, float b) {
+  const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
+  const f32x2 w = __builtin_convertvector(h, f32x2);
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(w, bf16x2));
+}
+// bf16 pair (RNE) of two floats
+__device__ __forceinline__ unsigned bf16_pair(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
-// d index of element e (0..7) of QK K-step j for lane half g
-template <int D>
-__device__ __forceinline__ int qk_d(int j, int g, int e) {
-  return g * (D / 2) + 16 * (j >> 1) + 4 * (j & 1) + (e >> 1) + 8 * (e & 1);
-}
-// PV output block mb, row m -> d, and the code position of the block
+// PV output block mb, MFMA row m -> d, and the code position of the block
 template <int D>
 __device__ __forceinline__ int pv_d(int mb, int m) {
   return (D == 256) ? 128 * (mb >> 2) + 4 * m + (mb & 3) : 4 * m + mb;
 }
 __device__ __forceinline__ int pv_pos(int mb) { return 2 * (mb & 3); }
+// slow-tile V buffer column of d-chunk c, element q + 4u (u = 0..3 consecutive)
+template <int D>
+__device__ __forceinline__ int vbuf_col(int g, int q, int c) {
+  return ((D == 256) ? 128 * g + 32 * q : 32 * q + 16 * g) + 4 * c;
+}
 
 // token (0..31) of MFMA K-element e for lane half g in PV K-step s
 __device__ __forceinline__ int pv_tok(int s, int g, int e) {
   return 16 * s + 4 * g + (e & 3) + 8 * (e >> 2);
 }
-// token of S^T output register r for lane half g
+// token of S^T output register r for lane half g (also the O^T row of register r)
 __device__ __forceinline__ int out_tok(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
+// bf16 pairs (element k, element k+8), k = 0..7, of 16 elements held as two
+// 8-element vectors
+__device__ __forceinline__ void interleave8(const u32x4& lo, const u32x4& hi, unsigned o[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    o[2 * w] = __builtin_amdgcn_perm(hi[w], lo[w], 0x05040100u);
+    o[2 * w + 1] = __builtin_amdgcn_perm(hi[w], lo[w], 0x07060302u);
+  }
+}
+
+// history value table of one token, bf16(fp16(c*scale + zero)) for c = 0..3
+__device__ __forceinline__ void value_table(unsigned scale_zero, unsigned& lo, unsigned& hi) {
+  const float s = f16_bits_to_f32(scale_zero & 0xffff), z = f16_bits_to_f32(scale_zero >> 16);
+  float v[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(__fmul_rn((float)c, s), z);  // mul, then add
+  lo = hist_pair(v[0], v[1]);
+  hi = hist_pair(v[2], v[3]);
+}
+
+// bf16 pairs (element k, element k+8) of the 16 codes of one code dword
+__device__ __forceinline__ void table_pairs(unsigned w, unsigned lo, unsigned hi, unsigned o[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const unsigned y = (w >> (2 * k)) & 0x00030003u;
+    o[k] = __builtin_amdgcn_perm(hi, lo, y * 0x202u + 0x01000100u);
+  }
+}
+
 template <int D>
-struct Item {
-  int req, kvh, kb, ke;
-  int a, nq, seq, hist, nrows;
+struct TileRegs {
+  u32x4 k[Cfg<D>::NQ];  // this lane's half of the K codes
+  u32x4 v[Cfg<D>::NQ];  // this lane's half of the V codes
+  u32x2 meta;           // K scale, K zero, V scale, V zero (fp16)
+  int64_t own;          // owner tag of the token's staging seat
+  int blk;              // physical block of the tile (0 off the history)
 };
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = lane & 31, g = lane >> 5;
+  // item record: request, kv head | query count << 16, tiles first + stride * j for
+  // j < count (32 keys each), partial slot, the request's first query token and length
   const int32_t* it = A.items + (int64_t)blockIdx.x * OSCAR_WORK_INTS;
-  Item<D> I;
-  I.req = it[0]; I.kvh = it[1]; I.kb = it[2]; I.ke = it[3];
-  I.a = A.query_start_loc[I.req];
-  I.nq = A.query_start_loc[I.req + 1] - I.a;
-  I.seq = A.seq_lens[I.req];
-  const bool has_new = A.k_new != nullptr;
-  I.hist = has_new ? I.seq - I.nq : I.seq;
+  const int req = it[0], kvh = it[1] & 0xffff, nq = it[1] >> 16;
+  const int first = it[2], stride = it[3], count = it[4], part = it[5];
+  const int qa = it[6], seq = it[7];
   const int G = P.group;
-  I.nrows = I.nq * G;
-  const int64_t bs = A.cache.block_size;
+  const bool has_new = A.k_new != nullptr;
+  const int hist = has_new ? seq - nq : seq;
+  const int nrows = nq * G;
+  const int bs = (int)A.cache.block_size;  // a multiple of 32
   const int64_t hk = A.cache.num_kv_heads;
+  if (part < 0 || part >= A.num_items) return;
+  // an item that breaks oscar_attn_plan_v1's rules poisons its partial (NaN LSE, so
+  // the merged rows are NaN) instead of reading out of bounds
+  if (req < 0 || req >= A.num_reqs || kvh >= hk || nq < 1 || nrows > 32 || hist < 0 ||
+      qa < 0 || qa + nq > A.num_tokens || first < 0 || stride < 1 || count < 0 ||
+      count > kMaxItemTokens / kTile ||
+      (count > 0 && (first + (int64_t)stride * (count - 1)) * kTile >= seq)) {
+    if (tid < 32) P.part_lse[(int64_t)part * 32 + tid] = NAN;
+    return;
+  }
+  const int lim0 = seq - nq + 1;                              // first key masked for a row
+  const int fast_end = hist < lim0 ? hist : lim0;             // fast tiles end at or before
+  auto tile_t0 = [&](int j) { return (first + stride * j) * kTile; };  // first key of item tile j
 
   // LDS
-  __shared__ int32_t s_table[256 + 2];                 // block ids of the item's pages
+  __shared__ int32_t s_blk[kMaxPages];                 // block ids of the item's pages
+  __shared__ int32_t s_seat[kMaxPages];                // their seat-row base (blk % rows) * bs
   __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][kTile * C::NB];
-  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][4][kTile];
+  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][kTile];
   __shared__ __attribute__((aligned(16))) float s_ml[kWaves][2][32];
-  // union: slow-tile V values (fp16) / cross-wave merge buffers
-  __shared__ __attribute__((aligned(16))) uint8_t s_big[2 * D * 33 * 4];
-  uint16_t* s_slowv = (uint16_t*)s_big + wave * (kTile * D);   // [32 tokens][D] fp16
+  __shared__ __attribute__((aligned(16))) uint16_t s_cur[2][kMaxCur][D];  // current K / V
+  __shared__ __attribute__((aligned(16))) u32x4 s_q[C::KSTEPS][64];        // Q^T operand
+  // union: slow-tile V values (bf16, permuted columns) / cross-wave merge buffers
+  constexpr int kMergeBytes = 2 * C::NV * 16, kSlowBytes = kWaves * kTile * C::VROW * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t s_big[kMergeBytes > kSlowBytes ? kMergeBytes : kSlowBytes];
+  uint16_t* s_slowv = (uint16_t*)s_big + wave * (kTile * C::VROW);
+  const unsigned st_rows = (unsigned)P.st.rows;
 
-  // page ids of the history pages this item reads; ids outside the cache are
-  // clamped (the host validates tables, this keeps a bad table from faulting)
-  const int page0 = I.kb / bs;
-  const int hist_end = I.ke < I.hist ? I.ke : I.hist;
-  const int npages = hist_end > I.kb ? (hist_end - 1) / bs - page0 + 1 : 0;
-  for (int i = tid; i < npages; i += kThreads) {
-    int32_t b = A.block_table[(int64_t)I.req * A.block_table_stride + page0 + i];
-    s_table[i] = (b < 0 || b >= A.cache.num_blocks) ? 0 : b;
+  // ---- prologue: page of every item tile, current chunk and queries, loaded together
+  bool any_cur_tile = false;
+  for (int j = tid; j < count; j += kThreads) {
+    const int t0 = tile_t0(j);
+    int32_t b = 0;
+    if (t0 < hist) {
+      b = A.block_table[(int64_t)req * A.block_table_stride + t0 / bs];
+      // ids outside the cache are clamped (the host validates tables; this keeps a
+      // bad table from faulting)
+      b = (b < 0 || b >= A.cache.num_blocks) ? 0 : b;
+    }
+    s_blk[j] = b;
+    s_seat[j] = P.has_stage ? (int)((unsigned)b % st_rows) * bs : 0;
   }
-
-  // ---- queries: lane (row n = m, half g) holds q[n][g*D/2 .. +D/2)
+  if (count > 0) any_cur_tile = has_new && tile_t0(count - 1) + kTile > hist;  // tiles ascend
+  if (any_cur_tile) {
+    constexpr int V8 = D / 8;
+    for (int e = tid; e < nq * V8; e += kThreads) {
+      const int t = e / V8, col = (e % V8) * 8;
+      const int64_t src = (int64_t)(qa + t) * A.kv_new_stride_token + (int64_t)kvh * D + col;
+      *(u32x4*)&s_cur[0][t][col] = *(const u32x4*)((const uint16_t*)A.k_new + src);
+      *(u32x4*)&s_cur[1][t][col] = *(const u32x4*)((const uint16_t*)A.v_new + src);
+    }
+  }
+  // queries: lane (row n = m, half g) holds q[n][g*D/2 .. +D/2) in the K-step order
+  // of the code dwords (elements k, k+8 of each 16-element chunk paired); the Q^T
+  // operand of K-step j for lane l lives at s_q[j][l] (shared by the waves)
   const int n = m;
-  const bool row_ok = n < I.nrows;
-  const int qtok = I.a + (row_ok ? n / G : 0);
-  const int qhead = I.kvh * G + (row_ok ? n % G : 0);
-  const uint16_t* qrow = (const uint16_t*)A.q + (int64_t)qtok * A.q_stride_token + (int64_t)qhead * D;
-  // Q^T operand (bf16, exact), element e of K-step j holds d = qk_d(j, g, e)
-  bf16x8 qb[C::KSTEPS];
+  const bool row_ok = n < nrows;
+  if (wave == 0) {
+    const int qtok = qa + (row_ok ? n / G : 0);
+    const int qhead = kvh * G + (row_ok ? n % G : 0);
+    const uint16_t* qrow = (const uint16_t*)A.q + (int64_t)qtok * A.q_stride_token + (int64_t)qhead * D + g * (D / 2);
 #pragma unroll
-  for (int j = 0; j < C::KSTEPS; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      qb[j][e] = __builtin_bit_cast(__bf16, (unsigned short)(row_ok ? qrow[qk_d<D>(j, g, e)] : 0));
+    for (int c = 0; c < C::NCH; ++c) {
+      u32x4 lo = *(const u32x4*)(qrow + 16 * c);
+      u32x4 hi = *(const u32x4*)(qrow + 16 * c + 8);
+      if (!row_ok) lo = hi = u32x4{0u, 0u, 0u, 0u};
+      unsigned o[8];
+      interleave8(lo, hi, o);
+      s_q[2 * c][lane] = u32x4{o[0], o[1], o[2], o[3]};
+      s_q[2 * c + 1][lane] = u32x4{o[4], o[5], o[6], o[7]};
+    }
+  }
   const float c_score = A.scale * kLog2e;  // scores in log2 units
   __syncthreads();
+  auto qop = [&](int j) { return __builtin_bit_cast(bf16x8, s_q[j][lane]); };
 
-  // ---- running state (per lane row n): max m_run (log2 units), partial sum l, z
+  // ---- running state (per lane row n): reference max m_run (log2 units), sum l, z
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f;
   f32x16 O[C::MBLK];
 #pragma unroll
@@ -162,132 +265,138 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[b][r] = 0.f;
 
-  const int ntiles = (I.ke - I.kb + kTile - 1) / kTile;
-  const int min_limit = I.seq - I.nq + 1;  // first key masked for some row
-  uint64_t slow_mask = 0;
-  const uint8_t* kbase = A.cache.k;
-  const uint8_t* vbase = A.cache.v;
+  // wave w takes item tiles j = w + 4 i, i < my
+  const int my = count > wave ? (count - 1 - wave) / kWaves + 1 : 0;
+  uint64_t slow_mask = 0, st_bits = 0;
+  const uint8_t* kbase = A.cache.k + (int64_t)kvh * A.cache.k_stride[2];
+  const uint8_t* vbase = A.cache.v + (int64_t)kvh * A.cache.v_stride[2];
+  const int64_t ks0 = A.cache.k_stride[0], ks1 = A.cache.k_stride[1];
+  const int64_t vs0 = A.cache.v_stride[0], vs1 = A.cache.v_stride[1];
   const int64_t* owner = P.st.owner;
-  const int64_t st_rows = P.st.rows;
 
-  // move O, l, z (relative to m_run) to a new running max; wave-uniform
+  // Lazy: the reference max of a row only moves when a tile's max exceeds it by
+  // more than kLazy (log2 units), so probabilities stay <= 2^kLazy and the O
+  // accumulators (kept in AGPRs by the MFMAs) are touched by the VALU only then.
   auto update_max = [&](float mx) {
-    const float m_new = fmaxf(m_run, mx);
-    if (__any(m_new > m_run)) {
-      const float f = (m_new == m_run) ? 1.f : (m_run == -INFINITY ? 0.f : exp2f(m_run - m_new));
+    const bool move = mx > m_run + kLazy;  // also true for the first finite max
+    if (__any(move)) {
+      const float m_new = move ? mx : m_run;
+      const float f = (!move || m_run == -INFINITY) ? (move ? 0.f : 1.f) : exp2f(m_run - m_new);
+      if (__any(move && m_run != -INFINITY)) {
 #pragma unroll
-      for (int b = 0; b < C::MBLK; ++b)
+        for (int b = 0; b < C::MBLK; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) O[b][r] *= f;
+          for (int r = 0; r < 16; ++r) O[b][r] *= f;
+      }
       l_run *= f;
       z_run *= f;
+      m_run = m_new;
     }
-    m_run = m_new;
   };
 
-  for (int tile = wave, ti = 0; tile < ntiles; tile += kWaves, ++ti) {
-    const int t0 = I.kb + tile * kTile;
-    const int p = t0 + m;                   // this lane's token (lanes m, m+32 share it)
-    const bool in_range = p < I.ke;
-    const bool is_hist = in_range && p < I.hist;
-    int64_t blk = 0, off = 0;
-    bool staged = false;
-    if (is_hist) {
-      blk = s_table[p / bs - page0];
-      off = p % bs;
-      if (P.has_stage) {
-        int64_t o = owner[((blk % st_rows) * bs + off)];
-        staged = (o == blk);
-      }
+  // page of item tile j, first key t0 (wave-uniform): block, in-page offset of t0
+  // and seat-row base.  Tiles past the history, and the placeholder tile j >= count
+  // a wave without tiles loads in the pipeline prologue (its s_blk entry is never
+  // written), read block 0 at offsets 0..31 (< block_size).
+  auto tile_page = [&](int j, int t0, int& blk, int& off0, int& seat0) {
+    blk = 0;
+    off0 = 0;
+    seat0 = 0;
+    if (j < count && t0 < hist) {
+      off0 = t0 % bs;
+      blk = __builtin_amdgcn_readfirstlane(s_blk[j]);
+      seat0 = __builtin_amdgcn_readfirstlane(s_seat[j]);
     }
-    const bool tile_fast = (t0 + kTile <= I.ke) && (t0 + kTile <= I.hist) &&
-                           (t0 + kTile <= min_limit) && !__any(staged);
-    if (!tile_fast) {
-      slow_mask |= 1ull << ti;
-      continue;
-    }
-    // ---- loads: K codes (this lane's half), meta, V codes (this lane's half)
-    const uint8_t* kslot = kbase + blk * A.cache.k_stride[0] + off * A.cache.k_stride[1] + I.kvh * A.cache.k_stride[2];
-    const uint8_t* vslot = vbase + blk * A.cache.v_stride[0] + off * A.cache.v_stride[1] + I.kvh * A.cache.v_stride[2];
-    unsigned kc[C::KDW], vc[C::KDW];
+  };
+
+  auto load_tile = [&](int ti, TileRegs<D>& r) {
+    const int j = wave + kWaves * ti;
+    const int t0 = tile_t0(j);
+    int off0, seat0;
+    tile_page(j, t0, r.blk, off0, seat0);
+    const int off = off0 + m;
+    const uint8_t* ks = kbase + (int64_t)r.blk * ks0 + (int64_t)off * ks1;
+    const uint8_t* vs = vbase + (int64_t)r.blk * vs0 + (int64_t)off * vs1;
 #pragma unroll
-    for (int i = 0; i < C::KDW; i += 4) {
-      u32x4 x = *(const u32x4*)(kslot + 32 + g * (D / 8) + 4 * i);
-      kc[i] = x[0]; kc[i + 1] = x[1]; kc[i + 2] = x[2]; kc[i + 3] = x[3];
-      u32x4 y = *(const u32x4*)(vslot + g * (D / 8) + 4 * i);
-      vc[i] = y[0]; vc[i + 1] = y[1]; vc[i + 2] = y[2]; vc[i + 3] = y[3];
+    for (int i = 0; i < C::NQ; ++i) {
+      r.k[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
+      r.v[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
     }
-    const u32x2 meta = *(const u32x2*)kslot;
-    // V codes to LDS, natural layout [token][NB]
+    r.meta = *(const u32x2*)ks;
+    // without a staging arena the tag is read from the item record (never matches)
+    const int64_t* op = P.has_stage ? owner + seat0 + off : (const int64_t*)it;
+    r.own = *op;
+  };
+
+  // ---------------------------------------------------------------- fast tiles
+  // Straight-line in the O accumulators (no branch around an MFMA, no VALU on O):
+  // a tile that turns out slow (staged token, mask, ragged end, or a max more than
+  // kLazy above the wave's reference max) or that only pads the pipeline runs with
+  // P = 0 and, if real, is queued for the slow pass.
+  auto fast_tile = [&](int ti, const TileRegs<D>& r) {
+    const int t0 = tile_t0(wave + kWaves * ti);
+    const int p = t0 + m;
+    const bool real = ti < my;
+    const bool staged = P.has_stage && real && p < hist && r.own == (int64_t)r.blk;
+    st_bits |= (uint64_t)staged << (ti & 63);  // ti < 64 whenever staged
+    bool slow = real && !((t0 + kTile <= fast_end) && !__any(staged));
+    // V codes to LDS, natural layout [token][NB]; per-token V constants
 #pragma unroll
-    for (int i = 0; i < C::KDW; i += 4) {
-      u32x4 y = {vc[i], vc[i + 1], vc[i + 2], vc[i + 3]};
-      *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 4 * i] = y;
-    }
-    // per-token V constants for the probability side
-    if (g == 0) {
-      s_cst[wave][2][m] = f16_bits_to_f32(meta[1] & 0xffff);
-      s_cst[wave][3][m] = f16_bits_to_f32(meta[1] >> 16);
-    }
-    // ---- K operand: the 4 possible history values of this token, rounded exactly as
-    // the reference (bf16(fp16(code*scale + zero))), form a byte table that v_perm_b32
-    // indexes with 2*code, 2*code+1 per bf16 element.
+    for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
+    s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
+    s_cst[wave][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
+    // S^T = K Q^T with the exact history values looked up per code pair
     unsigned lut_lo, lut_hi;
-    {
-      const float sk = f16_bits_to_f32(meta[0] & 0xffff), zk = f16_bits_to_f32(meta[0] >> 16);
-      unsigned short v[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = f32_to_bf16_bits(round_hist(__fadd_rn(__fmul_rn((float)c, sk), zk)));
-      lut_lo = (unsigned)v[0] | ((unsigned)v[1] << 16);
-      lut_hi = (unsigned)v[2] | ((unsigned)v[3] << 16);
-    }
-    // ---- S^T = K Q^T; element pair k of code dword w holds codes k and k+8
+    value_table(r.meta[0], lut_lo, lut_hi);
     f32x16 S = {};
 #pragma unroll
-    for (int i = 0; i < C::KDW; ++i) {
-      const unsigned w = kc[i];
+    for (int i = 0; i < C::NCH; ++i) {
       unsigned o[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const unsigned y = (w >> (2 * k)) & 0x00030003u;
-        o[k] = __builtin_amdgcn_perm(lut_hi, lut_lo, y * 0x202u + 0x01000100u);
-      }
-      const u32x4 a0 = {o[0], o[1], o[2], o[3]};
-      const u32x4 a1 = {o[4], o[5], o[6], o[7]};
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0), qb[2 * i], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), qb[2 * i + 1], S, 0, 0, 0);
+      table_pairs(r.k[i >> 2][i & 3], lut_lo, lut_hi, o);
+      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]}),
+                                                  qop(2 * i), S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]}),
+                                                  qop(2 * i + 1), S, 0, 0, 0);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_lds();
     __builtin_amdgcn_wave_barrier();
     float xs[16];
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      xs[r] = S[r] * c_score;
-      mx = fmaxf(mx, xs[r]);
+    for (int r2 = 0; r2 < 16; ++r2) {
+      xs[r2] = S[r2] * c_score;
+      mx = fmaxf(mx, xs[r2]);
     }
     mx = fmaxf(mx, swap_halves(mx));
-    update_max(mx);
+    // the first used tile sets the reference max (O, l, z are still zero); after
+    // that a tile whose max drifts more than kLazy above it goes to the slow pass
+    const bool first = m_run == -INFINITY;  // uniform: fast-tile scores are finite
+    slow = slow || (real && !first && __any(mx > m_run + kLazy));
+    if (slow) slow_mask |= 1ull << ti;
+    const bool use = real && !slow;
+    if (use && first) m_run = mx;
     // probabilities; P' = p * s_V feeds the MFMA, sum p*z_V the VALU
     u32x4 pb[2];
     float lsum = 0.f, zsum = 0.f;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const f32x4 sv = *(const f32x4*)&s_cst[wave][2][8 * q4 + 4 * g];
-      const f32x4 zv = *(const f32x4*)&s_cst[wave][3][8 * q4 + 4 * g];
+      const f32x4 sv = *(const f32x4*)&s_cst[wave][0][8 * q4 + 4 * g];
+      const f32x4 zv = *(const f32x4*)&s_cst[wave][1][8 * q4 + 4 * g];
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
         const int r0 = 4 * q4 + i;
-        float p0 = exp2f(xs[r0] - m_run), p1 = exp2f(xs[r0 + 1] - m_run);
+        // p <= 2^kLazy: no range reduction needed for v_exp_f32
+        const float p0 = use ? __builtin_amdgcn_exp2f(xs[r0] - m_run) : 0.f;
+        const float p1 = use ? __builtin_amdgcn_exp2f(xs[r0 + 1] - m_run) : 0.f;
         lsum += p0 + p1;
         zsum = fmaf(p0, zv[i], fmaf(p1, zv[i + 1], zsum));
-        auto h = __builtin_amdgcn_cvt_pkrtz(p0 * sv[i], p1 * sv[i + 1]);
+        const f16x2 h = {(_Float16)(p0 * sv[i]), (_Float16)(p1 * sv[i + 1])};
         pb[r0 >> 3][(r0 & 7) >> 1] = __builtin_bit_cast(unsigned, h);
       }
     }
     l_run += lsum;
     z_run += zsum;
-    // ---- O^T += V^T P'^T, V^T from LDS via transpose reads
+    // O^T += V^T P'^T, V^T from LDS via transpose reads
     const int G16 = lane >> 4, i16 = lane & 15;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -299,150 +408,198 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
         const uint8_t* addr = &s_vcode[wave][tok * C::NB + chunk * 16 + half8];
         i32x2 tr = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             (__attribute__((address_space(3))) i32x2*)(addr));
-        unsigned x0 = (unsigned)tr[0], x1 = (unsigned)tr[1];
-        unsigned t0 = __builtin_amdgcn_perm(0u, x0, 0x0C010C00u);
-        unsigned t1 = __builtin_amdgcn_perm(0u, x0, 0x0C030C02u);
-        unsigned t2 = __builtin_amdgcn_perm(0u, x1, 0x0C010C00u);
-        unsigned t3 = __builtin_amdgcn_perm(0u, x1, 0x0C030C02u);
+        const unsigned x0 = (unsigned)tr[0], x1 = (unsigned)tr[1];
+        const unsigned t0w = __builtin_amdgcn_perm(0u, x0, 0x0C010C00u);
+        const unsigned t1w = __builtin_amdgcn_perm(0u, x0, 0x0C030C02u);
+        const unsigned t2w = __builtin_amdgcn_perm(0u, x1, 0x0C010C00u);
+        const unsigned t3w = __builtin_amdgcn_perm(0u, x1, 0x0C030C02u);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          unsigned msk = 0x00030003u << (2 * k);
-          u32x4 av = {t0 & msk, t1 & msk, t2 & msk, t3 & msk};
+          const unsigned msk = 0x00030003u << (2 * k);
+          const u32x4 av = {t0w & msk, t1w & msk, t2w & msk, t3w & msk};
           const int mb = (D == 256) ? 4 * cp + k : k;
           O[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(av), __builtin_bit_cast(f16x8, pb[s]),
                                                          O[mb], 0, 0, 0);
         }
       }
     }
-  }
+  };
 
-  // ---- convert fast-tile accumulators to uniform units: O *= 2^(24-2k), += z
-  const float z_row = z_run + swap_halves(z_run);
+  // software pipeline: slot d holds tile base+d; after it is computed the slot is
+  // refilled with tile base+d+kDepth (clamped to the last tile: the surplus loads
+  // at the end re-read a tile already in cache and are never used)
+  {
+    TileRegs<D> R[kDepth];
+    const int last = my > 0 ? my - 1 : 0;
 #pragma unroll
-  for (int b = 0; b < C::MBLK; ++b) {
-    const float f = ldexpf(1.f, 24 - pv_pos(b));
+    for (int d = 0; d < kDepth; ++d) load_tile(d < last ? d : last, R[d]);
+    for (int base = 0; base < my; base += kDepth) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) O[b][r] = fmaf(O[b][r], f, z_row);
-  }
-  // z has been applied with the weight of both halves; keep l per lane (summed later)
-
-  // ---- slow tiles: full values with the reference rounding
-  if (slow_mask) {
-    for (int ti = 0; ti < 64; ++ti) {
-      if (!((slow_mask >> ti) & 1)) continue;
-      const int tile = wave + ti * kWaves;
-      const int t0 = I.kb + tile * kTile;
-      const int p = t0 + m;
-      const bool in_range = p < I.ke && p < I.seq;
-      const bool is_hist = in_range && p < I.hist;
-      const bool is_cur = in_range && !is_hist;
-      int64_t blk = 0, off = 0;
-      bool staged = false;
-      if (is_hist) {
-        blk = s_table[p / bs - page0];
-        off = p % bs;
-        if (P.has_stage) staged = owner[(blk % st_rows) * bs + off] == blk;
+      for (int d = 0; d < kDepth; ++d) {
+        const int ti = base + d;
+        fast_tile(ti, R[d]);
+        const int nx = ti + kDepth;
+        load_tile(nx < last ? nx : last, R[d]);
       }
-      // this lane's token values for its half of D (K) and all of D split by halves (V)
-      const uint8_t* kslot = kbase + blk * A.cache.k_stride[0] + off * A.cache.k_stride[1] + I.kvh * A.cache.k_stride[2];
-      const uint8_t* vslot = vbase + blk * A.cache.v_stride[0] + off * A.cache.v_stride[1] + I.kvh * A.cache.v_stride[2];
-      float sk = 0.f, zk = 0.f, svv = 0.f, zvv = 0.f;
-      if (is_hist && !staged) {
-        u32x2 meta = *(const u32x2*)kslot;
-        sk = f16_bits_to_f32(meta[0] & 0xffff); zk = f16_bits_to_f32(meta[0] >> 16);
-        svv = f16_bits_to_f32(meta[1] & 0xffff); zvv = f16_bits_to_f32(meta[1] >> 16);
-      }
-      const int64_t seat = (blk % (st_rows > 0 ? st_rows : 1)) * bs + off;
-      auto kval = [&](int d) -> float {
-        if (!in_range) return 0.f;
-        if (is_cur) {
-          const uint16_t* kn = (const uint16_t*)A.k_new +
-                               (int64_t)(I.a + p - I.hist) * A.kv_new_stride_token + I.kvh * D;
-          return bf16_bits_to_f32(kn[d]);
-        }
-        if (staged) return round_hist(P.st.stage_k[(seat * hk + I.kvh) * D + d]);
-        unsigned c = (kslot[32 + d / 4] >> (2 * (d & 3))) & 3u;
-        return round_hist(__fadd_rn(__fmul_rn((float)c, sk), zk));  // mul, then add
-      };
-      auto vval = [&](int d) -> float {
-        if (!in_range) return 0.f;
-        if (is_cur) {
-          const uint16_t* vn = (const uint16_t*)A.v_new +
-                               (int64_t)(I.a + p - I.hist) * A.kv_new_stride_token + I.kvh * D;
-          return bf16_bits_to_f32(vn[d]);
-        }
-        if (staged) return round_hist(P.st.stage_v[(seat * hk + I.kvh) * D + d]);
-        unsigned c = (vslot[d / 4] >> (2 * (d & 3))) & 3u;
-        return round_hist(__fadd_rn(__fmul_rn((float)c, svv), zvv));
-      };
-      f32x16 S = {};
-#pragma unroll
-      for (int j = 0; j < C::KSTEPS; ++j) {
-        bf16x8 ka;  // full values, already on the bf16 grid
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          ka[e] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(kval(qk_d<D>(j, g, e))));
-        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[j], S, 0, 0, 0);
-      }
-      // V values of this token to LDS (fp16), this lane's half of D
-      for (int d = g * (D / 2); d < (g + 1) * (D / 2); ++d)
-        s_slowv[m * D + d] = __half_as_ushort(__float2half_rn(vval(d)));
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
-      // masked scores
-      float xs[16];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = t0 + out_tok(r, g);
-        const int limit = I.seq - I.nq + (row_ok ? n / G : 0) + 1;
-        const bool vis = row_ok && tp < I.ke && tp < I.seq && tp < limit;
-        xs[r] = vis ? S[r] * c_score : -INFINITY;
-        mx = fmaxf(mx, xs[r]);
-      }
-      mx = fmaxf(mx, swap_halves(mx));
-      update_max(mx);
-      u32x4 pb[2];
-      float lsum = 0.f;
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          int r0 = 8 * s + 2 * q, r1 = r0 + 1;
-          float p0 = (xs[r0] == -INFINITY) ? 0.f : exp2f(xs[r0] - m_run);
-          float p1 = (xs[r1] == -INFINITY) ? 0.f : exp2f(xs[r1] - m_run);
-          lsum += p0 + p1;
-          auto h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
-          pb[s][q] = __builtin_bit_cast(unsigned, h);
-        }
-      l_run += lsum;
-#pragma unroll
-      for (int b = 0; b < C::MBLK; ++b) {
-        const int d = pv_d<D>(b, m);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          f16x8 va;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            va[e] = __builtin_bit_cast(_Float16, s_slowv[pv_tok(s, g, e) * D + d]);
-          O[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, __builtin_bit_cast(f16x8, pb[s]), O[b], 0, 0, 0);
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
     }
   }
 
-  // ---- per-wave row totals
+  // ---- fast-tile accumulators to value units: O = O * 2^(24-2k) + z
+  {
+    const float z_row = z_run + swap_halves(z_run);
+#pragma unroll
+    for (int b = 0; b < C::MBLK; ++b) {
+      const float f = ldexpf(1.f, 24 - pv_pos(b));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[b][r] = fmaf(O[b][r], f, z_row);
+    }
+    z_run = 0.f;
+  }
+
+  // ---------------------------------------------------------------- slow tiles
+  while (slow_mask) {
+    const int ti = __builtin_ctzll(slow_mask);
+    slow_mask &= slow_mask - 1;
+    const int j = wave + kWaves * ti;
+    const int t0 = tile_t0(j);
+    const int p = t0 + m;
+    const bool staged = (st_bits >> ti) & 1;
+    const bool hist_tok = p < hist;
+    const bool cur_tok = has_new && p < seq && p >= hist;
+    const bool any_st = __any(staged), any_cur = __any(cur_tok);
+    int blk, off0, seat0;
+    tile_page(j, t0, blk, off0, seat0);
+    const int off = off0 + m;
+    const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)off * ks1;
+    const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)off * vs1;
+    u32x4 kc[C::NQ], vc[C::NQ];
+#pragma unroll
+    for (int i = 0; i < C::NQ; ++i) {
+      kc[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
+      vc[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
+    }
+    const u32x2 meta = *(const u32x2*)ks;
+    // FP32 staged rows of this lane's token (seat row 0 for lanes without one)
+    const int64_t seat = staged ? (int64_t)seat0 + off : 0;
+    const float* sk_row = P.st.stage_k + (seat * hk + kvh) * D + g * (D / 2);
+    const float* sv_row = P.st.stage_v + (seat * hk + kvh) * D + g * (D / 2);
+    const int ci = cur_tok ? p - hist : 0;
+    unsigned klo, khi, vlo, vhi;
+    value_table(meta[0], klo, khi);
+    value_table(meta[1], vlo, vhi);
+
+    f32x16 S = {};
+#pragma unroll
+    for (int c0 = 0; c0 < C::NCH; c0 += C::CPR) {
+      f32x4 fk[C::CPR][4], fv[C::CPR][4];
+      if (any_st) {
+#pragma unroll
+        for (int cc = 0; cc < C::CPR; ++cc)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            fk[cc][u] = *(const f32x4*)(sk_row + 16 * (c0 + cc) + 4 * u);
+            fv[cc][u] = *(const f32x4*)(sv_row + 16 * (c0 + cc) + 4 * u);
+          }
+      }
+#pragma unroll
+      for (int cc = 0; cc < C::CPR; ++cc) {
+        const int c = c0 + cc;
+        unsigned ok[8], ov[8];
+        table_pairs(kc[c >> 2][c & 3], klo, khi, ok);
+        table_pairs(vc[c >> 2][c & 3], vlo, vhi, ov);
+        if (any_st && staged) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            ok[k] = hist_pair(fk[cc][k >> 2][k & 3], fk[cc][2 + (k >> 2)][k & 3]);
+            ov[k] = hist_pair(fv[cc][k >> 2][k & 3], fv[cc][2 + (k >> 2)][k & 3]);
+          }
+        }
+        if (any_cur && cur_tok) {
+          const uint16_t* kr = &s_cur[0][ci][g * (D / 2) + 16 * c];
+          const uint16_t* vr = &s_cur[1][ci][g * (D / 2) + 16 * c];
+          interleave8(*(const u32x4*)kr, *(const u32x4*)(kr + 8), ok);
+          interleave8(*(const u32x4*)vr, *(const u32x4*)(vr + 8), ov);
+        }
+        if (!hist_tok && !cur_tok) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ok[k] = ov[k] = 0u;
+        }
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{ok[0], ok[1], ok[2], ok[3]}),
+                                                    qop(2 * c), S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{ok[4], ok[5], ok[6], ok[7]}),
+                                                    qop(2 * c + 1), S, 0, 0, 0);
+        // V values of this token to the buffer, columns permuted so that MFMA row i
+        // of output block b reads column 32 b + i (d = pv_d(b, i))
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x2 w = {__builtin_amdgcn_perm(ov[q + 4], ov[q], 0x05040100u),
+                           __builtin_amdgcn_perm(ov[q + 4], ov[q], 0x07060302u)};
+          *(u32x2*)&s_slowv[m * C::VROW + vbuf_col<D>(g, q, c)] = w;
+        }
+      }
+    }
+    wait_lds();
+    __builtin_amdgcn_wave_barrier();
+    // masked scores
+    float xs[16];
+    float mx = -INFINITY;
+    const int limit = seq - nq + (row_ok ? n / G : 0) + 1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int tp = t0 + out_tok(r, g);
+      const bool vis = row_ok && tp < limit;  // limit <= seq
+      xs[r] = vis ? S[r] * c_score : -INFINITY;
+      mx = fmaxf(mx, xs[r]);
+    }
+    mx = fmaxf(mx, swap_halves(mx));
+    update_max(mx);
+    // P = hi + lo, both bf16
+    u32x4 ph[2], pl[2];
+    float lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const float p0 = (xs[r] == -INFINITY) ? 0.f : exp2f(xs[r] - m_run);
+      const float p1 = (xs[r + 1] == -INFINITY) ? 0.f : exp2f(xs[r + 1] - m_run);
+      lsum += p0 + p1;
+      const unsigned hb = bf16_pair(p0, p1);
+      ph[r >> 3][(r & 7) >> 1] = hb;
+      pl[r >> 3][(r & 7) >> 1] = bf16_pair(p0 - __uint_as_float(hb << 16), p1 - __uint_as_float(hb & 0xffff0000u));
+    }
+    l_run += lsum;
+    const int G16 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int b = 0; b < C::MBLK; ++b) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        bf16x8 va;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
+          const uint16_t* addr = &s_slowv[key * C::VROW + 32 * b + 16 * (G16 & 1) + 4 * (i16 & 3)];
+          auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) va[4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
+        }
+        O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, ph[s]), O[b], 0, 0, 0);
+        O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, pl[s]), O[b], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- cross-wave merge: common max M and total L per row, then the four wave
+  // partials are summed in LDS in MFMA register order (16-byte accesses)
   const float l_row = l_run + swap_halves(l_run);
-  // ---- cross-wave merge in LDS (deterministic tree: w0+w2, w1+w3, then w0+w1)
-  __syncthreads();
+  __syncthreads();  // every wave is past its slow tiles (s_big is free)
   if (g == 0) { s_ml[wave][0][m] = m_run; s_ml[wave][1][m] = l_row; }
   __syncthreads();
   float M = -INFINITY;
+#pragma unroll
   for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0][n]);
   float L = 0.f;
+#pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    float mw = s_ml[w][0][n];
+    const float mw = s_ml[w][0][n];
     if (mw != -INFINITY) L += s_ml[w][1][n] * exp2f(mw - M);
   }
   const float fw = (m_run == -INFINITY || !(L > 0.f)) ? 0.f : exp2f(m_run - M) / L;
@@ -450,37 +607,33 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   for (int b = 0; b < C::MBLK; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[b][r] *= fw;
-  float* buf = (float*)s_big;  // [2][D][33]
+  f32x4* buf = (f32x4*)s_big;  // [2][MBLK][4][64] f32x4
   auto put = [&](int slot) {
 #pragma unroll
     for (int b = 0; b < C::MBLK; ++b)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) buf[(slot * D + pv_d<D>(b, out_tok(r, g))) * 33 + n] = O[b][r];
-  };
-  auto add = [&](int slot) {
-#pragma unroll
-    for (int b = 0; b < C::MBLK; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) O[b][r] += buf[(slot * D + pv_d<D>(b, out_tok(r, g))) * 33 + n];
+      for (int q = 0; q < 4; ++q)
+        buf[((slot * C::MBLK + b) * 4 + q) * 64 + lane] =
+            f32x4{O[b][4 * q], O[b][4 * q + 1], O[b][4 * q + 2], O[b][4 * q + 3]};
   };
   if (wave >= 2) put(wave - 2);
   __syncthreads();
-  if (wave < 2) add(wave);
-  __syncthreads();
-  if (wave == 1) put(0);
-  __syncthreads();
-  if (wave == 0) {
-    add(0);
-    put(0);
+  if (wave < 2) {
+#pragma unroll
+    for (int b = 0; b < C::MBLK; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = buf[((wave * C::MBLK + b) * 4 + q) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) O[b][4 * q + j] += v[j];
+      }
+    put(wave);
   }
   __syncthreads();
-  // item partial: normalised O [32][D] and lse [32]
-  const int part = it[4];
-  float* po = P.part_o + (int64_t)part * 32 * D;
-  for (int e = tid; e < 32 * D; e += kThreads) {
-    int nn = e / D, dd = e % D;
-    po[e] = buf[dd * 33 + nn];
-  }
+  // item partial: slot 0 + slot 1, register order, rows < nrows; lse [32]
+  f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
+  for (int e = tid; e < C::NV; e += kThreads)
+    if ((e & 31) < nrows) po[e] = buf[e] + buf[C::NV + e];
   if (tid < 32) {
     float lse = (L > 0.f && M != -INFINITY) ? (M + log2f(L)) * kLn2 : -INFINITY;
     if (M != M || L != L) lse = NAN;
@@ -488,44 +641,99 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   }
 }
 
-// One workgroup of D threads per (group, row): FP32 LSE merge of the group's items
-// (slab_attention.py:341-356 applied in sequence; empty parts contribute nothing).
+// FP32 LSE merge of a group's items (slab_attention.py:341-356 applied in
+// sequence; empty parts contribute nothing).  Workgroup (group, chunk): 256 threads,
+// one 16-byte partial vector (register order: block b, quad q, lane) each; the
+// per-row max and sum over the items are reduced in LDS first.
 template <int D>
-__global__ __launch_bounds__(D) void attn_merge_kernel(AttnParams P) {
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams P) {
+  using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
   const int32_t* grp = A.groups + (int64_t)blockIdx.x * 4;
-  const int req = grp[0], kvh = grp[1], i0 = grp[2], i1 = grp[2] + grp[3];
-  const int row = blockIdx.y;
+  const int req = grp[0], kvh = grp[1], i0 = grp[2], ni = grp[3];
   const int a = A.query_start_loc[req];
   const int nq = A.query_start_loc[req + 1] - a;
   const int G = P.group;
-  if (row >= nq * G) return;
-  const int tok = a + row / G, head = kvh * G + row % G;
-  const int d = threadIdx.x;
-  float M = -INFINITY;
-  bool nan = false;
-  for (int i = i0; i < i1; ++i) {
-    float l = P.part_lse[(int64_t)i * 32 + row];
-    nan |= (l != l);
-    M = fmaxf(M, l);
-  }
-  float out = 0.f, lse = -INFINITY;
-  if (nan) {
-    out = NAN; lse = NAN;
-  } else if (M != -INFINITY) {
-    float acc = 0.f, L = 0.f;
-    for (int i = i0; i < i1; ++i) {
-      float l = P.part_lse[(int64_t)i * 32 + row];
-      if (l == -INFINITY) continue;
-      float w = expf(l - M);
-      L += w;
-      acc = fmaf(w, P.part_o[((int64_t)i * 32 + row) * D + d], acc);
+  const int nrows = nq * G;
+  const int tid = threadIdx.x;
+  __shared__ float s_part[2][8][32];
+  __shared__ float s_M[32], s_L[32];
+  __shared__ int s_nan[32];
+  // per-row statistics: thread (row = tid & 31, subset = tid >> 5) over items subset, +8, ...
+  {
+    const int row = tid & 31, sub = tid >> 5;
+    float mx = -INFINITY;
+    int bad = 0;
+    for (int i = sub; i < ni; i += 8) {
+      const float l = P.part_lse[(int64_t)(i0 + i) * 32 + row];
+      if (l != l) bad = 1;
+      else mx = fmaxf(mx, l);
     }
-    out = acc / L;
+    s_part[0][sub][row] = mx;
+    s_part[1][sub][row] = (float)bad;
+    __syncthreads();
+    if (tid < 32) {
+      float M = -INFINITY, nanf = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) { M = fmaxf(M, s_part[0][s][tid]); nanf = fmaxf(nanf, s_part[1][s][tid]); }
+      s_M[tid] = M;
+      s_nan[tid] = nanf != 0.f;
+    }
+    __syncthreads();
+    const float M = s_M[row];
+    float sum = 0.f;
+    if (M != -INFINITY)
+      for (int i = sub; i < ni; i += 8) {
+        const float l = P.part_lse[(int64_t)(i0 + i) * 32 + row];
+        if (l != -INFINITY) sum += expf(l - M);
+      }
+    s_part[0][sub][row] = sum;
+    __syncthreads();
+    if (tid < 32) {
+      float L = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) L += s_part[0][s][tid];
+      s_L[tid] = L;
+    }
+    __syncthreads();
+  }
+  const int e = blockIdx.y * kThreads + tid;  // f32x4 index in the partial
+  const int ln = e & 63, n = ln & 31, gg = ln >> 5, bq = e >> 6, b = bq >> 2, q = bq & 3;
+  if (n >= nrows) return;
+  const float M = s_M[n], L = s_L[n];
+  const bool nan = s_nan[n] != 0;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float lse = -INFINITY;
+  if (nan) {
+    acc = f32x4{NAN, NAN, NAN, NAN};
+    lse = NAN;
+  } else if (M != -INFINITY && L > 0.f) {
+    const float invL = 1.f / L;
+    const f32x4* po = (const f32x4*)P.part_o + (int64_t)i0 * C::NV + e;
+    int i = 0;
+    for (; i + 4 <= ni; i += 4) {
+      f32x4 x[4];
+      float l[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[u] = po[(int64_t)(i + u) * C::NV];
+        l[u] = P.part_lse[(int64_t)(i0 + i + u) * 32 + n];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (l[u] != -INFINITY) acc += x[u] * (expf(l[u] - M) * invL);
+    }
+    for (; i < ni; ++i) {
+      const float l = P.part_lse[(int64_t)(i0 + i) * 32 + n];
+      if (l != -INFINITY) acc += po[(int64_t)i * C::NV] * (expf(l - M) * invL);
+    }
     lse = M + logf(L);
   }
-  A.out_rot[((int64_t)tok * A.num_q_heads + head) * D + d] = out;
-  if (d == 0) A.lse[(int64_t)tok * A.num_q_heads + head] = lse;
+  const int tok = a + n / G, head = kvh * G + n % G;
+  float* orow = A.out_rot + ((int64_t)tok * A.num_q_heads + head) * D;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) orow[pv_d<D>(b, out_tok(4 * q + j, gg))] = acc[j];
+  if (bq == 0 && gg == 0) A.lse[(int64_t)tok * A.num_q_heads + head] = lse;
 }
 
 template <int D>
@@ -535,7 +743,7 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
     OSCAR_CHECK_LAUNCH("attn_main_kernel");
   }
   if (p.a.phases != 1) {
-    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, 32), dim3(D), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / kThreads), dim3(kThreads), 0, s, p);
     OSCAR_CHECK_LAUNCH("attn_merge_kernel");
   }
   return 0;
@@ -553,82 +761,97 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
                                   int32_t head_dim, int32_t chunk_tokens, int32_t target_items,
                                   int32_t* items, int32_t max_items, int32_t* groups,
                                   int32_t max_groups, oscar_plan_v1* plan) {
-  if (!qsl || !seqs || !plan || num_reqs < 0 || num_kv_heads < 1 || group < 1)
+  if (!qsl || !seqs || !plan || num_reqs < 0 || num_kv_heads < 1 || num_kv_heads > 0xffff || group < 1)
     return fail(-22, "oscar_attn_plan_v1: invalid arguments");
   if (head_dim != 128 && head_dim != 256)
     return fail(-22, "oscar_attn_plan_v1: head_dim %d unsupported (128/256)", head_dim);
   if (chunk_tokens < kTile) chunk_tokens = kTile;
-  if (chunk_tokens > 8192) chunk_tokens = 8192;
+  if (chunk_tokens > kMaxItemTokens) chunk_tokens = kMaxItemTokens;
   if (target_items < 1) target_items = 1;
-  // total visible keys over (request, kv head) groups with queries
-  int64_t total = 0;
-  int ngroups = 0;
+  // Per (request, kv head) group: body tiles are the full tiles every row sees
+  // (before min(history, seq - n_q + 1)); the tiles after them (current chunk,
+  // causal boundary, ragged end) form one tail item per group.  Body tiles are
+  // dealt to k items round-robin (item j: tiles j, j + k, ...), so a contiguous
+  // run of expensive tiles (the FP32 staging window) spreads over many items.
+  struct Grp { int req, kvh, nbody, ntail, k, first_slot; };
+  int ngroups = 0, ntails = 0;
+  int64_t body_total = 0;
   for (int r = 0; r < num_reqs; ++r) {
-    int nq = qsl[r + 1] - qsl[r];
+    const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
     if (nq * group > 32) return fail(-22, "oscar_attn_plan_v1: request %d has %d rows > 32", r, nq * group);
     if (seqs[r] < 0 || (has_new && seqs[r] < nq))
       return fail(-22, "oscar_attn_plan_v1: sequence length must cover its query chunk");
-    total += (int64_t)seqs[r] * num_kv_heads;
     ngroups += num_kv_heads;
   }
-  int64_t total_tiles = 0;
-  for (int r = 0; r < num_reqs; ++r)
-    if (qsl[r + 1] > qsl[r]) total_tiles += (int64_t)((seqs[r] + kTile - 1) / kTile) * num_kv_heads;
-  (void)total;
-  // per group: items of whole tiles, proportional to the group's share of all
-  // tiles (target_items overall), at most chunk_tokens (<= 8192) tokens each
-  struct Grp { int req, kvh, ntiles, nitems, first_slot; };
   Grp* gl = (Grp*)alloca(sizeof(Grp) * (ngroups > 0 ? ngroups : 1));
-  int gi = 0, nitems = 0, max_per_group = 0;
+  int gi = 0;
   for (int r = 0; r < num_reqs; ++r) {
-    int nq = qsl[r + 1] - qsl[r];
+    const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
+    const int seq = seqs[r], hist = has_new ? seq - nq : seq;
+    int fast_end = seq - nq + 1 < hist ? seq - nq + 1 : hist;
+    if (fast_end < 0) fast_end = 0;
+    const int nbody = fast_end / kTile;
+    const int ntail = (seq + kTile - 1) / kTile - nbody;
     for (int h = 0; h < num_kv_heads; ++h) {
-      int ntiles = (seqs[r] + kTile - 1) / kTile;
-      int k = total_tiles > 0 ? (int)(((int64_t)ntiles * target_items * 2 + total_tiles) / (2 * total_tiles)) : 1;
-      if (k < 1) k = 1;
-      const int max_tiles = chunk_tokens / kTile;
-      if ((ntiles + k - 1) / k > max_tiles) k = (ntiles + max_tiles - 1) / max_tiles;
-      if (k > ntiles && ntiles > 0) k = ntiles;
-      gl[gi] = {r, h, ntiles, k, nitems};
-      nitems += k;
-      if (k > max_per_group) max_per_group = k;
-      ++gi;
+      gl[gi++] = {r, h, nbody, ntail, 0, 0};
+      body_total += nbody;
+      ntails += ntail > 0;
     }
+  }
+  const int budget = target_items - ntails > ngroups ? target_items - ntails : ngroups;
+  const int max_tiles = chunk_tokens / kTile;
+  int nitems = 0, max_k = 0;
+  for (int q = 0; q < ngroups; ++q) {
+    Grp& G = gl[q];
+    int k = 0;
+    if (G.nbody > 0) {
+      k = (int)(((int64_t)G.nbody * budget * 2 + body_total) / (2 * body_total));
+      if (k < 1) k = 1;
+      if ((G.nbody + k - 1) / k > max_tiles) k = (G.nbody + max_tiles - 1) / max_tiles;
+      if (k > G.nbody) k = G.nbody;
+    }
+    G.k = k;
+    G.first_slot = nitems;
+    nitems += k + (G.ntail > 0);
+    if (k > max_k) max_k = k;
   }
   plan->num_items = nitems;
   plan->num_groups = ngroups;
   plan->partial_bytes = (int64_t)nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
   if (items == nullptr || groups == nullptr) return nitems;  // size query
   if (nitems > max_items || ngroups > max_groups) return fail(-28, "oscar_attn_plan_v1: buffers too small");
-  // Launch order interleaves groups (index = position * ngroups + group, compacted)
-  // so that workgroup i runs on XCD i % 8 and a group's items share one L2; the
-  // partial slots of a group stay contiguous for the merge.
+  // Launch order: the tail items first (they carry the slow work), then the body
+  // items interleaved over the groups so that consecutive workgroups, which the
+  // hardware deals round-robin to the 8 XCDs, spread every group over the chip.
+  // The partial slots of a group stay contiguous (tail, then body) for the merge.
   int idx = 0;
-  for (int pos = 0; pos < max_per_group; ++pos) {
+  auto emit = [&](const Grp& G, int slot, int first, int stride, int count) {
+    int32_t* it = items + (int64_t)idx++ * OSCAR_WORK_INTS;
+    const int nq = qsl[G.req + 1] - qsl[G.req];
+    it[0] = G.req;
+    it[1] = G.kvh | (nq << 16);
+    it[2] = first;
+    it[3] = stride;
+    it[4] = count;
+    it[5] = slot;
+    it[6] = qsl[G.req];
+    it[7] = seqs[G.req];
+  };
+  for (int q = 0; q < ngroups; ++q)
+    if (gl[q].ntail > 0) emit(gl[q], gl[q].first_slot, gl[q].nbody, 1, gl[q].ntail);
+  for (int pos = 0; pos < max_k; ++pos)
     for (int q = 0; q < ngroups; ++q) {
-      if (pos >= gl[q].nitems) continue;
-      const int k = gl[q].nitems;
-      const int tb = (int)((int64_t)gl[q].ntiles * pos / k);
-      const int te = (int)((int64_t)gl[q].ntiles * (pos + 1) / k);
-      int32_t* it = items + (int64_t)idx * OSCAR_WORK_INTS;
-      const int seq = seqs[gl[q].req];
-      it[0] = gl[q].req;
-      it[1] = gl[q].kvh;
-      it[2] = tb * kTile;
-      it[3] = te * kTile < seq ? te * kTile : seq;
-      it[4] = gl[q].first_slot + pos;
-      it[5] = q;
-      it[6] = it[7] = 0;
-      ++idx;
+      const Grp& G = gl[q];
+      if (pos >= G.k) continue;
+      emit(G, G.first_slot + (G.ntail > 0) + pos, pos, G.k, (G.nbody - pos + G.k - 1) / G.k);
     }
-  }
   for (int q = 0; q < ngroups; ++q) {
     groups[q * 4 + 0] = gl[q].req;
     groups[q * 4 + 1] = gl[q].kvh;
     groups[q * 4 + 2] = gl[q].first_slot;
-    groups[q * 4 + 3] = gl[q].nitems;
+    groups[q * 4 + 3] = gl[q].k + (gl[q].ntail > 0);
   }
   return nitems;
 }
@@ -648,11 +871,19 @@ extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream
   if (a.cache.num_kv_heads < 1 || a.num_q_heads % a.cache.num_kv_heads)
     return fail(-22, "oscar_attn_decode_v1: Hq must be a multiple of Hk");
   if ((a.cache.k_stride[2] & 15) || (a.cache.v_stride[2] & 15) || (a.cache.k_stride[1] & 15) ||
-      (a.cache.v_stride[1] & 15) || (((uintptr_t)a.cache.k) & 15) || (((uintptr_t)a.cache.v) & 15))
+      (a.cache.v_stride[1] & 15) || (a.cache.k_stride[0] & 15) || (a.cache.v_stride[0] & 15) ||
+      (((uintptr_t)a.cache.k) & 15) || (((uintptr_t)a.cache.v) & 15))
     return fail(-22, "oscar_attn_decode_v1: cache slots must be 16-byte aligned");
-  if (a.cache.block_size < 1 || 8192 / a.cache.block_size + 2 > 256)
-    return fail(-22, "oscar_attn_decode_v1: block_size %lld too small for the page table stage",
-                (long long)a.cache.block_size);
+  // queries and the current chunk are read as 16-byte vectors
+  if ((a.q_stride_token & 7) || (((uintptr_t)a.q) & 15) ||
+      (a.k_new && ((a.kv_new_stride_token & 7) || (((uintptr_t)a.k_new) & 15) || (((uintptr_t)a.v_new) & 15))))
+    return fail(-22, "oscar_attn_decode_v1: q / k_new / v_new rows must be 16-byte aligned");
+  if (a.cache.block_size < kTile || a.cache.block_size % kTile || a.cache.block_size > (1 << 20))
+    return fail(-22, "oscar_attn_decode_v1: block_size %lld must be a multiple of %d (<= 2^20)",
+                (long long)a.cache.block_size, kTile);
+  if (a.staging && (a.staging->rows < 1 || a.staging->rows * a.cache.block_size >= (1ll << 31) ||
+                    (((uintptr_t)a.staging->stage_k) & 15) || (((uintptr_t)a.staging->stage_v) & 15)))
+    return fail(-22, "oscar_attn_decode_v1: staging arena rows out of range or unaligned");
   AttnParams p{};
   p.a = a;
   p.has_stage = a.staging != nullptr;

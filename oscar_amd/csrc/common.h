@@ -59,6 +59,31 @@ __device__ __forceinline__ void store_elem(void* base, int32_t dtype, int64_t i,
   else ((float*)base)[i] = x;
 }
 
+// 8 consecutive elements (16-byte aligned for 2-byte types, 2 x 16 bytes for fp32)
+// of dtype DT as floats
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float* v) {
+  if constexpr (DT == OSCAR_F32) {
+    const f32x4 a = *(const f32x4*)((const float*)base + i);
+    const f32x4 b = *(const f32x4*)((const float*)base + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[4 + e] = b[e]; }
+  } else {
+    const u32x4 a = *(const u32x4*)((const uint16_t*)base + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned w = a[e];
+      if constexpr (DT == OSCAR_BF16) {
+        v[2 * e] = __uint_as_float(w << 16);
+        v[2 * e + 1] = __uint_as_float(w & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_bits_to_f32(w & 0xffff);
+        v[2 * e + 1] = f16_bits_to_f32(w >> 16);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ float wave_max(float x) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -68,5 +93,13 @@ __device__ __forceinline__ float wave_min(float x) {
   for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
   return x;
 }
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// s_waitcnt lgkmcnt(0) leaving vmcnt/expcnt at their maxima (gfx9 encoding):
+// waits for this wave's LDS traffic without draining outstanding global loads.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 }  // namespace oscar

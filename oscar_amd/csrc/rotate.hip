@@ -6,45 +6,63 @@
 // (x_hi R_hi + x_lo R_hi + x_hi R_lo, hi = bf16(v), lo = bf16(v - hi)), which keeps
 // the product error below 2^-16 of |x||R| with fp32 accumulation; the result is
 // rounded once to the output dtype.
+//
+// The input dtype, the output dtype and the transpose flag are template
+// parameters, so the operand loads of all K-steps are plain vector loads with no
+// branch between them and the compiler issues them ahead of the MFMAs.
 #include "common.h"
 
 namespace oscar {
 
 namespace {
 
-struct Split { __bf16 hi, lo; };
+typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
+typedef float __attribute__((ext_vector_type(2))) f32x2;
 
-__device__ __forceinline__ Split split_bf16(float v) {
-  unsigned short h = f32_to_bf16_bits(v);
-  float hv = bf16_bits_to_f32(h);
-  unsigned short l = f32_to_bf16_bits(v - hv);
-  return {__builtin_bit_cast(__bf16, h), __builtin_bit_cast(__bf16, l)};
+// hi/lo bf16 split of 8 floats into two MFMA operands
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2 a = {v[2 * i], v[2 * i + 1]};
+    const bf16x2 hb = __builtin_convertvector(a, bf16x2);
+    const f32x2 hv = __builtin_convertvector(hb, f32x2);
+    h[i] = __builtin_bit_cast(unsigned, hb);
+    l[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(a - hv, bf16x2));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
 }
 
+template <int D, int XT, int OT, bool TR>
 __global__ __launch_bounds__(64) void rotate_kernel(oscar_rotate_args_v1 a) {
   const int lane = threadIdx.x, m = lane & 31, g = lane >> 5;
   const int64_t row0 = (int64_t)blockIdx.x * 32;
   const int col0 = blockIdx.y * 32;
-  const int64_t D = a.head_dim;
   const int64_t row = row0 + m;
   const bool row_ok = row < a.rows;
+  const int64_t xrow = (row_ok ? row : row0) * a.x_stride_row;  // row0 < rows always
+  const int col = col0 + m;
   f32x16 acc = {};
-  for (int k0 = 0; k0 < D; k0 += 16) {
-    bf16x8 xh, xl, rh, rl;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int k = k0 + 8 * g + e;
-      float xv = row_ok ? load_elem(a.x, a.x_dtype, row * a.x_stride_row + k) : 0.f;
-      const Split xs = split_bf16(xv);
-      xh[e] = xs.hi;
-      xl[e] = xs.lo;
-      // B[k][n] = R[k][col] or R^T[k][col] = R[col][k]
-      const int col = col0 + m;
-      float rv = a.transpose ? a.r[(int64_t)col * D + k] : a.r[(int64_t)k * D + col];
-      const Split rs = split_bf16(rv);
-      rh[e] = rs.hi;
-      rl[e] = rs.lo;
+  for (int k0 = 0; k0 < D; k0 += 16) {
+    const int kk = k0 + 8 * g;
+    float xv[8], rv[8];
+    load8<XT>(a.x, xrow + kk, xv);
+    if (!row_ok) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = 0.f;
     }
+    // B[k][n]: R[k][col], or R^T[k][col] = R[col][k] (contiguous in k)
+    if constexpr (TR) {
+      load8<OSCAR_F32>(a.r, (int64_t)col * D + kk, rv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rv[e] = a.r[(int64_t)(kk + e) * D + col];
+    }
+    bf16x8 xh, xl, rh, rl;
+    split8(xv, xh, xl);
+    split8(rv, rh, rl);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, rh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, rh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, rl, acc, 0, 0, 0);
@@ -54,8 +72,28 @@ __global__ __launch_bounds__(64) void rotate_kernel(oscar_rotate_args_v1 a) {
   for (int r = 0; r < 16; ++r) {
     const int i = 8 * (r >> 2) + 4 * g + (r & 3);
     const int64_t orow = row0 + i;
-    if (orow < a.rows) store_elem(a.out, a.out_dtype, orow * a.out_stride_row + col0 + m, acc[r]);
+    if (orow < a.rows) store_elem(a.out, OT, orow * a.out_stride_row + col, acc[r]);
   }
+}
+
+template <int D, int XT, int OT>
+void launch_tr(const oscar_rotate_args_v1& a, dim3 grid, hipStream_t s) {
+  if (a.transpose) hipLaunchKernelGGL((rotate_kernel<D, XT, OT, true>), grid, dim3(64), 0, s, a);
+  else hipLaunchKernelGGL((rotate_kernel<D, XT, OT, false>), grid, dim3(64), 0, s, a);
+}
+
+template <int D, int XT>
+void launch_out(const oscar_rotate_args_v1& a, dim3 grid, hipStream_t s) {
+  if (a.out_dtype == OSCAR_BF16) launch_tr<D, XT, OSCAR_BF16>(a, grid, s);
+  else if (a.out_dtype == OSCAR_F16) launch_tr<D, XT, OSCAR_F16>(a, grid, s);
+  else launch_tr<D, XT, OSCAR_F32>(a, grid, s);
+}
+
+template <int D>
+void launch_in(const oscar_rotate_args_v1& a, dim3 grid, hipStream_t s) {
+  if (a.x_dtype == OSCAR_BF16) launch_out<D, OSCAR_BF16>(a, grid, s);
+  else if (a.x_dtype == OSCAR_F16) launch_out<D, OSCAR_F16>(a, grid, s);
+  else launch_out<D, OSCAR_F32>(a, grid, s);
 }
 
 }  // namespace
@@ -69,13 +107,22 @@ extern "C" int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream) {
   const oscar_rotate_args_v1& a = *args;
   if (a.rows == 0) return 0;
   if (a.rows < 0 || !a.x || !a.r || !a.out) return fail(-22, "oscar_rotate_v1: invalid arguments");
-  if (a.head_dim % 32 || a.head_dim <= 0 || a.head_dim > 1024)
-    return fail(-22, "oscar_rotate_v1: head_dim must be a multiple of 32");
+  if (a.head_dim != 128 && a.head_dim != 256)
+    return fail(-22, "oscar_rotate_v1: head_dim %lld unsupported (128/256)", (long long)a.head_dim);
   if (a.x_stride_row < a.head_dim || a.out_stride_row < a.head_dim)
     return fail(-22, "oscar_rotate_v1: row strides smaller than head_dim");
+  if ((a.x_dtype != OSCAR_F32 && a.x_dtype != OSCAR_F16 && a.x_dtype != OSCAR_BF16) ||
+      (a.out_dtype != OSCAR_F32 && a.out_dtype != OSCAR_F16 && a.out_dtype != OSCAR_BF16))
+    return fail(-22, "oscar_rotate_v1: unsupported dtype");
+  // rows are read as 16-byte vectors (8 elements of bf16/fp16, 2 x 4 of fp32)
+  const int esz = a.x_dtype == OSCAR_F32 ? 4 : 2;
+  if ((((uintptr_t)a.x) & 15) || ((a.x_stride_row * esz) & 15) || (((uintptr_t)a.r) & 15))
+    return fail(-22, "oscar_rotate_v1: x rows and R must be 16-byte aligned");
   if (a.rows > (int64_t)1 << 36) return fail(-22, "oscar_rotate_v1: too many rows");
   dim3 grid((unsigned)((a.rows + 31) / 32), (unsigned)(a.head_dim / 32));
-  hipLaunchKernelGGL(rotate_kernel, grid, dim3(64), 0, (hipStream_t)stream, a);
+  hipStream_t s = (hipStream_t)stream;
+  if (a.head_dim == 256) launch_in<256>(a, grid, s);
+  else launch_in<128>(a, grid, s);
   OSCAR_CHECK_LAUNCH("rotate_kernel");
   return 0;
 }

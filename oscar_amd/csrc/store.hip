@@ -10,17 +10,25 @@
 //                        y = x @ R with fp64 accumulation: every product of a
 //                        bf16/fp16/fp32 input with an fp32 rotation entry is exact in
 //                        fp64 and the sum is rounded once, which yields the correctly
-//                        rounded fp32 value independent of summation order.  Writes y
-//                        (fp32 workspace, K/V only) and the read-path copies in the
-//                        input dtype.  Column block 0 of the K kind also records the
-//                        last-writer claims (64-bit atomicMax of epoch<<32 | token)
+//                        rounded fp32 value independent of summation order.  The
+//                        workgroup stages its 64 columns of R and its input vectors in
+//                        LDS with one batch of vector loads, then accumulates from LDS.
+//                        Writes y (fp32 workspace, K/V only) and the read-path copies
+//                        in the input dtype.  Column block 0 of the K kind also records
+//                        the last-writer claims (64-bit atomicMax of epoch<<24 | token)
 //                        for cache slots and staging seats, and performs the owner-tag
 //                        invalidation of a standalone KV update.
 //   store_quant_kernel   one wave per (token, kv head, K|V) vector: optional sort-clip,
 //                        fp16-rounded scale/zero, codes clamp(floor((x-zero)/scale+0.5),
 //                        0, 3), 2-bit packing and the byte writes of the slot winner;
 //                        staging winners write the owner tag and, inside the sink/recent
-//                        window, the unclipped fp32 rotated vector.
+//                        window, the unclipped fp32 rotated vector.  Its global reads
+//                        come in two rounds (slot, row, request bounds; then the claims).
+//
+// Claim epochs live on the device in two int64 words so that a captured graph
+// replays with fresh epochs and no extra launch: the rotate kernel uses
+// E = word0 + 1 and stores E in word1; the quant kernel reads word1 and copies it
+// to word0 for the next call.
 #include "common.h"
 
 namespace oscar {
@@ -29,7 +37,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kCols = 64;     // output columns per rotate workgroup
-constexpr int kChunk = 32;    // contraction rows staged in LDS per step
 
 enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
 
@@ -43,12 +50,30 @@ __device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
   // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
   return (long long)((epoch << 24) | (token & 0xffffffll));
 }
+constexpr int64_t kMaxEpoch = (1ll << 39) - 1;
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, int64_t bs, int64_t rows) {
   return ((slot / bs) % rows) * bs + slot % bs;
 }
 
-template <int D, int TV>
+// 4 floats to dtype DT at element i (8 or 16 bytes, aligned)
+template <int DT>
+__device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
+  if constexpr (DT == OSCAR_F32) {
+    *(f32x4*)((float*)base + i) = f32x4{y[0], y[1], y[2], y[3]};
+  } else {
+    unsigned w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const unsigned lo = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j]) : f32_to_f16_bits(y[2 * j]);
+      const unsigned hi = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j + 1]) : f32_to_f16_bits(y[2 * j + 1]);
+      w[j] = lo | (hi << 16);
+    }
+    *(u32x2*)((uint16_t*)base + i) = u32x2{w[0], w[1]};
+  }
+}
+
+template <int D, int TV, int XT>
 __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
   const oscar_store_args_v1& a = p.a;
   const int kind = blockIdx.z;
@@ -59,9 +84,48 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
   const int col0 = blockIdx.y * kCols;
   const int tid = threadIdx.x;
 
+  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
+  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
+                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
+  const float* R = (kind == KIND_V) ? a.rv : a.rk;
+  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
+  float* y_out = (kind == KIND_Q) ? nullptr : p.y + (int64_t)kind * a.num_tokens * heads * D;
+
+  // ---- one batch of loads: this block's 64 columns of R and its TV input vectors
+  __shared__ __attribute__((aligned(16))) float s_r[D][kCols];
+  __shared__ float s_x[D][TV + 1];
+  constexpr int RV = D * kCols / 4 / kThreads;       // float4 of R per thread
+  constexpr int XV = TV * (D / 8) / kThreads;        // 8-element x loads per thread
+  static_assert(RV >= 1 && (TV * (D / 8)) % kThreads == 0, "tile shape");
+  f32x4 rr[RV];
+  float xv[XV][8];
+#pragma unroll
+  for (int i = 0; i < RV; ++i) {
+    const int e = tid + i * kThreads, k = e / (kCols / 4), c4 = e % (kCols / 4);
+    if (R != nullptr) {
+      rr[i] = *(const f32x4*)(R + (int64_t)k * D + col0 + 4 * c4);
+    } else {
+      const int c = col0 + 4 * c4 - k;
+      rr[i] = f32x4{c == 0 ? 1.f : 0.f, c == -1 ? 1.f : 0.f, c == -2 ? 1.f : 0.f, c == -3 ? 1.f : 0.f};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
+    const int64_t vec = vec0 + v < nvec ? vec0 + v : vec0;
+    const int64_t t = vec / heads, h = vec % heads;
+    load8<XT>(src, t * src_stride + h * D + k8, xv[i]);
+    if (vec0 + v >= nvec) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
+    }
+  }
+
   // last-writer claims and standalone invalidation, once per token
   if (kind == KIND_K && blockIdx.y == 0) {
-    const int64_t epoch = *a.epoch_counter + 1;
+    const int64_t e0 = a.epoch_counter[0];
+    const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
+    if (blockIdx.x == 0 && tid == 0) a.epoch_counter[1] = epoch;
     for (int i = tid; i < TV; i += kThreads) {
       int64_t vec = vec0 + i;
       if (vec >= nvec || vec % heads != 0) continue;
@@ -76,14 +140,19 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
     }
   }
 
-  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
-  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
-                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
-  const float* R = (kind == KIND_V) ? a.rv : a.rk;
-  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
-  float* y_out = (kind == KIND_Q) ? nullptr : p.y + (int64_t)kind * a.num_tokens * heads * D;
+#pragma unroll
+  for (int i = 0; i < RV; ++i) {
+    const int e = tid + i * kThreads, k = e / (kCols / 4), c4 = e % (kCols / 4);
+    *(f32x4*)&s_r[k][4 * c4] = rr[i];
+  }
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_x[k8 + j][v] = xv[i][j];
+  }
+  __syncthreads();
 
-  __shared__ double xs[kChunk][TV];
   // thread tile: 4 consecutive columns x RPT vectors
   constexpr int kColGroups = kCols / 4;              // 16
   constexpr int kRowGroups = kThreads / kColGroups;  // 16
@@ -95,63 +164,28 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
   for (int i = 0; i < RPT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
-
-  for (int k0 = 0; k0 < D; k0 += kChunk) {
-    __syncthreads();
-    for (int e = tid; e < kChunk * TV; e += kThreads) {
-      int vv = e / kChunk, kk = e % kChunk;
-      int64_t vec = vec0 + vv;
-      double x = 0.0;
-      if (vec < nvec) {
-        int64_t t = vec / heads, h = vec % heads;
-        x = (double)load_elem(src, a.kv_dtype, t * src_stride + h * D + k0 + kk);
-      }
-      xs[kk][vv] = x;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < kChunk; ++kk) {
-      double r0, r1, r2, r3;
-      if (R != nullptr) {
-        float4 r4 = *(const float4*)(R + (int64_t)(k0 + kk) * D + col0 + cg * 4);
-        r0 = r4.x; r1 = r4.y; r2 = r4.z; r3 = r4.w;
-      } else {
-        int c = col0 + cg * 4 - (k0 + kk);
-        r0 = c == 0; r1 = c == -1; r2 = c == -2; r3 = c == -3;
-      }
+#pragma unroll 8
+  for (int k = 0; k < D; ++k) {
+    const f32x4 r4 = *(const f32x4*)&s_r[k][4 * cg];
+    const double r0 = r4[0], r1 = r4[1], r2 = r4[2], r3 = r4[3];
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        double x = xs[kk][rg * RPT + i];
-        acc[i][0] = fma(x, r0, acc[i][0]);
-        acc[i][1] = fma(x, r1, acc[i][1]);
-        acc[i][2] = fma(x, r2, acc[i][2]);
-        acc[i][3] = fma(x, r3, acc[i][3]);
-      }
+    for (int i = 0; i < RPT; ++i) {
+      const double x = s_x[k][rg * RPT + i];
+      acc[i][0] = fma(x, r0, acc[i][0]);
+      acc[i][1] = fma(x, r1, acc[i][1]);
+      acc[i][2] = fma(x, r2, acc[i][2]);
+      acc[i][3] = fma(x, r3, acc[i][3]);
     }
   }
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
-    int64_t vec = vec0 + rg * RPT + i;
+    const int64_t vec = vec0 + rg * RPT + i;
     if (vec >= nvec) continue;
-    float y[4] = {(float)acc[i][0], (float)acc[i][1], (float)acc[i][2], (float)acc[i][3]};
-    int64_t base = vec * D + col0 + cg * 4;
-    if (y_out != nullptr) *(float4*)(y_out + base) = make_float4(y[0], y[1], y[2], y[3]);
-    if (rot_out != nullptr) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) store_elem(rot_out, a.kv_dtype, base + j, y[j]);
-    }
+    const float y[4] = {(float)acc[i][0], (float)acc[i][1], (float)acc[i][2], (float)acc[i][3]};
+    const int64_t base = vec * D + col0 + cg * 4;
+    if (y_out != nullptr) *(f32x4*)(y_out + base) = f32x4{y[0], y[1], y[2], y[3]};
+    if (rot_out != nullptr) store4<XT>(rot_out, base, y);
   }
-}
-
-// token -> request by binary search over query_start_loc clipped to num_tokens
-__device__ int find_request(const int32_t* qsl, int num_reqs, int64_t num_tokens, int64_t t) {
-  int lo = 0, hi = num_reqs;
-  while (hi - lo > 1) {
-    int mid = (lo + hi) >> 1;
-    int64_t start = qsl[mid] < num_tokens ? qsl[mid] : num_tokens;
-    if (start <= t) lo = mid; else hi = mid;
-  }
-  return lo;
 }
 
 // Sort-based clip threshold (backend.py:140-145): the idx-th smallest |x| of a
@@ -175,57 +209,84 @@ __device__ float clip_threshold(const float* row, int idx, volatile float* slot)
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
+  constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
   const oscar_store_args_v1& a = p.a;
   const int kind = blockIdx.y;  // K or V
   const int64_t hk = a.cache.num_kv_heads;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // this call's epoch (word1, set by the rotate launch); word0 takes it for the next
+  // call (no other quant workgroup reads word0)
+  const int64_t epoch = a.epoch_counter[1];
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
   const int64_t vec = (int64_t)blockIdx.x * (kThreads / 64) + wave;
   if (vec >= a.num_tokens * hk) return;
   const int64_t t = vec / hk, h = vec % hk;
-  const int64_t slot = a.slot_mapping[t];
-  if (slot < 0 || slot >= p.capacity) return;
-  const int64_t epoch = *a.epoch_counter + 1;
+  const bool active = lane < NL;
 
+  // ---- round 1: slot, this vector's row, request starts
+  const int64_t slot = a.slot_mapping[t];
+  const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
+  const f32x4 x4 = *(const f32x4*)(y + 4 * (active ? lane : 0));
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t
+  int req = 0;
+  if (window) {
+    int count = 0;
+    for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
+      const int r = c0 + lane;
+      const int64_t st = r < a.num_reqs ? a.query_start_loc[r] : a.num_tokens;
+      const int64_t start = st < a.num_tokens ? st : a.num_tokens;
+      count += __popcll(__ballot(r < a.num_reqs && start <= t));
+    }
+    req = count > 0 ? count - 1 : 0;
+  }
+  if (slot < 0 || slot >= p.capacity) return;
+  const int64_t bs = a.cache.block_size;
+  const int64_t blk = slot / bs, off = slot % bs;
+
+  // ---- round 2: claims and the request's bounds
+  const long long mine = claim_value(epoch, t);
+  const long long slot_claim = (long long)a.slot_claims[slot];
+  int64_t seat = 0;
+  long long seat_claim = 0;
+  int64_t seq = 0, end = 0;
+  if (window) {
+    seat = seat_of(slot, bs, a.staging.rows);
+    seat_claim = (long long)a.seat_claims[seat];
+    seq = a.seq_lens[req];
+    end = a.query_start_loc[req + 1];
+  }
   __shared__ float rows[kThreads / 64][D];
   __shared__ float clip_slot[kThreads / 64];
   float* row = rows[wave];
-  const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
-  for (int i = lane; i < D; i += 64) row[i] = y[i];
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
+  if (active) *(f32x4*)&row[4 * lane] = x4;
 
-  const int64_t bs = a.cache.block_size;
-  const int64_t blk = slot / bs, off = slot % bs;
-  if (a.stage_mode == OSCAR_STAGE_WRITE) {
-    const int64_t seat = seat_of(slot, bs, a.staging.rows);
-    if ((long long)a.seat_claims[seat] == claim_value(epoch, t)) {
-      int r = find_request(a.query_start_loc, a.num_reqs, a.num_tokens, t);
-      int64_t seq = a.seq_lens[r], end = a.query_start_loc[r + 1];
-      int64_t pos = seq - end + t;
-      bool keep = (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
-      if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
-      if (keep) {
-        float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) + (seat * hk + h) * D;
-        for (int i = lane; i < D; i += 64) dst[i] = row[i];
-      }
+  if (window && seat_claim == mine) {
+    const int64_t pos = seq - end + t;
+    const bool keep = (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
+    if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
+    if (keep && active) {
+      float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) + (seat * hk + h) * D;
+      *(f32x4*)&dst[4 * lane] = x4;
     }
   }
-  if ((long long)a.slot_claims[slot] != claim_value(epoch, t)) return;
+  if (slot_claim != mine) return;
 
   const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
   float thr = INFINITY;
   if (clip > 0.f) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
     int idx = (int)(clip * (float)D);
     if (idx > D - 1) idx = D - 1;
     thr = clip_threshold<D>(row, idx, &clip_slot[wave]);
   }
   // lane b handles byte b = elements 4b..4b+3
-  const bool active = lane < D / 4;
   float x[4];
   float vmin = INFINITY, vmax = -INFINITY;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float v = active ? row[lane * 4 + j] : 0.f;
+    float v = active ? x4[j] : 0.f;
     if (clip > 0.f) v = fminf(fmaxf(v, -thr), thr);
     x[j] = v;
     if (active) { vmin = fminf(vmin, v); vmax = fmaxf(vmax, v); }
@@ -256,31 +317,30 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   }
 }
 
-// Advance the per-device claim epoch once both launches of a call have finished
-// (vector store: the counter is ordinary device memory).
-__global__ void store_epoch_kernel(int64_t* counter) {
-  const int64_t e = *counter + 1;
-  if (e < (1ll << 39) - 1) *counter = e;  // saturates (5e11 calls) instead of wrapping
+template <int D, int TV>
+void launch_rotate(const StoreParams& p, dim3 grid, hipStream_t s) {
+  dim3 block(kThreads);
+  if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_BF16>), grid, block, 0, s, p);
+  else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_F16>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_F32>), grid, block, 0, s, p);
 }
 
 template <int D>
 int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_t s) {
   const int kinds = q_vec ? 3 : 2;
   const int64_t max_vec = kv_vec > q_vec ? kv_vec : q_vec;
-  dim3 block(kThreads);
   if (max_vec >= 4096) {
     dim3 grid((unsigned)((max_vec + 63) / 64), D / kCols, kinds);
-    hipLaunchKernelGGL((store_rotate_kernel<D, 64>), grid, block, 0, s, p);
+    launch_rotate<D, 64>(p, grid, s);
   } else {
-    dim3 grid((unsigned)((max_vec + 15) / 16), D / kCols, kinds);
-    hipLaunchKernelGGL((store_rotate_kernel<D, 16>), grid, block, 0, s, p);
+    constexpr int TV = D == 64 ? 32 : 16;  // at least one 8-element load per thread
+    dim3 grid((unsigned)((max_vec + TV - 1) / TV), D / kCols, kinds);
+    launch_rotate<D, TV>(p, grid, s);
   }
   OSCAR_CHECK_LAUNCH("store_rotate_kernel");
   dim3 qgrid((unsigned)((kv_vec + 3) / 4), 2);
-  hipLaunchKernelGGL(store_quant_kernel<D>, qgrid, block, 0, s, p);
+  hipLaunchKernelGGL(store_quant_kernel<D>, qgrid, dim3(kThreads), 0, s, p);
   OSCAR_CHECK_LAUNCH("store_quant_kernel");
-  hipLaunchKernelGGL(store_epoch_kernel, dim3(1), dim3(1), 0, s, p.a.epoch_counter);
-  OSCAR_CHECK_LAUNCH("store_epoch_kernel");
   return 0;
 }
 
@@ -319,6 +379,17 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
     return fail(-22, "oscar_store_v1: cache base must be 4-byte aligned");
   if (a.key_stride_token < a.cache.num_kv_heads * D || a.value_stride_token < a.cache.num_kv_heads * D)
     return fail(-22, "oscar_store_v1: key/value row stride smaller than heads*D");
+  // inputs are read 8 elements (16 or 32 bytes) at a time, outputs written 4 at a time
+  const int esz = a.kv_dtype == OSCAR_F32 ? 4 : 2;
+  auto misaligned = [&](const void* ptr, int64_t stride) {
+    return ptr != nullptr && ((((uintptr_t)ptr) & 15) || ((stride * esz) & 15));
+  };
+  if (misaligned(a.key, a.key_stride_token) || misaligned(a.value, a.value_stride_token) ||
+      (a.query_rot != nullptr && misaligned(a.query, a.query_stride_token)))
+    return fail(-22, "oscar_store_v1: key/value/query rows must be 16-byte aligned");
+  if ((a.key_rot && (((uintptr_t)a.key_rot) & 15)) || (a.value_rot && (((uintptr_t)a.value_rot) & 15)) ||
+      (a.query_rot && (((uintptr_t)a.query_rot) & 15)))
+    return fail(-22, "oscar_store_v1: rotated outputs must be 16-byte aligned");
   if ((a.rk && (((uintptr_t)a.rk) & 15)) || (a.rv && (((uintptr_t)a.rv) & 15)))
     return fail(-22, "oscar_store_v1: rotations must be 16-byte aligned");
   if (a.slot_claims == nullptr || a.epoch_counter == nullptr)
@@ -331,6 +402,9 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
         (a.seat_claims == nullptr || a.staging.stage_k == nullptr || a.staging.stage_v == nullptr ||
          a.query_start_loc == nullptr || a.seq_lens == nullptr || a.num_reqs <= 0))
       return fail(-22, "oscar_store_v1: window write needs seat_claims, arena and request metadata");
+    if (a.stage_mode == OSCAR_STAGE_WRITE &&
+        ((((uintptr_t)a.staging.stage_k) & 15) || (((uintptr_t)a.staging.stage_v) & 15)))
+      return fail(-22, "oscar_store_v1: staging arena must be 16-byte aligned");
   }
   if (a.query_rot != nullptr &&
       (a.query == nullptr || a.num_q_heads <= 0 || a.query_stride_token < a.num_q_heads * D))

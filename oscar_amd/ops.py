@@ -69,7 +69,7 @@ class DeviceScratch:
     def __init__(self, device: torch.device):
         self.device = device
         # claim epoch lives on the device so that captured graphs replay with fresh epochs
-        self.epoch_counter = torch.zeros(1, dtype=torch.int64, device=device)
+        self.epoch_counter = torch.zeros(2, dtype=torch.int64, device=device)
         self.slot_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.seat_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.store_ws = torch.empty(0, dtype=torch.uint8, device=device)

@@ -81,14 +81,15 @@ def test_decode_plan_covers_each_history_token_once(cuda):
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=1, group=6,
                            head_dim=256, device=torch.device("cuda"), target_items=256)
     items = np.array(plan.host_items).reshape(-1, 8)
-    assert plan.num_items == 256
+    assert plan.num_items == 256  # 8 tail items + 248 body items
     for r, seq in enumerate(c["seqs"]):
         rows = items[items[:, 0] == r]
-        cover = np.zeros(seq, np.int32)
-        for _, _, kb, ke, *_ in rows:
-            cover[kb:ke] += 1
+        cover = np.zeros((seq + 31) // 32, np.int32)
+        for _, kvh_nq, first, stride, count, *_ in rows:
+            cover[first + stride * np.arange(count)] += 1
+            assert kvh_nq >> 16 == 4
         assert (cover == 1).all()
-        assert len(set(rows[:, 4])) == len(rows)
+        assert len(set(rows[:, 5])) == len(rows)
 
 
 def test_prefill_fresh_only_matches_sdpa(cuda):
