@@ -198,8 +198,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // LDS
   __shared__ int32_t s_blk[kMaxPages];                 // block ids of the item's pages
   __shared__ int32_t s_seat[kMaxPages];                // their seat-row base (blk % rows) * bs
-  __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][kTile * C::NB];
-  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][kTile];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][2][kTile * C::NB];  // double buffer
+  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][2][kTile];
   __shared__ __attribute__((aligned(16))) float s_ml[kWaves][2][32];
   __shared__ __attribute__((aligned(16))) uint16_t s_cur[2][kMaxCur][D];  // current K / V
   __shared__ __attribute__((aligned(16))) u32x4 s_q[C::KSTEPS][64];        // Q^T operand
@@ -333,22 +333,30 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // a tile that turns out slow (staged token, mask, ragged end, or a max more than
   // kLazy above the wave's reference max) or that only pads the pipeline runs with
   // P = 0 and, if real, is queued for the slow pass.
-  auto fast_tile = [&](int ti, const TileRegs<D>& r) {
+  //
+  // Two tiles are in compute at once: iteration i runs the QK MFMAs of tile i+1
+  // (their operands looked up on the VALU in between), then the softmax of tile
+  // i+1 on the VALU next to the PV MFMAs of tile i, so the MFMA and VALU pipes
+  // overlap.  V codes and V constants sit in LDS double buffers (tile parity).
+
+  // QK of tile ti: V codes and V constants to LDS buffer bf, S^T = K Q^T with the
+  // exact history values looked up per code pair.  Returns the pre-softmax slow
+  // flag (a staged token, or a tile beyond the fast range).
+  auto qk_tile = [&](int ti, const TileRegs<D>& r, int bf, f32x16& S) -> bool {
     const int t0 = tile_t0(wave + kWaves * ti);
     const int p = t0 + m;
     const bool real = ti < my;
     const bool staged = P.has_stage && real && p < hist && r.own == (int64_t)r.blk;
     st_bits |= (uint64_t)staged << (ti & 63);  // ti < 64 whenever staged
-    bool slow = real && !((t0 + kTile <= fast_end) && !__any(staged));
-    // V codes to LDS, natural layout [token][NB]; per-token V constants
+    const bool slow = real && !((t0 + kTile <= fast_end) && !__any(staged));
 #pragma unroll
-    for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
-    s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
-    s_cst[wave][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
-    // S^T = K Q^T with the exact history values looked up per code pair
+    for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][bf][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
+    s_cst[wave][bf][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
+    s_cst[wave][bf][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
     unsigned lut_lo, lut_hi;
     value_table(r.meta[0], lut_lo, lut_hi);
-    f32x16 S = {};
+#pragma unroll
+    for (int r2 = 0; r2 < 16; ++r2) S[r2] = 0.f;
 #pragma unroll
     for (int i = 0; i < C::NCH; ++i) {
       unsigned o[8];
@@ -358,6 +366,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]}),
                                                   qop(2 * i + 1), S, 0, 0, 0);
     }
+    return slow;
+  };
+
+  // softmax of tile ti (scores S, V constants in buffer bf): P' = p * s_V (fp16)
+  // feeds the PV MFMA, sum p and sum p * z_V accumulate on the VALU
+  auto softmax_tile = [&](int ti, const f32x16& S, bool slow, int bf, u32x4* pb) {
+    const bool real = ti < my;
     wait_lds();
     __builtin_amdgcn_wave_barrier();
     float xs[16];
@@ -375,13 +390,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (slow) slow_mask |= 1ull << ti;
     const bool use = real && !slow;
     if (use && first) m_run = mx;
-    // probabilities; P' = p * s_V feeds the MFMA, sum p*z_V the VALU
-    u32x4 pb[2];
     float lsum = 0.f, zsum = 0.f;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const f32x4 sv = *(const f32x4*)&s_cst[wave][0][8 * q4 + 4 * g];
-      const f32x4 zv = *(const f32x4*)&s_cst[wave][1][8 * q4 + 4 * g];
+      const f32x4 sv = *(const f32x4*)&s_cst[wave][bf][0][8 * q4 + 4 * g];
+      const f32x4 zv = *(const f32x4*)&s_cst[wave][bf][1][8 * q4 + 4 * g];
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
         const int r0 = 4 * q4 + i;
@@ -396,7 +409,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
     l_run += lsum;
     z_run += zsum;
-    // O^T += V^T P'^T, V^T from LDS via transpose reads
+  };
+
+  // PV of a tile whose V codes sit in buffer bf: O^T += V^T P'^T, V^T from LDS via
+  // transpose reads
+  auto pv_tile = [&](int bf, const u32x4* pb) {
     const int G16 = lane >> 4, i16 = lane & 15;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -405,7 +422,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 #pragma unroll
       for (int cp = 0; cp < D / 128; ++cp) {
         const int chunk = (D == 256) ? (2 * cp + (G16 & 1)) : (G16 & 1);
-        const uint8_t* addr = &s_vcode[wave][tok * C::NB + chunk * 16 + half8];
+        const uint8_t* addr = &s_vcode[wave][bf][tok * C::NB + chunk * 16 + half8];
         i32x2 tr = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             (__attribute__((address_space(3))) i32x2*)(addr));
         const unsigned x0 = (unsigned)tr[0], x1 = (unsigned)tr[1];
@@ -425,21 +442,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
   };
 
-  // software pipeline: slot d holds tile base+d; after it is computed the slot is
-  // refilled with tile base+d+kDepth (clamped to the last tile: the surplus loads
-  // at the end re-read a tile already in cache and are never used)
+  // software pipeline: tile t's packed data sits in register slot t % 3 from its load
+  // until its QK, then the slot is refilled with tile t + 3 (clamped to the last tile:
+  // the surplus loads at the end re-read a tile already in cache and are never used)
   {
+    static_assert(kDepth == 3, "the unrolled slot rotation below assumes three slots");
     TileRegs<D> R[kDepth];
     const int last = my > 0 ? my - 1 : 0;
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) load_tile(d < last ? d : last, R[d]);
+    f32x16 S;
+    u32x4 pb[2];
+    {
+      const bool sl = qk_tile(0, R[0], 0, S);
+      softmax_tile(0, S, sl, 0, pb);
+      load_tile(3 < last ? 3 : last, R[0]);
+    }
     for (int base = 0; base < my; base += kDepth) {
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        const int ti = base + d;
-        fast_tile(ti, R[d]);
-        const int nx = ti + kDepth;
-        load_tile(nx < last ? nx : last, R[d]);
+        const int i = base + d;          // tile whose PV runs now
+        const int dn = (d + 1) % kDepth;  // slot of tile i + 1
+        f32x16 Sn;
+        const bool sl = qk_tile(i + 1, R[dn], (i + 1) & 1, Sn);
+        u32x4 pbn[2];
+        softmax_tile(i + 1, Sn, sl, (i + 1) & 1, pbn);
+        pv_tile(i & 1, pb);
+        pb[0] = pbn[0];
+        pb[1] = pbn[1];
+        load_tile(i + 4 < last ? i + 4 : last, R[dn]);
       }
     }
   }
@@ -642,11 +673,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 }
 
 // FP32 LSE merge of a group's items (slab_attention.py:341-356 applied in
-// sequence; empty parts contribute nothing).  Workgroup (group, chunk): 256 threads,
-// one 16-byte partial vector (register order: block b, quad q, lane) each; the
-// per-row max and sum over the items are reduced in LDS first.
+// sequence; empty parts contribute nothing).  One wave per (group, 64-vector chunk
+// of the register-order partial): lane l owns partial vector chunk * 64 + l, i.e.
+// row l % 32, four d values.  Online merge over batches of kBatch items whose
+// partial vectors and LSEs are loaded together.
+constexpr int kBatch = 16;
+
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams P) {
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams P) {
   using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
   const int32_t* grp = A.groups + (int64_t)blockIdx.x * 4;
@@ -654,80 +688,55 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams P) {
   const int a = A.query_start_loc[req];
   const int nq = A.query_start_loc[req + 1] - a;
   const int G = P.group;
-  const int nrows = nq * G;
-  const int tid = threadIdx.x;
-  __shared__ float s_part[2][8][32];
-  __shared__ float s_M[32], s_L[32];
-  __shared__ int s_nan[32];
-  // per-row statistics: thread (row = tid & 31, subset = tid >> 5) over items subset, +8, ...
-  {
-    const int row = tid & 31, sub = tid >> 5;
-    float mx = -INFINITY;
-    int bad = 0;
-    for (int i = sub; i < ni; i += 8) {
-      const float l = P.part_lse[(int64_t)(i0 + i) * 32 + row];
-      if (l != l) bad = 1;
-      else mx = fmaxf(mx, l);
-    }
-    s_part[0][sub][row] = mx;
-    s_part[1][sub][row] = (float)bad;
-    __syncthreads();
-    if (tid < 32) {
-      float M = -INFINITY, nanf = 0.f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) { M = fmaxf(M, s_part[0][s][tid]); nanf = fmaxf(nanf, s_part[1][s][tid]); }
-      s_M[tid] = M;
-      s_nan[tid] = nanf != 0.f;
-    }
-    __syncthreads();
-    const float M = s_M[row];
-    float sum = 0.f;
-    if (M != -INFINITY)
-      for (int i = sub; i < ni; i += 8) {
-        const float l = P.part_lse[(int64_t)(i0 + i) * 32 + row];
-        if (l != -INFINITY) sum += expf(l - M);
-      }
-    s_part[0][sub][row] = sum;
-    __syncthreads();
-    if (tid < 32) {
-      float L = 0.f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) L += s_part[0][s][tid];
-      s_L[tid] = L;
-    }
-    __syncthreads();
-  }
-  const int e = blockIdx.y * kThreads + tid;  // f32x4 index in the partial
-  const int ln = e & 63, n = ln & 31, gg = ln >> 5, bq = e >> 6, b = bq >> 2, q = bq & 3;
-  if (n >= nrows) return;
-  const float M = s_M[n], L = s_L[n];
-  const bool nan = s_nan[n] != 0;
+  const int lane = threadIdx.x;
+  const int n = lane & 31, gg = lane >> 5;
+  const int bq = blockIdx.y, b = bq >> 2, q = bq & 3;
+  const int e = bq * 64 + lane;  // f32x4 index in the partial
+  const bool row_ok = n < nq * G;
+  const f32x4* po = (const f32x4*)P.part_o + (int64_t)i0 * C::NV + e;
+  const float* pl = P.part_lse + (int64_t)i0 * 32 + n;
+  float M = -INFINITY, L = 0.f;
+  bool nan = false;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < ni; i += kBatch) {
+    float l[kBatch];
+    f32x4 x[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool in = i + u < ni;
+      l[u] = in ? pl[(int64_t)(i + u) * 32] : -INFINITY;
+      x[u] = (in && row_ok) ? po[(int64_t)(i + u) * C::NV] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      nan |= l[u] != l[u];
+      mb = fmaxf(mb, l[u]);
+    }
+    const float Mn = fmaxf(M, mb);
+    if (Mn != -INFINITY) {
+      const float f = (M == -INFINITY) ? 0.f : expf(M - Mn);
+      acc *= f;
+      L *= f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float w = (l[u] == -INFINITY) ? 0.f : expf(l[u] - Mn);
+        L += w;
+        acc += (w > 0.f) ? x[u] * w : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      M = Mn;
+    }
+  }
+  if (!row_ok) return;
   float lse = -INFINITY;
   if (nan) {
     acc = f32x4{NAN, NAN, NAN, NAN};
     lse = NAN;
   } else if (M != -INFINITY && L > 0.f) {
-    const float invL = 1.f / L;
-    const f32x4* po = (const f32x4*)P.part_o + (int64_t)i0 * C::NV + e;
-    int i = 0;
-    for (; i + 4 <= ni; i += 4) {
-      f32x4 x[4];
-      float l[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        x[u] = po[(int64_t)(i + u) * C::NV];
-        l[u] = P.part_lse[(int64_t)(i0 + i + u) * 32 + n];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (l[u] != -INFINITY) acc += x[u] * (expf(l[u] - M) * invL);
-    }
-    for (; i < ni; ++i) {
-      const float l = P.part_lse[(int64_t)(i0 + i) * 32 + n];
-      if (l != -INFINITY) acc += po[(int64_t)i * C::NV] * (expf(l - M) * invL);
-    }
+    acc *= 1.f / L;
     lse = M + logf(L);
+  } else {
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const int tok = a + n / G, head = kvh * G + n % G;
   float* orow = A.out_rot + ((int64_t)tok * A.num_q_heads + head) * D;
@@ -743,7 +752,7 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
     OSCAR_CHECK_LAUNCH("attn_main_kernel");
   }
   if (p.a.phases != 1) {
-    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / kThreads), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / 64), dim3(64), 0, s, p);
     OSCAR_CHECK_LAUNCH("attn_merge_kernel");
   }
   return 0;

@@ -1,15 +1,16 @@
 // Dense D x D rotation y = x @ R (or x @ R^T) for gfx950.
 //
 // Replaces the fp32 matmuls of oscar_ascend/backend.py:371 (q @ R_k) and :382
-// (out_rot @ R_v^T).  One wave computes a 32 x 32 output tile with
+// (out_rot @ R_v^T).  A workgroup of four waves computes a 32 x 32 output tile with
 // v_mfma_f32_32x32x16_bf16 over a three-term split of both operands
 // (x_hi R_hi + x_lo R_hi + x_hi R_lo, hi = bf16(v), lo = bf16(v - hi)), which keeps
-// the product error below 2^-16 of |x||R| with fp32 accumulation; the result is
-// rounded once to the output dtype.
+// the product error below 2^-16 of |x||R| with fp32 accumulation; each wave takes
+// a quarter of the contraction, the four partial tiles are summed in LDS and the
+// result is rounded once to the output dtype.
 //
 // The input dtype, the output dtype and the transpose flag are template
 // parameters, so the operand loads of all K-steps are plain vector loads with no
-// branch between them and the compiler issues them ahead of the MFMAs.
+// branch between them, issued together ahead of the MFMAs.
 #include "common.h"
 
 namespace oscar {
@@ -35,38 +36,61 @@ __device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
 }
 
 template <int D, int XT, int OT, bool TR>
-__global__ __launch_bounds__(64) void rotate_kernel(oscar_rotate_args_v1 a) {
-  const int lane = threadIdx.x, m = lane & 31, g = lane >> 5;
+__global__ __launch_bounds__(256) void rotate_kernel(oscar_rotate_args_v1 a) {
+  constexpr int KS = D / 16 / 4;  // K-steps per wave
+  const int lane = threadIdx.x & 63, m = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row0 = (int64_t)blockIdx.x * 32;
   const int col0 = blockIdx.y * 32;
   const int64_t row = row0 + m;
   const bool row_ok = row < a.rows;
   const int64_t xrow = (row_ok ? row : row0) * a.x_stride_row;  // row0 < rows always
   const int col = col0 + m;
-  f32x16 acc = {};
+  // all operand loads of this wave's K range first
+  float xv[KS][8], rv[KS][8];
 #pragma unroll
-  for (int k0 = 0; k0 < D; k0 += 16) {
-    const int kk = k0 + 8 * g;
-    float xv[8], rv[8];
-    load8<XT>(a.x, xrow + kk, xv);
-    if (!row_ok) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[e] = 0.f;
-    }
+  for (int s = 0; s < KS; ++s) {
+    const int kk = (wave * KS + s) * 16 + 8 * g;
+    load8<XT>(a.x, xrow + kk, xv[s]);
     // B[k][n]: R[k][col], or R^T[k][col] = R[col][k] (contiguous in k)
     if constexpr (TR) {
-      load8<OSCAR_F32>(a.r, (int64_t)col * D + kk, rv);
+      load8<OSCAR_F32>(a.r, (int64_t)col * D + kk, rv[s]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) rv[e] = a.r[(int64_t)(kk + e) * D + col];
+      for (int e = 0; e < 8; ++e) rv[s][e] = a.r[(int64_t)(kk + e) * D + col];
+    }
+  }
+  f32x16 acc = {};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (!row_ok) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[s][e] = 0.f;
     }
     bf16x8 xh, xl, rh, rl;
-    split8(xv, xh, xl);
-    split8(rv, rh, rl);
+    split8(xv[s], xh, xl);
+    split8(rv[s], rh, rl);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, rh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, rh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, rl, acc, 0, 0, 0);
   }
+  // sum of the four wave tiles (register order), then the store
+  __shared__ f32x4 part[3][4][64];
+  if (wave > 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      part[wave - 1][q][lane] = f32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 v = part[w][q][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[4 * q + j] += v[j];
+    }
   // D[i][j]: lane = j + 32*((i/4)%2), register = (i%4) + 4*(i/8); here i = row, j = col
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -78,8 +102,8 @@ __global__ __launch_bounds__(64) void rotate_kernel(oscar_rotate_args_v1 a) {
 
 template <int D, int XT, int OT>
 void launch_tr(const oscar_rotate_args_v1& a, dim3 grid, hipStream_t s) {
-  if (a.transpose) hipLaunchKernelGGL((rotate_kernel<D, XT, OT, true>), grid, dim3(64), 0, s, a);
-  else hipLaunchKernelGGL((rotate_kernel<D, XT, OT, false>), grid, dim3(64), 0, s, a);
+  if (a.transpose) hipLaunchKernelGGL((rotate_kernel<D, XT, OT, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((rotate_kernel<D, XT, OT, false>), grid, dim3(256), 0, s, a);
 }
 
 template <int D, int XT>

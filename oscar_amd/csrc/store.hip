@@ -73,6 +73,126 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
   }
 }
 
+// Last-writer claims and standalone invalidation for vectors [vec0, vec0 + count)
+// of the K kind (once per token: head 0); block (0, 0) publishes the call's epoch.
+__device__ void record_claims(const StoreParams& p, int64_t vec0, int count, int64_t heads, int64_t nvec) {
+  const oscar_store_args_v1& a = p.a;
+  const int64_t e0 = a.epoch_counter[0];
+  const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[1] = epoch;
+  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    const int64_t vec = vec0 + i;
+    if (vec >= nvec || vec % heads != 0) continue;
+    const int64_t t = vec / heads;
+    const int64_t s = a.slot_mapping[t];
+    if (s < 0 || s >= p.capacity) continue;
+    atomicMax((unsigned long long*)&a.slot_claims[s], (unsigned long long)claim_value(epoch, t));
+    if (a.stage_mode == OSCAR_STAGE_NONE) continue;
+    const int64_t seat = seat_of(s, a.cache.block_size, a.staging.rows);
+    if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
+    else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
+  }
+}
+
+// Small calls (decode steps): 16 vectors x 16 columns per workgroup, the
+// contraction split over the four waves (64-key quarters each, fp64 accumulate),
+// partial sums added in wave order in LDS, so a 32-token step spreads over ~1024
+// waves instead of a few long fp64 chains.
+constexpr int kSV = 16, kSC = 16;
+
+template <int D, int XT>
+__global__ __launch_bounds__(kThreads) void store_rotate_small_kernel(StoreParams p) {
+  const oscar_store_args_v1& a = p.a;
+  const int kind = blockIdx.z;
+  const int64_t heads = (kind == KIND_Q) ? a.num_q_heads : a.cache.num_kv_heads;
+  const int64_t nvec = a.num_tokens * heads;
+  const int64_t vec0 = (int64_t)blockIdx.x * kSV;
+  if (vec0 >= nvec) return;
+  const int col0 = blockIdx.y * kSC;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
+  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
+                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
+  const float* R = (kind == KIND_V) ? a.rv : a.rk;
+  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
+  float* y_out = (kind == KIND_Q) ? nullptr : p.y + (int64_t)kind * a.num_tokens * heads * D;
+
+  __shared__ __attribute__((aligned(16))) float s_r[D][kSC];
+  __shared__ float s_x[D][kSV + 1];
+  __shared__ double s_red[3][4][64];
+  constexpr int RN = D * kSC / 4;   // float4 of R
+  constexpr int XN = kSV * D / 8;   // 8-element x loads
+  constexpr int RI = (RN + kThreads - 1) / kThreads, XI = (XN + kThreads - 1) / kThreads;
+  f32x4 rr[RI];
+  float xv[XI][8];
+#pragma unroll
+  for (int i = 0; i < RI; ++i) {
+    const int e = tid + i * kThreads, k = e / (kSC / 4), c4 = e % (kSC / 4);
+    if (e >= RN) break;
+    if (R != nullptr) {
+      rr[i] = *(const f32x4*)(R + (int64_t)k * D + col0 + 4 * c4);
+    } else {
+      const int c = col0 + 4 * c4 - k;
+      rr[i] = f32x4{c == 0 ? 1.f : 0.f, c == -1 ? 1.f : 0.f, c == -2 ? 1.f : 0.f, c == -3 ? 1.f : 0.f};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
+    if (e >= XN) break;
+    const int64_t vec = vec0 + v < nvec ? vec0 + v : vec0;
+    load8<XT>(src, (vec / heads) * src_stride + (vec % heads) * D + k8, xv[i]);
+    if (vec0 + v >= nvec) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
+    }
+  }
+  if (kind == KIND_K && blockIdx.y == 0) record_claims(p, vec0, kSV, heads, nvec);
+#pragma unroll
+  for (int i = 0; i < RI; ++i) {
+    const int e = tid + i * kThreads, k = e / (kSC / 4), c4 = e % (kSC / 4);
+    if (e < RN) *(f32x4*)&s_r[k][4 * c4] = rr[i];
+  }
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
+    if (e < XN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_x[k8 + j][v] = xv[i][j];
+    }
+  }
+  __syncthreads();
+  // lane -> vector v (16) x column group cg (4 columns); wave -> key quarter
+  const int v = lane >> 2, cg = lane & 3;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  constexpr int KQ = D / 4;
+#pragma unroll 8
+  for (int kk = 0; kk < KQ; ++kk) {
+    const int k = wave * KQ + kk;
+    const f32x4 r4 = *(const f32x4*)&s_r[k][4 * cg];
+    const double x = s_x[k][v];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = fma(x, (double)r4[j], acc[j]);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_red[wave - 1][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += s_red[w][j][lane];
+  const int64_t vec = vec0 + v;
+  if (vec >= nvec) return;
+  const float y[4] = {(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
+  const int64_t base = vec * D + col0 + 4 * cg;
+  if (y_out != nullptr) *(f32x4*)(y_out + base) = f32x4{y[0], y[1], y[2], y[3]};
+  if (rot_out != nullptr) store4<XT>(rot_out, base, y);
+}
+
 template <int D, int TV, int XT>
 __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
   const oscar_store_args_v1& a = p.a;
@@ -121,24 +241,7 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
     }
   }
 
-  // last-writer claims and standalone invalidation, once per token
-  if (kind == KIND_K && blockIdx.y == 0) {
-    const int64_t e0 = a.epoch_counter[0];
-    const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
-    if (blockIdx.x == 0 && tid == 0) a.epoch_counter[1] = epoch;
-    for (int i = tid; i < TV; i += kThreads) {
-      int64_t vec = vec0 + i;
-      if (vec >= nvec || vec % heads != 0) continue;
-      int64_t t = vec / heads;
-      int64_t s = a.slot_mapping[t];
-      if (s < 0 || s >= p.capacity) continue;
-      atomicMax((unsigned long long*)&a.slot_claims[s], (unsigned long long)claim_value(epoch, t));
-      if (a.stage_mode == OSCAR_STAGE_NONE) continue;
-      int64_t seat = seat_of(s, a.cache.block_size, a.staging.rows);
-      if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
-      else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
-    }
-  }
+  if (kind == KIND_K && blockIdx.y == 0) record_claims(p, vec0, TV, heads, nvec);
 
 #pragma unroll
   for (int i = 0; i < RV; ++i) {
@@ -333,9 +436,11 @@ int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_
     dim3 grid((unsigned)((max_vec + 63) / 64), D / kCols, kinds);
     launch_rotate<D, 64>(p, grid, s);
   } else {
-    constexpr int TV = D == 64 ? 32 : 16;  // at least one 8-element load per thread
-    dim3 grid((unsigned)((max_vec + TV - 1) / TV), D / kCols, kinds);
-    launch_rotate<D, TV>(p, grid, s);
+    dim3 grid((unsigned)((max_vec + kSV - 1) / kSV), D / kSC, kinds);
+    dim3 block(kThreads);
+    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_BF16>), grid, block, 0, s, p);
+    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_F16>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_F32>), grid, block, 0, s, p);
   }
   OSCAR_CHECK_LAUNCH("store_rotate_kernel");
   dim3 qgrid((unsigned)((kv_vec + 3) / 4), 2);
