@@ -142,7 +142,16 @@ int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
 
 /* Work planning for the split-K decode (host function, no device access).
  * qsl/seqs are host arrays.  Writes up to max_items work items of
- * OSCAR_WORK_INTS int32 each and returns the item count (or < 0). */
+ * OSCAR_WORK_INTS int32 each and returns the item count (or < 0); with
+ * items == NULL or groups == NULL it only fills *plan (size query).
+ *
+ * Keys of a (request, kv head) group are cut into 32-token tiles.  Body tiles
+ * (before min(history, seq - n_q + 1)) are dealt round-robin to k items; the
+ * remaining tiles (current chunk, causal boundary, ragged end) form one tail
+ * item.  Item record, int32[8]:
+ *   [0] request  [1] kv_head | n_q << 16  [2] first tile  [3] tile stride
+ *   [4] tile count  [5] partial slot  [6] first query token  [7] seq length
+ * Group record, int32[4]: request, kv head, first partial slot, slot count. */
 #define OSCAR_WORK_INTS 8
 typedef struct oscar_plan_v1 {
   int32_t num_items;

@@ -22,15 +22,21 @@ cases      seeded generators for the BASELINE configurations.
 """
 
 PINNING = {
-    "fmt.vector_scales": "closed form (fp16 RNE of min/max, 2^-14 floor); constant-vector KAT",
-    "fmt.quantize": "brute force vs exhaustive threshold table; floor(x+0.5) tie KAT",
-    "fmt.pack/unpack": "exhaustive over all 256 byte values",
-    "fmt.make_slot_bytes": "byte positions KAT (scale/zero LE at 0..7, codes at 32/96)",
-    "store.rotate": "R=I exactness; Hadamard closed form vs fp64; order independence",
-    "store.clip": "k-th order statistic KAT",
-    "store.store_ref": "negative-slot no-op, last-writer-wins KATs, R=I round trip",
-    "store.staging_write_ref": "reference lifecycle KATs (persist, recycle, collision, padding)",
-    "attention.attention_ref": "fp64 brute-force softmax; closed forms 3.0, 45/8, 75/9, -3, -4",
-    "attention.merge_ref": "edge cases: -inf parts, LSE +-1000, NaN propagation",
-    "backend.forward_ref": "SDPA equality without history; rotation invariance",
+    "fmt.pack/unpack": "exhaustive over all 256 byte values; hand-derived bytes (test_oracle_format)",
+    "fmt.quantize": "floor(x+0.5) tie KAT, fp16-scale-before-coding KAT, float64 nearest-level "
+                    "brute force, constant-vector KATs of tests/test_backend.py:139-146",
+    "fmt.make_slot_bytes": "hand-derived 160-byte slot (scale/zero LE at 0..7, codes at 32/96)",
+    "fmt.bf16_round": "bit-equal to torch's bfloat16 conversion incl. ties, subnormals, inf",
+    "store.rotate": "bit-equal to exact rational dot products rounded once; R=I; Hadamard rows",
+    "store.clip": "order-statistic KATs; tests/test_numeric.py:354-367 bound",
+    "store.store_ref": "negative-slot no-op (tests/test_backend.py:56-75), split bytes == logical "
+                       "slot (tests/test_numeric.py:82-103), last writer wins",
+    "store.Staging": "reference lifecycle KATs: geometry, persist/recycle, collision + padding, "
+                     "standalone invalidation; staging_order at the 2^24 boundary",
+    "attention.attention_ref": "closed forms 3.0, 45/8, 75/9, -3, -4, all-ones of "
+                               "tests/test_streaming_backend.py; float64 SDPA over independently "
+                               "decoded history; empty rows; NaN propagation",
+    "attention.merge_ref": "hand-derived edge cases (-inf parts, LSE +-1000, NaN); split-softmax identity",
+    "attention.causal_prefill_ref": "float64 SDPA with GQA",
+    "backend.forward": "fresh prefill == SDPA; rotated path == original-domain attention",
 }

@@ -22,9 +22,8 @@ from .store import dequant_split_ref
 
 
 def round_history(x, q_dtype: str) -> np.ndarray:
-    """streaming_attention.py:124: ``x.half().to(dtype)``."""
-    x = fmt.f16_round(x)
-    return fmt.bf16_round(x) if q_dtype == "bf16" else x
+    """streaming_attention.py:124: ``x.half().to(dtype)`` (fp16 first, whatever q_dtype)."""
+    return fmt.round_to(fmt.f16_round(x), q_dtype)
 
 
 def read_history(k8, v8, bt_row, start: int, end: int, hk: int, d: int, stage, q_dtype: str):
@@ -129,5 +128,4 @@ def causal_prefill_ref(q, k, v, scale, *, q_dtype="bf16"):
         m = s.max(-1, keepdims=True)
         p = np.exp(s - m)
         out[:, h] = (p @ v[:, h // group]) / p.sum(-1, keepdims=True)
-    out = out.astype(np.float32)
-    return fmt.bf16_round(out) if q_dtype == "bf16" else fmt.f16_round(out)
+    return fmt.round_to(out.astype(np.float32), q_dtype)

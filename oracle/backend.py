@@ -79,7 +79,9 @@ def forward(layer: OracleLayer, query, key, value, slot_mapping, qsl, seqs, bloc
     query [N, Hq, D], key/value [N, Hk, D] or None; all on the q_dtype grid.
     Returns the output [N, Hq, D] on the q_dtype grid (float32 array).
     """
-    rnd = fmt.bf16_round if q_dtype == "bf16" else fmt.f16_round
+    def rnd(x):
+        return fmt.round_to(x, q_dtype)
+
     query = np.asarray(query, np.float32)
     n_tok = query.shape[0]
     actual_md = n_tok if num_actual_tokens is None else num_actual_tokens

@@ -49,6 +49,17 @@ def f16_round(x) -> np.ndarray:
     return f32(x).astype(np.float16).astype(np.float32)
 
 
+def round_to(x, q_dtype: str) -> np.ndarray:
+    """Round float32 values to the grid of the query dtype ("bf16", "f16" or "f32")."""
+    if q_dtype == "bf16":
+        return bf16_round(x)
+    if q_dtype == "f16":
+        return f16_round(x)
+    if q_dtype == "f32":
+        return f32(x)
+    raise ValueError(f"unknown q_dtype {q_dtype!r}")
+
+
 def bf16_bits(x) -> np.ndarray:
     """bfloat16 bit patterns (uint16) of float32 values already on the bf16 grid."""
     return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)

@@ -6,10 +6,11 @@ num_kv_heads, slot_bytes]`` exactly as the reference addresses them through
 
 Rotation.  The reference computes ``x.float() @ R`` with torch's CPU sgemm
 (backend.py:131, :554), whose last bits depend on the BLAS blocking.  The
-oracle pins the mathematically canonical value instead: the exact dot
-product rounded once to float32 (products of bf16 x fp32 are exact in fp64;
-the fp64 sum is rounded to fp32).  ``rotate_f32gemm`` reproduces the
-reference's own op for comparisons.
+oracle pins the mathematically canonical value instead: the dot product
+evaluated in float64 (products of two float32 values are exact there) and
+rounded once to float32, which equals the correctly rounded result unless
+the exact sum lies within ~2^-45 (relative) of a float32 rounding boundary.
+``rotate_f32gemm`` reproduces the reference's own op for comparisons.
 """
 from __future__ import annotations
 

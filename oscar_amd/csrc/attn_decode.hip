@@ -40,6 +40,8 @@
 //    (loaded in batched rounds) and the current chunk (copied to LDS once per
 //    workgroup); V goes through LDS and is read transposed with ds_read_b64_tr_b16;
 //    P is split into bf16 hi + lo parts.
+#include <vector>
+
 #include "common.h"
 
 namespace oscar {
@@ -792,8 +794,9 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
     if (seqs[r] < 0 || (has_new && seqs[r] < nq))
       return fail(-22, "oscar_attn_plan_v1: sequence length must cover its query chunk");
     ngroups += num_kv_heads;
+    if (ngroups > (1 << 24)) return fail(-22, "oscar_attn_plan_v1: too many request x kv-head groups");
   }
-  Grp* gl = (Grp*)alloca(sizeof(Grp) * (ngroups > 0 ? ngroups : 1));
+  std::vector<Grp> gl((size_t)(ngroups > 0 ? ngroups : 1));
   int gi = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];

@@ -1,0 +1,179 @@
+"""The C-ABI boundary on the CPU: exports, struct layout, host planner, argument checks.
+
+Nothing here launches a kernel: the library is loaded and only its host-side
+functions (planner, size queries, argument validation) are called.
+"""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oscar_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "oscar_amd.h"
+TILE = 32
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from oscar_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def header_functions() -> set:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(oscar_[a-z_0-9]+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_header_symbol(lib):
+    names = header_functions()
+    assert len(names) == 8, names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert names == set(_lib.SIGNATURES)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T oscar_" in line}
+    assert exported == names  # nothing undeclared leaks out
+    assert lib.oscar_abi_version() == int(re.search(r"OSCAR_ABI_VERSION (\d+)", HEADER.read_text())[1])
+
+
+STRUCTS = {
+    "oscar_cache_v1": _lib.Cache, "oscar_staging_v1": _lib.Staging,
+    "oscar_store_args_v1": _lib.StoreArgs, "oscar_rotate_args_v1": _lib.RotateArgs,
+    "oscar_plan_v1": _lib.Plan, "oscar_attn_args_v1": _lib.AttnArgs,
+    "oscar_prefill_args_v1": _lib.PrefillArgs,
+}
+
+
+def test_ctypes_structs_match_c_layout(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, py in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["return 0; }"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        s, f, v = line.split()
+        got[(s, f)] = int(v)
+    for cname, py in STRUCTS.items():
+        assert got[(cname, "size")] == C.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
+
+
+# ------------------------------------------------------------------ planner
+def plan(lib, qsl, seqs, has_new=True, hk=1, group=6, d=256, chunk=8192, target=256):
+    n = len(seqs)
+    qa = (C.c_int32 * (n + 1))(*qsl)
+    sa = (C.c_int32 * max(n, 1))(*seqs)
+    p = _lib.Plan()
+    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, None, 0, None, 0,
+                                 C.byref(p))
+    if cnt < 0:
+        return cnt, None, None, p
+    items = (C.c_int32 * max(p.num_items * 8, 1))()
+    groups = (C.c_int32 * max(p.num_groups * 4, 1))()
+    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, items, p.num_items,
+                                 groups, p.num_groups, C.byref(p))
+    assert cnt == p.num_items
+    it = np.array(list(items)[:p.num_items * 8], np.int64).reshape(-1, 8)
+    gr = np.array(list(groups)[:p.num_groups * 4], np.int64).reshape(-1, 4)
+    return cnt, it, gr, p
+
+
+PLAN_CASES = [
+    ([0, 4, 7, 8, 10], [133, 1028, 4, 302], True, 1, 6),      # MTP, mixed lengths
+    ([0] + [4 * i for i in range(1, 9)], [24580] * 8, True, 1, 6),
+    ([0, 1, 1, 5, 10], [0, 257, 3, 263], False, 1, 6),        # cache-only, empty request
+    ([0, 4, 6], [1025, 702], True, 2, 4),
+    ([0] + list(range(1, 65)), [2048 + 37 * i for i in range(64)], False, 1, 6),
+]
+
+
+@pytest.mark.parametrize("qsl,seqs,has_new,hk,group", PLAN_CASES)
+def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, has_new, hk, group):
+    cnt, items, groups, p = plan(lib, qsl, seqs, has_new, hk, group)
+    assert cnt > 0
+    assert sorted(items[:, 5].tolist()) == list(range(cnt))          # partial slots: a permutation
+    assert p.partial_bytes == cnt * 32 * (256 + 1) * 4
+    seen_body = False
+    for it in items:
+        req, kvh, nq, first, stride, count, part, qa, seq = (it[0], it[1] & 0xFFFF, it[1] >> 16, *it[2:8])
+        hist = seq - nq if has_new else seq
+        assert nq == qsl[req + 1] - qsl[req] and qa == qsl[req] and seq == seqs[req]
+        assert 0 <= kvh < hk and nq * group <= 32
+        assert 1 <= count <= 8192 // TILE and stride >= 1
+        assert (first + stride * (count - 1)) * TILE < seq               # no tile past the end
+        body = min(hist, seq - nq + 1) // TILE
+        is_tail = first >= body
+        if is_tail:
+            assert not seen_body  # tail items (the slow work) are launched first
+            assert stride == 1 and first == body
+        else:
+            seen_body = True
+            assert first + stride * (count - 1) < body
+    # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous
+    for req, kvh, first_slot, nslots in groups:
+        rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh)]
+        assert sorted(rows[:, 5].tolist()) == list(range(first_slot, first_slot + nslots))
+        cover = np.zeros((seqs[req] + TILE - 1) // TILE, np.int64)
+        for it in rows:
+            np.add.at(cover, it[2] + it[3] * np.arange(it[4]), 1)
+        assert (cover == 1).all()
+    assert len(groups) == hk * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+
+
+def test_plan_splits_long_history_across_items(lib):
+    _, items, _, _ = plan(lib, [0, 4], [100003], target=256)
+    body = items[items[:, 4] > 0]
+    assert len(items) > 64 and body[:, 4].max() * TILE <= 8192
+
+
+def test_plan_rejects_bad_requests(lib):
+    cnt, *_ = plan(lib, [0, 6], [100], group=6)             # 36 rows > 32
+    assert cnt == -22 and b"rows" in lib.oscar_last_error()
+    cnt, *_ = plan(lib, [0, 4], [3], has_new=True)          # sequence shorter than its chunk
+    assert cnt == -22
+    cnt, *_ = plan(lib, [0, 1], [10], d=96)
+    assert cnt == -22 and b"head_dim" in lib.oscar_last_error()
+    qa, sa = (C.c_int32 * 2)(0, 1), (C.c_int32 * 1)(100)
+    p = _lib.Plan()
+    small = (C.c_int32 * 8)()
+    assert lib.oscar_attn_plan_v1(qa, sa, 1, 1, 1, 6, 256, 32, 64, small, 1, small, 2, C.byref(p)) == -28
+
+
+def test_empty_plan(lib):
+    cnt, items, groups, p = plan(lib, [0, 0, 0], [5, 7])
+    assert cnt == 0 and p.num_groups == 0 and p.partial_bytes == 0
+
+
+# ------------------------------------------------------------------ argument checks
+def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(lib):
+    assert lib.oscar_store_v1(None, None) == -22
+    assert b"null" in lib.oscar_last_error()
+    assert lib.oscar_rotate_v1(None, None) == -22
+    assert lib.oscar_attn_decode_v1(None, None) == -22
+    assert lib.oscar_attn_prefill_v1(None, None) == -22
+    r = _lib.RotateArgs(rows=4, head_dim=96, x=1, r=1, out=1)
+    assert lib.oscar_rotate_v1(C.byref(r), None) == -22 and b"head_dim" in lib.oscar_last_error()
+    r = _lib.RotateArgs(rows=0)
+    assert lib.oscar_rotate_v1(C.byref(r), None) == 0  # nothing to do
+    s = _lib.StoreArgs(num_tokens=3)
+    s.cache.head_dim = 200
+    assert lib.oscar_store_v1(C.byref(s), None) == -22
+    s = _lib.StoreArgs(num_tokens=0)
+    assert lib.oscar_store_v1(C.byref(s), None) == 0
+    assert lib.oscar_store_workspace_bytes_v1(10, 2, 256) == 2 * 10 * 2 * 256 * 4

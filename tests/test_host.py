@@ -1,0 +1,181 @@
+"""Host-side mirror of the reference plugin/impl on the CPU (no kernel launches).
+
+Restates the reference's host tests for this path: metadata accessors
+(tests/test_backend.py:112-120), class-surgery rollback (:141-157), rotation
+loading (:243-251, tests/test_numeric.py:160-183 and :274-296), MTP/hybrid
+routing (tests/test_numeric.py:218-246 and :369-379), configuration defaults
+(tests/test_streaming_backend.py:188-197) and cache geometry checks.
+"""
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from oscar_amd import plugin, rotation
+from oscar_amd.backend import OscarAttentionBackendImpl, metadata_batch_lists
+from oscar_amd.config import OscarConfig
+
+
+def meta(slots, ends, seqs):
+    return NS(num_actual_tokens=len(slots), slot_mapping=torch.tensor(slots),
+              query_start_loc=torch.tensor([0] + ends), actual_seq_lengths_q=ends,
+              seq_lens=torch.tensor(seqs), seq_lens_cpu=torch.tensor(seqs), seq_lens_list=seqs)
+
+
+def test_host_metadata_does_not_read_device_query_starts():
+    class NoRead:
+        def tolist(self):
+            raise AssertionError("unexpected device sync")
+
+    md = meta([0, 1], [1, 2], [9, 12])
+    md.query_start_loc = NoRead()
+    assert metadata_batch_lists(md) == ([0, 1, 2], [9, 12])
+    md2 = NS(query_start_loc_cpu=torch.tensor([0, 3]), seq_lens=NoRead(), seq_lens_list=[7])
+    assert metadata_batch_lists(md2) == ([0, 3], [7])
+
+
+def test_failed_surgery_restores_class_and_state():
+    class Original:
+        pass
+
+    class Broken(Original):
+        def _oscar_setup(self):
+            self.partial = True
+            raise ValueError("unsupported")
+
+    impl = Original()
+    impl.keep = 123
+    with pytest.raises(ValueError):
+        plugin.install_impl(impl, Broken)
+    assert type(impl) is Original and vars(impl) == {"keep": 123}
+
+
+def test_config_defaults_and_validation(monkeypatch):
+    for name in ("OSCAR_ASCEND_ATTENTION_MODE", "OSCAR_ASCEND_SINK_TOKENS", "OSCAR_ASCEND_GROUP_SIZE",
+                 "OSCAR_ASCEND_K_CLIP_RATIO", "OSCAR_ASCEND_STAGING_TOKENS"):
+        monkeypatch.delenv(name, raising=False)
+    cfg = OscarConfig.from_env(head_dim=256)
+    assert cfg.attention_mode == "streaming" and cfg.window_enabled
+    assert (cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens) == (64, 256, 8192)
+    assert cfg.slot_bytes == 160 and cfg.data_bytes == 64
+    monkeypatch.setenv("OSCAR_ASCEND_STAGING_TOKENS", "0")
+    assert not OscarConfig.from_env(head_dim=256).window_enabled
+    monkeypatch.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "1.5")
+    with pytest.raises(ValueError, match="clip"):
+        OscarConfig.from_env(head_dim=256)
+    monkeypatch.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "0")
+    monkeypatch.setenv("OSCAR_ASCEND_GROUP_SIZE", "32")
+    with pytest.raises(ValueError, match="per-vector"):
+        OscarConfig.from_env(head_dim=256)
+    monkeypatch.setenv("OSCAR_ASCEND_GROUP_SIZE", "0")
+    monkeypatch.setenv("OSCAR_ASCEND_ATTENTION_MODE", "bogus")
+    with pytest.raises(ValueError):
+        OscarConfig.from_env(head_dim=256)
+
+
+def test_missing_rotation_layer_rejected_when_strict(tmp_path):
+    path = tmp_path / "rotation.pt"
+    torch.save({"layers": {"1": {"rotation": torch.eye(64)}}}, path)
+    with pytest.raises(ValueError, match="missing layer"):
+        rotation.get_layer_rotation(str(path), "model.layers.0.self_attn.attn", 64, "cpu", strict=True)
+    r = rotation.get_layer_rotation(str(path), "model.layers.0.self_attn.attn", 64, "cpu")
+    assert torch.equal(r, torch.eye(64))
+
+
+def test_rotation_checkpoint_layouts(tmp_path):
+    q = torch.linalg.qr(torch.randn(64, 64, dtype=torch.float64))[0].float()
+    qv = torch.linalg.qr(torch.randn(64, 64, dtype=torch.float64))[0].float()
+    layouts = {
+        "nested": {"layers": {"model.layers.3.self_attn": {"rotation": q, "rotation_v": qv}}},
+        "flat": {3: q},
+        "names": {"model.layers.3.attn": q},
+        "stacked": torch.stack([torch.eye(64)] * 3 + [q]),
+    }
+    for name, obj in layouts.items():
+        path = tmp_path / f"{name}.pt"
+        torch.save(obj, path)
+        rk = rotation.get_layer_rotation(str(path), "model.layers.3.self_attn.attn", 64, "cpu",
+                                         mode="k", strict=True)
+        assert torch.equal(rk, q), name
+        rv = rotation.get_layer_rotation(str(path), "model.layers.3.self_attn.attn", 64, "cpu",
+                                         mode="v", strict=True)
+        assert torch.equal(rv, qv if name == "nested" else q), name
+    bad = tmp_path / "bad.pt"
+    torch.save({3: torch.ones(64, 64)}, bad)
+    with pytest.raises(ValueError, match="orthogonal"):
+        rotation.get_layer_rotation(str(bad), "model.layers.3.attn", 64, "cpu", strict=True)
+    torch.save({3: torch.eye(32)}, bad)
+    rotation._load_checkpoint.cache_clear()
+    with pytest.raises(ValueError, match="shape"):
+        rotation.get_layer_rotation(str(bad), "model.layers.3.attn", 64, "cpu")
+
+
+def test_layer_index_parsing():
+    assert rotation.layer_index_from_name("model.layers.11.self_attn.attn") == 11
+    assert rotation.layer_index_from_name("blocks_7") == 7
+    assert rotation.layer_index_from_name("attn") is None
+
+
+def test_should_oscar_routes_only_full_decoder_layers_of_hybrid_models():
+    hybrid = NS(is_hybrid=False, hf_text_config=NS(layer_types=["linear_attention", "full_attention"]))
+    dense = NS(is_hybrid=False, hf_text_config=NS(layer_types=["attention", "attention"]))
+    assert plugin._is_hybrid_config(hybrid) and not plugin._is_hybrid_config(dense)
+    assert plugin._is_hybrid_config(NS(is_hybrid=True))
+    impl = NS(attn_type="decoder", sliding_window=None, sinks=None)
+    full = NS(layer_name="model.layers.3.self_attn.attn")
+    assert plugin._should_oscar(full, impl, hybrid)
+    assert not plugin._should_oscar(NS(layer_name="model.mtp.layers.0.self_attn.attn"), impl, hybrid)
+    assert not plugin._should_oscar(full, impl, dense)
+    assert not plugin._should_oscar(full, NS(attn_type=NS(value="encoder"), sliding_window=None,
+                                             sinks=None), hybrid)
+    assert not plugin._should_oscar(full, NS(attn_type="decoder", sliding_window=128, sinks=None), hybrid)
+
+
+def make_impl(d=256, hq=6, hk=1):
+    impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
+    impl.head_size, impl.num_heads, impl.num_kv_heads, impl.scale = d, hq, hk, d ** -0.5
+    impl.key_cache = impl.value_cache = None
+    impl._oscar_setup()
+    return impl
+
+
+def test_cache_geometry_checks():
+    impl = make_impl()
+    impl._set_caches([torch.zeros(4, 128, 1, 256, dtype=torch.int8)] * 2)    # packed
+    impl = make_impl()
+    impl._set_caches([torch.zeros(4, 128, 1, 256, dtype=torch.bfloat16)] * 2)  # legacy width
+    impl = make_impl()
+    with pytest.raises(AssertionError, match="slot width"):
+        impl._set_caches([torch.zeros(4, 128, 1, 200, dtype=torch.int8)] * 2)
+    impl = make_impl()
+    with pytest.raises(ValueError):
+        impl._set_caches(None)
+    with pytest.raises(ValueError, match="divisible"):
+        make_impl(hq=6, hk=4)
+
+
+def test_staging_arena_geometry_matches_reference_sizing():
+    impl = make_impl()
+    impl._oscar.sink_tokens, impl._oscar.recent_tokens, impl._oscar.staging_tokens = 64, 256, 8192
+    layer = NS()
+    cache = [torch.zeros(8, 128, 1, 256, dtype=torch.int8)] * 2
+    impl._ensure_staging(layer, cache)
+    assert layer._oscar_stage_rows == 64 and impl.sink_eff == 0
+    assert layer._oscar_stage_k.shape == (64, 128, 1, 256)
+    assert (layer._oscar_slot_owner == -1).all()
+    addr = layer._oscar_stage_k.data_ptr()
+    impl._ensure_staging(layer, cache)
+    assert layer._oscar_stage_k.data_ptr() == addr  # allocated once per layer
+
+
+def test_forward_requires_output_and_paired_kv():
+    impl = make_impl()
+    cache = [torch.zeros(4, 128, 1, 256, dtype=torch.int8)] * 2
+    q = torch.zeros(1, 6 * 256, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        impl.forward(NS(), q, None, None, cache, meta([0], [1], [1]), output=None)
+    out = torch.ones(1, 6 * 256, dtype=torch.bfloat16)
+    assert (impl.forward(NS(), q, None, None, cache, None, output=out) == 0).all()
+    with pytest.raises(ValueError, match="together"):
+        impl.forward(NS(), q, torch.zeros(1, 256, dtype=torch.bfloat16), None, cache,
+                     meta([0], [1], [1]), output=out)
