@@ -151,8 +151,10 @@ int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
  * item.  Item record, int32[8]:
  *   [0] request  [1] kv_head | n_q << 16  [2] first tile  [3] tile stride
  *   [4] tile count  [5] partial slot  [6] first query token  [7] seq length
- * Group record, int32[4]: request, kv head, first partial slot, slot count. */
+ * Group record, int32[OSCAR_GROUP_INTS]: request, kv head, first partial slot,
+ * slot count, first query token, query count, 0, 0. */
 #define OSCAR_WORK_INTS 8
+#define OSCAR_GROUP_INTS 8
 typedef struct oscar_plan_v1 {
   int32_t num_items;
   int32_t num_groups;           /* request x kv-head groups with queries */

@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "liboscar_amd.so"
 OSCAR_F32, OSCAR_F16, OSCAR_BF16 = 0, 1, 2
 STAGE_NONE, STAGE_INVALIDATE, STAGE_WRITE = 0, 1, 2
 WORK_INTS = 8
+GROUP_INTS = 8
 
 vp = C.c_void_p
 i32, i64, f32 = C.c_int32, C.c_int64, C.c_float

@@ -48,10 +48,10 @@ namespace oscar {
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;            // two waves per SIMD
 constexpr int kThreads = kWaves * 64;
+constexpr int kSlowWaves = 4;        // waves that run the queued slow tiles
 constexpr int kTile = 32;
-constexpr int kDepth = 3;            // tiles of packed data in flight per wave
 constexpr int kMaxCur = 32;          // current-chunk tokens of a request (rows <= 32)
 constexpr int kMaxItemTokens = 8192; // keys per item (64 tiles per wave)
 constexpr int kMaxPages = kMaxItemTokens / kTile + 2;
@@ -71,7 +71,7 @@ struct Cfg {
   static constexpr int NB = D / 4;       // code bytes per token
   static constexpr int MBLK = D / 32;    // PV output blocks (32 d each)
   static constexpr int VROW = D + 8;     // bf16 per row of the slow-tile V buffer
-  static constexpr int CPR = 2;          // chunks per staged-row load round
+  static constexpr int CPR = 1;          // chunks per staged-row load round
   static constexpr int NV = MBLK * 4 * 64;  // f32x4 of one item partial (register order)
 };
 
@@ -155,6 +155,43 @@ __device__ __forceinline__ void table_pairs(unsigned w, unsigned lo, unsigned hi
   }
 }
 
+// bf16 pairs of 16 elements (lo = e0..e7, hi = e8..e15) in the K-step order of lut16:
+// (e0,e4) (e1,e5) (e2,e6) (e3,e7) | (e8,e12) (e9,e13) (e10,e14) (e11,e15)
+__device__ __forceinline__ void kpairs16(const u32x4& lo, const u32x4& hi, unsigned o[8]) {
+  o[0] = __builtin_amdgcn_perm(lo[2], lo[0], 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(lo[2], lo[0], 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(lo[3], lo[1], 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(lo[3], lo[1], 0x07060302u);
+  o[4] = __builtin_amdgcn_perm(hi[2], hi[0], 0x05040100u);
+  o[5] = __builtin_amdgcn_perm(hi[2], hi[0], 0x07060302u);
+  o[6] = __builtin_amdgcn_perm(hi[3], hi[1], 0x05040100u);
+  o[7] = __builtin_amdgcn_perm(hi[3], hi[1], 0x07060302u);
+}
+
+// the four history values of a token as byte tables: t_lo = low bytes of the bf16
+// values for codes 0..3, t_hi = their high bytes
+__device__ __forceinline__ void byte_tables(unsigned scale_zero, unsigned& t_lo, unsigned& t_hi) {
+  unsigned lo, hi;
+  value_table(scale_zero, lo, hi);
+  t_lo = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
+  t_hi = __builtin_amdgcn_perm(hi, lo, 0x07050301u);
+}
+
+// bf16 values of the 16 codes of one code dword (byte j holds elements 4j..4j+3 at
+// bits 2k), in the pair order of kpairs16.  Per k: the four codes 4j + k as bytes
+// select table bytes directly (v_perm_b32 selectors 0..3), one perm each for the low
+// and high bytes, then two perms interleave them into bf16 pairs: 23 VALU per dword.
+__device__ __forceinline__ void lut16(unsigned w, unsigned t_lo, unsigned t_hi, unsigned o[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const unsigned x = (w >> (2 * k)) & 0x03030303u;
+    const unsigned lo = __builtin_amdgcn_perm(t_hi, t_lo, x);
+    const unsigned hi = __builtin_amdgcn_perm(t_lo, t_hi, x);
+    o[k] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // (e_k, e_4+k)
+    o[4 + k] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // (e_8+k, e_12+k)
+  }
+}
+
 template <int D>
 struct TileRegs {
   u32x4 k[Cfg<D>::NQ];  // this lane's half of the K codes
@@ -200,31 +237,90 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // LDS
   __shared__ int32_t s_blk[kMaxPages];                 // block ids of the item's pages
   __shared__ int32_t s_seat[kMaxPages];                // their seat-row base (blk % rows) * bs
-  __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][2][kTile * C::NB];  // double buffer
-  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][2][kTile];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][kTile * C::NB];
+  __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][kTile];
   __shared__ __attribute__((aligned(16))) float s_ml[kWaves][2][32];
   __shared__ __attribute__((aligned(16))) uint16_t s_cur[2][kMaxCur][D];  // current K / V
   __shared__ __attribute__((aligned(16))) u32x4 s_q[C::KSTEPS][64];        // Q^T operand
-  // union: slow-tile V values (bf16, permuted columns) / cross-wave merge buffers
-  constexpr int kMergeBytes = 2 * C::NV * 16, kSlowBytes = kWaves * kTile * C::VROW * 2;
+  __shared__ int32_t s_nslow[kWaves];
+  __shared__ int16_t s_slow[kMaxItemTokens / kTile];   // queued slow tiles of all waves
+  // union: slow-tile V values (bf16, permuted columns) / cross-wave merge rounds
+  constexpr int kMergeBytes = kWaves * 2 * 4 * 64 * 16, kSlowBytes = kSlowWaves * kTile * C::VROW * 2;
   __shared__ __attribute__((aligned(16))) uint8_t s_big[kMergeBytes > kSlowBytes ? kMergeBytes : kSlowBytes];
-  uint16_t* s_slowv = (uint16_t*)s_big + wave * (kTile * C::VROW);
   const unsigned st_rows = (unsigned)P.st.rows;
 
-  // ---- prologue: page of every item tile, current chunk and queries, loaded together
-  bool any_cur_tile = false;
-  for (int j = tid; j < count; j += kThreads) {
+  // wave w takes item tiles j = w + kWaves * i, i < my (my <= 32)
+  const int my = count > wave ? (count - 1 - wave) / kWaves + 1 : 0;
+  const uint8_t* kbase = A.cache.k + (int64_t)kvh * A.cache.k_stride[2];
+  const uint8_t* vbase = A.cache.v + (int64_t)kvh * A.cache.v_stride[2];
+  const int64_t ks0 = A.cache.k_stride[0], ks1 = A.cache.k_stride[1];
+  const int64_t vs0 = A.cache.v_stride[0], vs1 = A.cache.v_stride[1];
+  const int64_t* owner = P.st.owner;
+
+  // ---- prologue.  Lane i < my of each wave fetches the page of the wave's tile i
+  // (kept in a register for the fast pass, and in LDS for the slow pass, which may
+  // run the tile on another wave), so the first tile loads go out before the
+  // workgroup barrier that publishes the queries and the current chunk.
+  int wblk = 0, wseat = 0;
+  if (lane < my) {
+    const int j = wave + kWaves * lane;
     const int t0 = tile_t0(j);
-    int32_t b = 0;
     if (t0 < hist) {
-      b = A.block_table[(int64_t)req * A.block_table_stride + t0 / bs];
+      const int32_t b = A.block_table[(int64_t)req * A.block_table_stride + t0 / bs];
       // ids outside the cache are clamped (the host validates tables; this keeps a
       // bad table from faulting)
-      b = (b < 0 || b >= A.cache.num_blocks) ? 0 : b;
+      wblk = (b < 0 || b >= A.cache.num_blocks) ? 0 : b;
     }
-    s_blk[j] = b;
-    s_seat[j] = P.has_stage ? (int)((unsigned)b % st_rows) * bs : 0;
+    wseat = P.has_stage ? (int)((unsigned)wblk % st_rows) * bs : 0;
+    s_blk[j] = wblk;
+    s_seat[j] = wseat;
   }
+
+  // page of item tile j < count, first key t0 (wave-uniform): block, in-page offset
+  // of t0 and seat-row base; tiles past the history and the clamped placeholder a
+  // wave without tiles loads read block 0 at offsets 0..31 (< block_size).  The
+  // wave's own tile i comes from lane i of wblk / wseat; other tiles (slow pass,
+  // after a barrier) from LDS.
+  auto tile_page = [&](int j, int t0, int& blk, int& off0, int& seat0) {
+    blk = 0;
+    off0 = 0;
+    seat0 = 0;
+    if (j < count && t0 < hist) {
+      off0 = t0 % bs;
+      blk = __builtin_amdgcn_readfirstlane(s_blk[j]);
+      seat0 = __builtin_amdgcn_readfirstlane(s_seat[j]);
+    }
+  };
+
+  auto load_tile = [&](int ti, TileRegs<D>& r) {
+    const int j = wave + kWaves * ti;
+    const int t0 = tile_t0(j);
+    const bool real = j < count && t0 < hist;
+    const int off0 = real ? t0 % bs : 0;
+    r.blk = real ? __builtin_amdgcn_readlane(wblk, ti) : 0;
+    const int seat0 = real ? __builtin_amdgcn_readlane(wseat, ti) : 0;
+    const int off = off0 + m;
+    const uint8_t* ks = kbase + (int64_t)r.blk * ks0 + (int64_t)off * ks1;
+    const uint8_t* vs = vbase + (int64_t)r.blk * vs0 + (int64_t)off * vs1;
+#pragma unroll
+    for (int i = 0; i < C::NQ; ++i) {
+      r.k[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
+      r.v[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
+    }
+    r.meta = *(const u32x2*)ks;
+    // without a staging arena the tag is read from the item record (never matches)
+    const int64_t* op = P.has_stage ? owner + seat0 + off : (const int64_t*)it;
+    r.own = *op;
+  };
+
+  // the wave's first two tiles (register slots A and B, see the main loop)
+  const int last = my > 0 ? my - 1 : 0;
+  TileRegs<D> RA, RB;
+  load_tile(0, RA);
+  load_tile(1 < last ? 1 : last, RB);
+
+  // current chunk (tail items) and queries to LDS
+  bool any_cur_tile = false;
   if (count > 0) any_cur_tile = has_new && tile_t0(count - 1) + kTile > hist;  // tiles ascend
   if (any_cur_tile) {
     constexpr int V8 = D / 8;
@@ -236,8 +332,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
   }
   // queries: lane (row n = m, half g) holds q[n][g*D/2 .. +D/2) in the K-step order
-  // of the code dwords (elements k, k+8 of each 16-element chunk paired); the Q^T
-  // operand of K-step j for lane l lives at s_q[j][l] (shared by the waves)
+  // of the code lookup (kpairs16); the Q^T operand of K-step j for lane l lives at
+  // s_q[j][l] (shared by the waves)
   const int n = m;
   const bool row_ok = n < nrows;
   if (wave == 0) {
@@ -250,14 +346,17 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       u32x4 hi = *(const u32x4*)(qrow + 16 * c + 8);
       if (!row_ok) lo = hi = u32x4{0u, 0u, 0u, 0u};
       unsigned o[8];
-      interleave8(lo, hi, o);
+      kpairs16(lo, hi, o);
       s_q[2 * c][lane] = u32x4{o[0], o[1], o[2], o[3]};
       s_q[2 * c + 1][lane] = u32x4{o[4], o[5], o[6], o[7]};
     }
   }
   const float c_score = A.scale * kLog2e;  // scores in log2 units
   __syncthreads();
-  auto qop = [&](int j) { return __builtin_bit_cast(bf16x8, s_q[j][lane]); };
+  // Q^T operands are read from LDS at each use (volatile: kept out of registers)
+  auto qop = [&](int j) {
+    return __builtin_bit_cast(bf16x8, *(const volatile u32x4*)&s_q[j][lane]);
+  };
 
   // ---- running state (per lane row n): reference max m_run (log2 units), sum l, z
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f;
@@ -266,15 +365,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   for (int b = 0; b < C::MBLK; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[b][r] = 0.f;
-
-  // wave w takes item tiles j = w + 4 i, i < my
-  const int my = count > wave ? (count - 1 - wave) / kWaves + 1 : 0;
-  uint64_t slow_mask = 0, st_bits = 0;
-  const uint8_t* kbase = A.cache.k + (int64_t)kvh * A.cache.k_stride[2];
-  const uint8_t* vbase = A.cache.v + (int64_t)kvh * A.cache.v_stride[2];
-  const int64_t ks0 = A.cache.k_stride[0], ks1 = A.cache.k_stride[1];
-  const int64_t vs0 = A.cache.v_stride[0], vs1 = A.cache.v_stride[1];
-  const int64_t* owner = P.st.owner;
 
   // Lazy: the reference max of a row only moves when a tile's max exceeds it by
   // more than kLazy (log2 units), so probabilities stay <= 2^kLazy and the O
@@ -296,113 +386,64 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
   };
 
-  // page of item tile j, first key t0 (wave-uniform): block, in-page offset of t0
-  // and seat-row base.  Tiles past the history, and the placeholder tile j >= count
-  // a wave without tiles loads in the pipeline prologue (its s_blk entry is never
-  // written), read block 0 at offsets 0..31 (< block_size).
-  auto tile_page = [&](int j, int t0, int& blk, int& off0, int& seat0) {
-    blk = 0;
-    off0 = 0;
-    seat0 = 0;
-    if (j < count && t0 < hist) {
-      off0 = t0 % bs;
-      blk = __builtin_amdgcn_readfirstlane(s_blk[j]);
-      seat0 = __builtin_amdgcn_readfirstlane(s_seat[j]);
-    }
-  };
-
-  auto load_tile = [&](int ti, TileRegs<D>& r) {
-    const int j = wave + kWaves * ti;
-    const int t0 = tile_t0(j);
-    int off0, seat0;
-    tile_page(j, t0, r.blk, off0, seat0);
-    const int off = off0 + m;
-    const uint8_t* ks = kbase + (int64_t)r.blk * ks0 + (int64_t)off * ks1;
-    const uint8_t* vs = vbase + (int64_t)r.blk * vs0 + (int64_t)off * vs1;
-#pragma unroll
-    for (int i = 0; i < C::NQ; ++i) {
-      r.k[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
-      r.v[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
-    }
-    r.meta = *(const u32x2*)ks;
-    // without a staging arena the tag is read from the item record (never matches)
-    const int64_t* op = P.has_stage ? owner + seat0 + off : (const int64_t*)it;
-    r.own = *op;
-  };
-
   // ---------------------------------------------------------------- fast tiles
-  // Straight-line in the O accumulators (no branch around an MFMA, no VALU on O):
-  // a tile that turns out slow (staged token, mask, ragged end, or a max more than
-  // kLazy above the wave's reference max) or that only pads the pipeline runs with
-  // P = 0 and, if real, is queued for the slow pass.
-  //
-  // Two tiles are in compute at once: iteration i runs the QK MFMAs of tile i+1
-  // (their operands looked up on the VALU in between), then the softmax of tile
-  // i+1 on the VALU next to the PV MFMAs of tile i, so the MFMA and VALU pipes
-  // overlap.  V codes and V constants sit in LDS double buffers (tile parity).
-
-  // QK of tile ti: V codes and V constants to LDS buffer bf, S^T = K Q^T with the
-  // exact history values looked up per code pair.  Returns the pre-softmax slow
-  // flag (a staged token, or a tile beyond the fast range).
-  auto qk_tile = [&](int ti, const TileRegs<D>& r, int bf, f32x16& S) -> bool {
+  // Phase 1 (QK) of tile ti: decides whether the tile is fast (INT2 history only,
+  // no staged token, no mask); if so, its V codes and V constants go to this wave's
+  // LDS slots and S^T = K Q^T runs with the exact history values looked up per code.
+  auto qk_tile = [&](int ti, const TileRegs<D>& r, f32x16& S) -> bool {
     const int t0 = tile_t0(wave + kWaves * ti);
     const int p = t0 + m;
-    const bool real = ti < my;
-    const bool staged = P.has_stage && real && p < hist && r.own == (int64_t)r.blk;
-    st_bits |= (uint64_t)staged << (ti & 63);  // ti < 64 whenever staged
-    const bool slow = real && !((t0 + kTile <= fast_end) && !__any(staged));
+    const bool staged = P.has_stage && p < hist && r.own == (int64_t)r.blk;
+    if (!((t0 + kTile <= fast_end) && !__any(staged))) return false;
 #pragma unroll
-    for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][bf][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
-    s_cst[wave][bf][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
-    s_cst[wave][bf][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
-    unsigned lut_lo, lut_hi;
-    value_table(r.meta[0], lut_lo, lut_hi);
+    for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
+    s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
+    s_cst[wave][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
+    unsigned t_lo, t_hi;
+    byte_tables(r.meta[0], t_lo, t_hi);
 #pragma unroll
     for (int r2 = 0; r2 < 16; ++r2) S[r2] = 0.f;
 #pragma unroll
     for (int i = 0; i < C::NCH; ++i) {
       unsigned o[8];
-      table_pairs(r.k[i >> 2][i & 3], lut_lo, lut_hi, o);
+      lut16(r.k[i >> 2][i & 3], t_lo, t_hi, o);
       S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]}),
                                                   qop(2 * i), S, 0, 0, 0);
       S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]}),
                                                   qop(2 * i + 1), S, 0, 0, 0);
     }
-    return slow;
+    return true;
   };
 
-  // softmax of tile ti (scores S, V constants in buffer bf): P' = p * s_V (fp16)
-  // feeds the PV MFMA, sum p and sum p * z_V accumulate on the VALU
-  auto softmax_tile = [&](int ti, const f32x16& S, bool slow, int bf, u32x4* pb) {
-    const bool real = ti < my;
+  // Phase 2: softmax against the wave's reference max and O^T += V^T P'^T.  Returns
+  // false (nothing accumulated) when a row's max drifts more than kLazy above it.
+  // P' = p * s_V (fp16) is the B operand; V^T comes from LDS by transpose reads as
+  // the subnormals c * 2^(2k-24); sum p and sum p * z_V accumulate on the VALU.
+  auto pv_tile = [&](const f32x16& S) -> bool {
     wait_lds();
     __builtin_amdgcn_wave_barrier();
-    float xs[16];
     float mx = -INFINITY;
 #pragma unroll
-    for (int r2 = 0; r2 < 16; ++r2) {
-      xs[r2] = S[r2] * c_score;
-      mx = fmaxf(mx, xs[r2]);
-    }
-    mx = fmaxf(mx, swap_halves(mx));
-    // the first used tile sets the reference max (O, l, z are still zero); after
-    // that a tile whose max drifts more than kLazy above it goes to the slow pass
-    const bool first = m_run == -INFINITY;  // uniform: fast-tile scores are finite
-    slow = slow || (real && !first && __any(mx > m_run + kLazy));
-    if (slow) slow_mask |= 1ull << ti;
-    const bool use = real && !slow;
-    if (use && first) m_run = mx;
+    for (int r2 = 0; r2 < 16; ++r2) mx = fmaxf(mx, S[r2]);
+    mx = fmaxf(mx, swap_halves(mx)) * c_score;  // c_score > 0
+    // the first fast tile sets the reference max (O, l, z are still zero); the
+    // state is uniform across the wave's rows until the slow pass
+    const bool first = m_run == -INFINITY;
+    if (!first && __any(mx > m_run + kLazy)) return false;
+    if (first) m_run = mx;
+    const float nm = -m_run;
+    u32x4 pb[2];
     float lsum = 0.f, zsum = 0.f;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const f32x4 sv = *(const f32x4*)&s_cst[wave][bf][0][8 * q4 + 4 * g];
-      const f32x4 zv = *(const f32x4*)&s_cst[wave][bf][1][8 * q4 + 4 * g];
+      const f32x4 sv = *(const f32x4*)&s_cst[wave][0][8 * q4 + 4 * g];
+      const f32x4 zv = *(const f32x4*)&s_cst[wave][1][8 * q4 + 4 * g];
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
         const int r0 = 4 * q4 + i;
         // p <= 2^kLazy: no range reduction needed for v_exp_f32
-        const float p0 = use ? __builtin_amdgcn_exp2f(xs[r0] - m_run) : 0.f;
-        const float p1 = use ? __builtin_amdgcn_exp2f(xs[r0 + 1] - m_run) : 0.f;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(S[r0], c_score, nm));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(S[r0 + 1], c_score, nm));
         lsum += p0 + p1;
         zsum = fmaf(p0, zv[i], fmaf(p1, zv[i + 1], zsum));
         const f16x2 h = {(_Float16)(p0 * sv[i]), (_Float16)(p1 * sv[i + 1])};
@@ -411,11 +452,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
     l_run += lsum;
     z_run += zsum;
-  };
-
-  // PV of a tile whose V codes sit in buffer bf: O^T += V^T P'^T, V^T from LDS via
-  // transpose reads
-  auto pv_tile = [&](int bf, const u32x4* pb) {
     const int G16 = lane >> 4, i16 = lane & 15;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -424,7 +460,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 #pragma unroll
       for (int cp = 0; cp < D / 128; ++cp) {
         const int chunk = (D == 256) ? (2 * cp + (G16 & 1)) : (G16 & 1);
-        const uint8_t* addr = &s_vcode[wave][bf][tok * C::NB + chunk * 16 + half8];
+        const uint8_t* addr = &s_vcode[wave][tok * C::NB + chunk * 16 + half8];
         i32x2 tr = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             (__attribute__((address_space(3))) i32x2*)(addr));
         const unsigned x0 = (unsigned)tr[0], x1 = (unsigned)tr[1];
@@ -442,38 +478,29 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
         }
       }
     }
+    __builtin_amdgcn_wave_barrier();  // the LDS slots are rewritten by the next tile
+    return true;
   };
 
-  // software pipeline: tile t's packed data sits in register slot t % 3 from its load
-  // until its QK, then the slot is refilled with tile t + 3 (clamped to the last tile:
-  // the surplus loads at the end re-read a tile already in cache and are never used)
+  // Two register slots hold the packed data of the wave's next tiles: slot A the
+  // even tiles, slot B the odd ones.  A slot is refilled (index clamped to the last
+  // tile, so every path issues the same loads) as soon as its tile's QK has consumed
+  // it, so the next two tiles are in flight while a tile is computed.
+  uint32_t slow_bits = 0;  // wave tiles (index i) queued for the slow pass
   {
-    static_assert(kDepth == 3, "the unrolled slot rotation below assumes three slots");
-    TileRegs<D> R[kDepth];
-    const int last = my > 0 ? my - 1 : 0;
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) load_tile(d < last ? d : last, R[d]);
-    f32x16 S;
-    u32x4 pb[2];
-    {
-      const bool sl = qk_tile(0, R[0], 0, S);
-      softmax_tile(0, S, sl, 0, pb);
-      load_tile(3 < last ? 3 : last, R[0]);
-    }
-    for (int base = 0; base < my; base += kDepth) {
-#pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
-        const int i = base + d;          // tile whose PV runs now
-        const int dn = (d + 1) % kDepth;  // slot of tile i + 1
-        f32x16 Sn;
-        const bool sl = qk_tile(i + 1, R[dn], (i + 1) & 1, Sn);
-        u32x4 pbn[2];
-        softmax_tile(i + 1, Sn, sl, (i + 1) & 1, pbn);
-        pv_tile(i & 1, pb);
-        pb[0] = pbn[0];
-        pb[1] = pbn[1];
-        load_tile(i + 4 < last ? i + 4 : last, R[dn]);
+    for (int i = 0; i < my; i += 2) {
+      {
+        f32x16 S;
+        const bool fast = qk_tile(i, RA, S);
+        load_tile(i + 2 < last ? i + 2 : last, RA);
+        if (!(fast && pv_tile(S))) slow_bits |= 1u << i;
       }
+      const bool second = i + 1 < my;
+      f32x16 S;
+      bool fast = false;
+      if (second) fast = qk_tile(i + 1, RB, S);
+      load_tile(i + 3 < last ? i + 3 : last, RB);
+      if (second && !(fast && pv_tile(S))) slow_bits |= 2u << i;
     }
   }
 
@@ -490,16 +517,28 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   }
 
   // ---------------------------------------------------------------- slow tiles
-  while (slow_mask) {
-    const int ti = __builtin_ctzll(slow_mask);
-    slow_mask &= slow_mask - 1;
-    const int j = wave + kWaves * ti;
+  // Every wave's queued tiles go to one list; waves 0..kSlowWaves-1 take them in
+  // turn (a wave may add any tile of the item to its own softmax state: the wave
+  // states are merged below).
+  if (lane == 0) s_nslow[wave] = __popc(slow_bits);
+  __syncthreads();
+  int nslow = 0, slot0 = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int c = s_nslow[w];
+    slot0 += w < wave ? c : 0;
+    nslow += c;
+  }
+  for (uint32_t bits = slow_bits; bits; bits &= bits - 1, ++slot0)
+    if (lane == 0) s_slow[slot0] = (int16_t)(wave + kWaves * __builtin_ctz(bits));
+  __syncthreads();
+  uint16_t* s_slowv = (uint16_t*)s_big + (wave % kSlowWaves) * (kTile * C::VROW);
+  for (int k = wave; wave < kSlowWaves && k < nslow; k += kSlowWaves) {
+    const int j = s_slow[k];
     const int t0 = tile_t0(j);
     const int p = t0 + m;
-    const bool staged = (st_bits >> ti) & 1;
     const bool hist_tok = p < hist;
     const bool cur_tok = has_new && p < seq && p >= hist;
-    const bool any_st = __any(staged), any_cur = __any(cur_tok);
     int blk, off0, seat0;
     tile_page(j, t0, blk, off0, seat0);
     const int off = off0 + m;
@@ -512,13 +551,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       vc[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
     }
     const u32x2 meta = *(const u32x2*)ks;
+    const int64_t own = P.has_stage ? owner[seat0 + off] : -1;
+    const bool staged = P.has_stage && hist_tok && own == (int64_t)blk;
+    const bool any_st = __any(staged), any_cur = __any(cur_tok);
     // FP32 staged rows of this lane's token (seat row 0 for lanes without one)
     const int64_t seat = staged ? (int64_t)seat0 + off : 0;
     const float* sk_row = P.st.stage_k + (seat * hk + kvh) * D + g * (D / 2);
     const float* sv_row = P.st.stage_v + (seat * hk + kvh) * D + g * (D / 2);
     const int ci = cur_tok ? p - hist : 0;
-    unsigned klo, khi, vlo, vhi;
-    value_table(meta[0], klo, khi);
+    unsigned kt_lo, kt_hi, vlo, vhi;
+    byte_tables(meta[0], kt_lo, kt_hi);
     value_table(meta[1], vlo, vhi);
 
     f32x16 S = {};
@@ -538,19 +580,23 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       for (int cc = 0; cc < C::CPR; ++cc) {
         const int c = c0 + cc;
         unsigned ok[8], ov[8];
-        table_pairs(kc[c >> 2][c & 3], klo, khi, ok);
+        lut16(kc[c >> 2][c & 3], kt_lo, kt_hi, ok);
         table_pairs(vc[c >> 2][c & 3], vlo, vhi, ov);
         if (any_st && staged) {
+          // K in the lookup's pair order (e, e+4) / (e+8, e+12); V as (e, e+8)
 #pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            ok[k] = hist_pair(fk[cc][k >> 2][k & 3], fk[cc][2 + (k >> 2)][k & 3]);
-            ov[k] = hist_pair(fv[cc][k >> 2][k & 3], fv[cc][2 + (k >> 2)][k & 3]);
+          for (int k = 0; k < 4; ++k) {
+            ok[k] = hist_pair(fk[cc][0][k], fk[cc][1][k]);
+            ok[4 + k] = hist_pair(fk[cc][2][k], fk[cc][3][k]);
           }
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            ov[k] = hist_pair(fv[cc][k >> 2][k & 3], fv[cc][2 + (k >> 2)][k & 3]);
         }
         if (any_cur && cur_tok) {
           const uint16_t* kr = &s_cur[0][ci][g * (D / 2) + 16 * c];
           const uint16_t* vr = &s_cur[1][ci][g * (D / 2) + 16 * c];
-          interleave8(*(const u32x4*)kr, *(const u32x4*)(kr + 8), ok);
+          kpairs16(*(const u32x4*)kr, *(const u32x4*)(kr + 8), ok);
           interleave8(*(const u32x4*)vr, *(const u32x4*)(vr + 8), ov);
         }
         if (!hist_tok && !cur_tok) {
@@ -620,8 +666,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     __builtin_amdgcn_wave_barrier();
   }
 
-  // ---- cross-wave merge: common max M and total L per row, then the four wave
-  // partials are summed in LDS in MFMA register order (16-byte accesses)
+  // ---- cross-wave merge: common max M and total L per row, then the wave partials
+  // are summed in LDS in MFMA register order, two output blocks per round
   const float l_row = l_run + swap_halves(l_run);
   __syncthreads();  // every wave is past its slow tiles (s_big is free)
   if (g == 0) { s_ml[wave][0][m] = m_run; s_ml[wave][1][m] = l_row; }
@@ -636,37 +682,26 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (mw != -INFINITY) L += s_ml[w][1][n] * exp2f(mw - M);
   }
   const float fw = (m_run == -INFINITY || !(L > 0.f)) ? 0.f : exp2f(m_run - M) / L;
+  f32x4* buf = (f32x4*)s_big;  // [kWaves][2 blocks][4][64] f32x4
+  f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
 #pragma unroll
-  for (int b = 0; b < C::MBLK; ++b)
+  for (int rb = 0; rb < C::MBLK / 2; ++rb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) O[b][r] *= fw;
-  f32x4* buf = (f32x4*)s_big;  // [2][MBLK][4][64] f32x4
-  auto put = [&](int slot) {
-#pragma unroll
-    for (int b = 0; b < C::MBLK; ++b)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        buf[((slot * C::MBLK + b) * 4 + q) * 64 + lane] =
-            f32x4{O[b][4 * q], O[b][4 * q + 1], O[b][4 * q + 2], O[b][4 * q + 3]};
-  };
-  if (wave >= 2) put(wave - 2);
-  __syncthreads();
-  if (wave < 2) {
-#pragma unroll
-    for (int b = 0; b < C::MBLK; ++b)
+    for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const f32x4 v = buf[((wave * C::MBLK + b) * 4 + q) * 64 + lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) O[b][4 * q + j] += v[j];
+        const f32x16& Ob = O[2 * rb + bb];
+        buf[((wave * 2 + bb) * 4 + q) * 64 + lane] =
+            f32x4{Ob[4 * q] * fw, Ob[4 * q + 1] * fw, Ob[4 * q + 2] * fw, Ob[4 * q + 3] * fw};
       }
-    put(wave);
+    __syncthreads();
+    f32x4 acc = buf[tid];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) acc += buf[w * kThreads + tid];
+    const int e = rb * kThreads + tid;  // f32x4 index of the partial (row = e % 32)
+    if ((e & 31) < nrows) po[e] = acc;
+    __syncthreads();
   }
-  __syncthreads();
-  // item partial: slot 0 + slot 1, register order, rows < nrows; lse [32]
-  f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
-  for (int e = tid; e < C::NV; e += kThreads)
-    if ((e & 31) < nrows) po[e] = buf[e] + buf[C::NV + e];
   if (tid < 32) {
     float lse = (L > 0.f && M != -INFINITY) ? (M + log2f(L)) * kLn2 : -INFINITY;
     if (M != M || L != L) lse = NAN;
@@ -679,16 +714,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 // of the register-order partial): lane l owns partial vector chunk * 64 + l, i.e.
 // row l % 32, four d values.  Online merge over batches of kBatch items whose
 // partial vectors and LSEs are loaded together.
-constexpr int kBatch = 16;
+constexpr int kBatch = 40;  // one round of loads for up to 40 items
 
 template <int D>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams P) {
   using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
-  const int32_t* grp = A.groups + (int64_t)blockIdx.x * 4;
-  const int req = grp[0], kvh = grp[1], i0 = grp[2], ni = grp[3];
-  const int a = A.query_start_loc[req];
-  const int nq = A.query_start_loc[req + 1] - a;
+  // the group record carries everything the merge needs (no dependent loads)
+  const int32_t* grp = A.groups + (int64_t)blockIdx.x * OSCAR_GROUP_INTS;
+  const int req = grp[0], kvh = grp[1], i0 = grp[2], ni = grp[3], a = grp[4], nq = grp[5];
+  (void)req;
   const int G = P.group;
   const int lane = threadIdx.x;
   const int n = lane & 31, gg = lane >> 5;
@@ -860,10 +895,14 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
       emit(G, G.first_slot + (G.ntail > 0) + pos, pos, G.k, (G.nbody - pos + G.k - 1) / G.k);
     }
   for (int q = 0; q < ngroups; ++q) {
-    groups[q * 4 + 0] = gl[q].req;
-    groups[q * 4 + 1] = gl[q].kvh;
-    groups[q * 4 + 2] = gl[q].first_slot;
-    groups[q * 4 + 3] = gl[q].k + (gl[q].ntail > 0);
+    int32_t* gr = groups + (int64_t)q * OSCAR_GROUP_INTS;
+    gr[0] = gl[q].req;
+    gr[1] = gl[q].kvh;
+    gr[2] = gl[q].first_slot;
+    gr[3] = gl[q].k + (gl[q].ntail > 0);
+    gr[4] = qsl[gl[q].req];
+    gr[5] = qsl[gl[q].req + 1] - qsl[gl[q].req];
+    gr[6] = gr[7] = 0;
   }
   return nitems;
 }

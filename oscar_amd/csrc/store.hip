@@ -44,7 +44,11 @@ struct StoreParams {
   oscar_store_args_v1 a;
   float* y;          // workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
   int64_t capacity;  // num_blocks * block_size
+  int scan;          // small call: winners found by scanning slot_mapping (no claims)
 };
+
+// calls of at most this many tokens resolve last writers by scanning
+constexpr int64_t kScanTokens = 1024;
 
 __device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
   // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
@@ -148,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void store_rotate_small_kernel(StoreParam
       for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
     }
   }
-  if (kind == KIND_K && blockIdx.y == 0) record_claims(p, vec0, kSV, heads, nvec);
+  if (kind == KIND_K && blockIdx.y == 0 && !p.scan) record_claims(p, vec0, kSV, heads, nvec);
 #pragma unroll
   for (int i = 0; i < RI; ++i) {
     const int e = tid + i * kThreads, k = e / (kSC / 4), c4 = e % (kSC / 4);
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
     }
   }
 
-  if (kind == KIND_K && blockIdx.y == 0) record_claims(p, vec0, TV, heads, nvec);
+  if (kind == KIND_K && blockIdx.y == 0 && !p.scan) record_claims(p, vec0, TV, heads, nvec);
 
 #pragma unroll
   for (int i = 0; i < RV; ++i) {
@@ -310,7 +314,7 @@ __device__ float clip_threshold(const float* row, int idx, volatile float* slot)
   return *slot;
 }
 
-template <int D>
+template <int D, bool SCAN>
 __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
   const oscar_store_args_v1& a = p.a;
@@ -318,53 +322,73 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   const int64_t hk = a.cache.num_kv_heads;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // this call's epoch (word1, set by the rotate launch); word0 takes it for the next
-  // call (no other quant workgroup reads word0)
-  const int64_t epoch = a.epoch_counter[1];
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
+  // call (no other quant workgroup reads word0).  Scan calls use no claims.
+  int64_t epoch = 0;
+  if constexpr (!SCAN) {
+    epoch = a.epoch_counter[1];
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
+  }
   const int64_t vec = (int64_t)blockIdx.x * (kThreads / 64) + wave;
   if (vec >= a.num_tokens * hk) return;
   const int64_t t = vec / hk, h = vec % hk;
   const bool active = lane < NL;
+  const int64_t bs = a.cache.block_size;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
 
-  // ---- round 1: slot, this vector's row, request starts
+  // ---- one round of loads: slot, this vector's row, the request table (and, for a
+  // scan call, every slot of the call)
   const int64_t slot = a.slot_mapping[t];
   const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
   const f32x4 x4 = *(const f32x4*)(y + 4 * (active ? lane : 0));
-  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
-  // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t
-  int req = 0;
-  if (window) {
-    int count = 0;
-    for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
-      const int r = c0 + lane;
-      const int64_t st = r < a.num_reqs ? a.query_start_loc[r] : a.num_tokens;
-      const int64_t start = st < a.num_tokens ? st : a.num_tokens;
-      count += __popcll(__ballot(r < a.num_reqs && start <= t));
-    }
-    req = count > 0 ? count - 1 : 0;
-  }
-  if (slot < 0 || slot >= p.capacity) return;
-  const int64_t bs = a.cache.block_size;
-  const int64_t blk = slot / bs, off = slot % bs;
-
-  // ---- round 2: claims and the request's bounds
-  const long long mine = claim_value(epoch, t);
-  const long long slot_claim = (long long)a.slot_claims[slot];
-  int64_t seat = 0;
-  long long seat_claim = 0;
+  // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
+  // length and query end come from the same loads (qsl is non-decreasing)
   int64_t seq = 0, end = 0;
   if (window) {
-    seat = seat_of(slot, bs, a.staging.rows);
-    seat_claim = (long long)a.seat_claims[seat];
-    seq = a.seq_lens[req];
-    end = a.query_start_loc[req + 1];
+    for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
+      const int r = c0 + lane;
+      const bool in = r < a.num_reqs;
+      const int64_t st = in ? a.query_start_loc[r] : a.num_tokens;
+      const int64_t nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
+      const int64_t sq = in ? a.seq_lens[r] : 0;
+      const int64_t start = st < a.num_tokens ? st : a.num_tokens;
+      const uint64_t bal = __ballot(in && start <= t);
+      if (bal) {
+        const int last = 63 - __builtin_clzll(bal);
+        seq = __shfl(sq, last);
+        end = __shfl(nx, last);
+      }
+    }
+  }
+  if (slot < 0 || slot >= p.capacity) return;
+  const int64_t blk = slot / bs, off = slot % bs;
+  const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
+  bool slot_win, seat_win;
+  if constexpr (SCAN) {
+    // last writer: no later valid token of the call has the same slot / seat
+    bool later_slot = false, later_seat = false;
+    for (int64_t c0 = 0; c0 < a.num_tokens; c0 += 64) {
+      const int64_t t2 = c0 + lane;
+      const int64_t s2 = t2 < a.num_tokens ? a.slot_mapping[t2] : -1;
+      const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
+      later_slot |= later && s2 == slot;
+      if (window) later_seat |= later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
+    }
+    slot_win = !__any(later_slot);
+    seat_win = !__any(later_seat);
+    // standalone KV update: every written seat loses its window copy
+    if (a.stage_mode == OSCAR_STAGE_INVALIDATE && kind == KIND_K && lane == 0) a.staging.owner[seat] = -1;
+  } else {
+    // ---- second round: the claims
+    const long long mine = claim_value(epoch, t);
+    slot_win = (long long)a.slot_claims[slot] == mine;
+    seat_win = window && (long long)a.seat_claims[seat] == mine;
   }
   __shared__ float rows[kThreads / 64][D];
   __shared__ float clip_slot[kThreads / 64];
   float* row = rows[wave];
   if (active) *(f32x4*)&row[4 * lane] = x4;
 
-  if (window && seat_claim == mine) {
+  if (window && seat_win) {
     const int64_t pos = seq - end + t;
     const bool keep = (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
     if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
@@ -373,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
       *(f32x4*)&dst[4 * lane] = x4;
     }
   }
-  if (slot_claim != mine) return;
+  if (!slot_win) return;
 
   const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
   float thr = INFINITY;
@@ -444,7 +468,8 @@ int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_
   }
   OSCAR_CHECK_LAUNCH("store_rotate_kernel");
   dim3 qgrid((unsigned)((kv_vec + 3) / 4), 2);
-  hipLaunchKernelGGL(store_quant_kernel<D>, qgrid, dim3(kThreads), 0, s, p);
+  if (p.scan) hipLaunchKernelGGL((store_quant_kernel<D, true>), qgrid, dim3(kThreads), 0, s, p);
+  else hipLaunchKernelGGL((store_quant_kernel<D, false>), qgrid, dim3(kThreads), 0, s, p);
   OSCAR_CHECK_LAUNCH("store_quant_kernel");
   return 0;
 }
@@ -517,7 +542,8 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
   const int64_t need = oscar_store_workspace_bytes_v1(a.num_tokens, a.cache.num_kv_heads, D);
   if (a.workspace == nullptr || a.workspace_bytes < need || (((uintptr_t)a.workspace) & 15))
     return fail(-22, "oscar_store_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
-  StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size};
+  StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size,
+                a.num_tokens <= kScanTokens};
   const int64_t kv_vec = a.num_tokens * a.cache.num_kv_heads;
   const int64_t q_vec = (a.query_rot != nullptr) ? a.num_tokens * a.num_q_heads : 0;
   hipStream_t s = (hipStream_t)stream;

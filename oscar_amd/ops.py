@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import (OSCAR_BF16, OSCAR_F16, OSCAR_F32, STAGE_INVALIDATE, STAGE_NONE,
+from ._lib import (GROUP_INTS, OSCAR_BF16, OSCAR_F16, OSCAR_F32, STAGE_INVALIDATE, STAGE_NONE,
                    STAGE_WRITE, WORK_INTS)
 
 _DTYPES = {torch.float32: OSCAR_F32, torch.float16: OSCAR_F16, torch.bfloat16: OSCAR_BF16}
@@ -227,7 +227,7 @@ def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, grou
     if n < 0:
         _lib.check(n, "oscar_attn_plan_v1")
     items = (C.c_int32 * max(plan.num_items * WORK_INTS, 1))()
-    groups = (C.c_int32 * max(plan.num_groups * 4, 1))()
+    groups = (C.c_int32 * max(plan.num_groups * GROUP_INTS, 1))()
     n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
                                chunk_tokens, target_items, items, plan.num_items, groups,
                                plan.num_groups, C.byref(plan))
@@ -235,7 +235,7 @@ def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, grou
         _lib.check(n, "oscar_attn_plan_v1")
     host_items = list(items)[: plan.num_items * WORK_INTS]
     it = torch.tensor(host_items or [0], dtype=torch.int32).view(-1)
-    gr = torch.tensor(list(groups)[: plan.num_groups * 4] or [0], dtype=torch.int32)
+    gr = torch.tensor(list(groups)[: plan.num_groups * GROUP_INTS] or [0], dtype=torch.int32)
     return DecodePlan(it.to(device), gr.to(device),
                       torch.tensor(qsl, dtype=torch.int32).to(device),
                       torch.tensor(seqs or [0], dtype=torch.int32).to(device),

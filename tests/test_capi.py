@@ -85,12 +85,12 @@ def plan(lib, qsl, seqs, has_new=True, hk=1, group=6, d=256, chunk=8192, target=
     if cnt < 0:
         return cnt, None, None, p
     items = (C.c_int32 * max(p.num_items * 8, 1))()
-    groups = (C.c_int32 * max(p.num_groups * 4, 1))()
+    groups = (C.c_int32 * max(p.num_groups * 8, 1))()
     cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, items, p.num_items,
                                  groups, p.num_groups, C.byref(p))
     assert cnt == p.num_items
     it = np.array(list(items)[:p.num_items * 8], np.int64).reshape(-1, 8)
-    gr = np.array(list(groups)[:p.num_groups * 4], np.int64).reshape(-1, 4)
+    gr = np.array(list(groups)[:p.num_groups * 8], np.int64).reshape(-1, 8)
     return cnt, it, gr, p
 
 
@@ -126,7 +126,8 @@ def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, 
             seen_body = True
             assert first + stride * (count - 1) < body
     # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous
-    for req, kvh, first_slot, nslots in groups:
+    for req, kvh, first_slot, nslots, qa, nq, z0, z1 in groups:
+        assert qa == qsl[req] and nq == qsl[req + 1] - qsl[req] and z0 == z1 == 0
         rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh)]
         assert sorted(rows[:, 5].tolist()) == list(range(first_slot, first_slot + nslots))
         cover = np.zeros((seqs[req] + TILE - 1) // TILE, np.int64)
@@ -151,7 +152,7 @@ def test_plan_rejects_bad_requests(lib):
     assert cnt == -22 and b"head_dim" in lib.oscar_last_error()
     qa, sa = (C.c_int32 * 2)(0, 1), (C.c_int32 * 1)(100)
     p = _lib.Plan()
-    small = (C.c_int32 * 8)()
+    small = (C.c_int32 * 16)()
     assert lib.oscar_attn_plan_v1(qa, sa, 1, 1, 1, 6, 256, 32, 64, small, 1, small, 2, C.byref(p)) == -28
 
 

@@ -46,10 +46,12 @@ def run_store(k, v, caches, slots, d, rk, rv, **kw):
     return kc.view(torch.uint8).cpu().numpy(), vc.view(torch.uint8).cpu().numpy()
 
 
+# 1500 tokens: last writers via claim tables; 300 tokens: via the slot scan of small calls
+@pytest.mark.parametrize("n", [1500, 300])
 @pytest.mark.parametrize("d,hk,rot", [(256, 1, "hadamard"), (256, 1, "identity"),
                                       (128, 2, "qr"), (64, 4, "hadamard")])
-def test_store_bytes_bit_exact(cuda, d, hk, rot):
-    n, bs, nb = 1500, 128, 16
+def test_store_bytes_bit_exact(cuda, d, hk, rot, n):
+    bs, nb = 128, 16
     k = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 1)
     v = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 2)
     rk = {"hadamard": cases.hadamard_rotation(d, 3), "qr": cases.qr_rotation(d, 3),
@@ -102,13 +104,16 @@ def test_store_clip_bit_exact(cuda):
     assert np.array_equal(got_v, v8)
 
 
-def test_store_window_tags_values_and_rotated_outputs(cuda):
+# the last request of each case is empty; with 100 blocks over 64 staging rows,
+# blocks b and b + 64 share seats (collisions resolved by the last writer)
+@pytest.mark.parametrize("qsl,seqs,nb", [([0, 700, 705, 1200, 1200], [700, 2000, 496, 10], 32),
+                                         ([0, 300, 305, 600, 600], [300, 2000, 496, 10], 100)])
+def test_store_window_tags_values_and_rotated_outputs(cuda, qsl, seqs, nb):
     """Forward write: codes + owner tags + FP32 window + rotated q/k/v for the read."""
     from oscar_amd import ops
     from oscar_amd._lib import STAGE_WRITE
 
-    d, hk, hq, bs, nb = 256, 1, 6, 128, 32
-    qsl, seqs = [0, 700, 705, 1200, 1200], [700, 2000, 496, 10]  # last request empty
+    d, hk, hq, bs = 256, 1, 6, 128
     n = qsl[-1]
     k = cases.kv_outliers(n, hk, d, 31)
     v = cases.kv_outliers(n, hk, d, 32)
