@@ -60,70 +60,95 @@ def hadamard_rotation(d, gen, dev):
 
 
 class Setup:
-    """16 layers of packed caches + staging arenas, and the step's static inputs."""
+    """Layers of packed caches + staging arenas and one step's static inputs.
 
-    def __init__(self, dev):
+    histories: per-request INT2 history lengths; q_len new (or, cache-only, last
+    cached) tokens per request.  The history of each request is written as a server
+    leaves it: a standalone KV update of all but its last `recent` tokens, then a
+    window write of those (so the FP32 recent window is live)."""
+
+    def __init__(self, dev, histories=None, q_len=None, has_new=True, layers=LAYERS, seed=20261201):
         from oscar_amd import ops
         from oscar_amd._lib import STAGE_INVALIDATE, STAGE_WRITE
 
         c = CONFIG
-        B, L, n, hq, hk, d, bs = (c["requests"], c["history"], c["q_len"], c["hq"], c["hk"],
-                                  c["d"], c["block_size"])
-        self.dev = dev
-        gen = torch.Generator(device=dev).manual_seed(20261201)
-        pages = math.ceil((L + n) / bs)
-        self.nb = B * pages
-        self.bt = torch.randperm(self.nb, generator=gen, device=dev).view(B, pages).to(torch.int32)
+        histories = histories or [c["history"]] * c["requests"]
+        n = q_len or c["q_len"]
+        B = len(histories)
+        hq, hk, d, bs = c["hq"], c["hk"], c["d"], c["block_size"]
+        self.dev, self.n, self.has_new, self.histories = dev, n, has_new, list(histories)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        span = [L + (n if has_new else 0) for L in histories]
+        pages = [math.ceil(x / bs) for x in span]
+        self.nb = sum(pages)
+        perm = torch.randperm(self.nb, generator=gen, device=dev).to(torch.int32)
+        self.bt = torch.zeros(B, max(pages), dtype=torch.int32, device=dev)
+        o = 0
+        for r, p in enumerate(pages):
+            self.bt[r, :p] = perm[o:o + p]
+            o += p
         self.rk = hadamard_rotation(d, gen, dev)
         self.rv = hadamard_rotation(d, gen, dev).flip(0).contiguous()
         self.scale = d ** -0.5
-        bs_ = bs
-        self.sink_eff = (c["sink_tokens"] // bs_) * bs_
-        rows = max(math.ceil(c["staging_tokens"] / bs_),
-                   self.sink_eff // bs_ + math.ceil(c["recent_tokens"] / bs_) + 1 + 2)
+        self.sink_eff = (c["sink_tokens"] // bs) * bs
+        rows = max(math.ceil(c["staging_tokens"] / bs),
+                   self.sink_eff // bs + math.ceil(c["recent_tokens"] / bs) + 1 + 2)
         recent = c["recent_tokens"]
-        pos = torch.arange(L, device=dev)
-        hist_slots = (self.bt[:, (pos // bs)].long() * bs + pos % bs)        # [B, L]
-        hist_k = outlier_kv(B * L, hk, d, gen, dev).view(B, L, hk, d)
-        hist_v = outlier_kv(B * L, hk, d, gen, dev).view(B, L, hk, d)
-        body, tail = slice(0, L - recent), slice(L - recent, L)
-        qsl_t = torch.arange(0, B * recent + 1, recent, dtype=torch.int32, device=dev)
-        seq_t = torch.full((B,), L, dtype=torch.int32, device=dev)
+        body_slots, tail_slots, tail_len = [], [], []
+        for r, L in enumerate(histories):
+            pos = torch.arange(L, device=dev)
+            sl = self.bt[r, pos // bs].long() * bs + pos % bs
+            cut = max(L - recent, 0)
+            body_slots.append(sl[:cut])
+            tail_slots.append(sl[cut:])
+            tail_len.append(L - cut)
+        body_slots, tail_slots = torch.cat(body_slots), torch.cat(tail_slots)
+        qsl_t = torch.tensor([0] + np.cumsum(tail_len).tolist(), dtype=torch.int32, device=dev)
+        seq_t = torch.tensor(histories, dtype=torch.int32, device=dev)
+        nbody, ntail = body_slots.numel(), tail_slots.numel()
         self.layers = []
-        for layer in range(LAYERS):
+        for layer in range(layers):
             kc = torch.zeros(self.nb, bs, hk, d, dtype=torch.int8, device=dev)
             vc = torch.zeros_like(kc)
             stage = (torch.zeros(rows, bs, hk, d, dtype=torch.float32, device=dev),
                      torch.zeros(rows, bs, hk, d, dtype=torch.float32, device=dev),
                      torch.full((rows, bs), -1, dtype=torch.int64, device=dev))
-            # standalone KV update of the prefix (tags nothing), then the window write
-            ops.store(hist_k[:, body].reshape(-1, hk, d), hist_v[:, body].reshape(-1, hk, d), kc, vc,
-                      hist_slots[:, body].reshape(-1), head_dim=d, rk=self.rk, rv=self.rv,
-                      stage=stage, stage_mode=STAGE_INVALIDATE)
-            ops.store(hist_k[:, tail].reshape(-1, hk, d), hist_v[:, tail].reshape(-1, hk, d), kc, vc,
-                      hist_slots[:, tail].reshape(-1), head_dim=d, rk=self.rk, rv=self.rv,
-                      stage=stage, stage_mode=STAGE_WRITE, qsl_dev=qsl_t, seqs_dev=seq_t,
-                      num_reqs=B, recent_tokens=recent, sink_tokens_eff=self.sink_eff)
+            for lo in range(0, nbody, 1 << 20):  # standalone KV update of the prefixes
+                hi = min(lo + (1 << 20), nbody)
+                ops.store(outlier_kv(hi - lo, hk, d, gen, dev), outlier_kv(hi - lo, hk, d, gen, dev), kc, vc,
+                          body_slots[lo:hi], head_dim=d, rk=self.rk, rv=self.rv, stage=stage,
+                          stage_mode=STAGE_INVALIDATE)
+            ops.store(outlier_kv(ntail, hk, d, gen, dev), outlier_kv(ntail, hk, d, gen, dev), kc, vc,
+                      tail_slots, head_dim=d, rk=self.rk, rv=self.rv, stage=stage,
+                      stage_mode=STAGE_WRITE, qsl_dev=qsl_t, seqs_dev=seq_t, num_reqs=B,
+                      recent_tokens=recent, sink_tokens_eff=self.sink_eff)
             self.layers.append((kc, vc, stage))
-        del hist_k, hist_v
         torch.cuda.synchronize()
-        # step inputs: 4 new tokens per request at positions L..L+3
+        # step inputs: n new tokens per request at positions L..L+n-1 (or, cache-only,
+        # n queries over the cached history)
         self.q = torch.randn(B * n, hq, d, generator=gen, device=dev).bfloat16()
-        self.k_new = outlier_kv(B * n, hk, d, gen, dev)
-        self.v_new = outlier_kv(B * n, hk, d, gen, dev)
-        npos = torch.arange(L, L + n, device=dev)
-        self.slots = (self.bt[:, npos // bs].long() * bs + npos % bs).reshape(-1).contiguous()
         self.qsl = [i * n for i in range(B + 1)]
-        self.seqs = [L + n] * B
+        self.q_rot = torch.empty_like(self.q)
+        if has_new:
+            self.k_new = outlier_kv(B * n, hk, d, gen, dev)
+            self.v_new = outlier_kv(B * n, hk, d, gen, dev)
+            sl = []
+            for r, L in enumerate(histories):
+                npos = torch.arange(L, L + n, device=dev)
+                sl.append(self.bt[r, npos // bs].long() * bs + npos % bs)
+            self.slots = torch.cat(sl).contiguous()
+            self.seqs = [L + n for L in histories]
+            self.k_rot = torch.empty_like(self.k_new)
+            self.v_rot = torch.empty_like(self.v_new)
+        else:
+            self.k_new = self.v_new = self.k_rot = self.v_rot = None
+            self.seqs = list(histories)
         self.qsl_dev = torch.tensor(self.qsl, dtype=torch.int32, device=dev)
         self.seq_dev = torch.tensor(self.seqs, dtype=torch.int32, device=dev)
-        self.q_rot = torch.empty_like(self.q)
-        self.k_rot = torch.empty_like(self.k_new)
-        self.v_rot = torch.empty_like(self.v_new)
         self.out_rot = torch.zeros(B * n, hq, d, dtype=torch.float32, device=dev)
         self.lse = torch.zeros(B * n, hq, dtype=torch.float32, device=dev)
         self.out = torch.empty(B * n, hq, d, dtype=torch.bfloat16, device=dev)
-        self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=True, num_kv_heads=hk,
+        self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=has_new, num_kv_heads=hk,
                                     group=hq // hk, head_dim=d, device=dev)
 
     def step(self, layer, phases=0):
@@ -132,11 +157,14 @@ class Setup:
 
         c = CONFIG
         kc, vc, stage = self.layers[layer]
-        ops.store(self.k_new, self.v_new, kc, vc, self.slots, head_dim=c["d"], rk=self.rk,
-                  rv=self.rv, stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
-                  seqs_dev=self.seq_dev, num_reqs=c["requests"], recent_tokens=c["recent_tokens"],
-                  sink_tokens_eff=self.sink_eff, query=self.q, query_rot=self.q_rot,
-                  key_rot=self.k_rot, value_rot=self.v_rot)
+        if self.has_new:
+            ops.store(self.k_new, self.v_new, kc, vc, self.slots, head_dim=c["d"], rk=self.rk,
+                      rv=self.rv, stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
+                      seqs_dev=self.seq_dev, num_reqs=len(self.seqs),
+                      recent_tokens=c["recent_tokens"], sink_tokens_eff=self.sink_eff, query=self.q,
+                      query_rot=self.q_rot, key_rot=self.k_rot, value_rot=self.v_rot)
+        else:
+            ops.rotate(self.q, self.rk, out=self.q_rot)
         self.attention(layer)
         ops.rotate(self.out_rot, self.rv, transpose=True, out_dtype=torch.bfloat16, out=self.out)
 
@@ -154,44 +182,45 @@ class Setup:
         _, _, (_, _, owner) = self.layers[0]
         own = owner.cpu().numpy()
         bt = self.bt.cpu().numpy().astype(np.int64)
-        bs, L = c["block_size"], c["history"]
-        pos = np.arange(L)
+        bs = c["block_size"]
         counts = []
-        for r in range(c["requests"]):
+        for r, L in enumerate(self.histories):
+            pos = np.arange(L)
             blk = bt[r, pos // bs]
             counts.append(int((own[blk % own.shape[0], pos % bs] == blk).sum()))
         return counts
 
-
-def algorithmic_bytes(staged):
-    """Unique bytes the attention pass must touch (history codes+meta, staged FP32
-    window, page-table entries, q, current k/v, owner tags) and the op's outputs."""
-    c = CONFIG
-    L, n, hq, hk, d, bs = c["history"], c["q_len"], c["hq"], c["hk"], c["d"], c["block_size"]
-    per_req = [136 * L + 2048 * s + 4 * math.ceil(L / bs) + 2 * n * hq * d + 4 * n * hk * d
-               for s in staged]
-    owner = 8 * math.ceil(c["staging_tokens"] / bs) * bs
-    b_main = sum(per_req) + owner
-    b_out = c["requests"] * n * hq * (2 * d + 4)
-    return b_main, b_main + b_out
+    def algorithmic_bytes(self, staged):
+        """Unique bytes the attention pass must touch (history codes+meta, staged FP32
+        window, page-table entries, q, current k/v, owner tags) and the op's outputs."""
+        c = CONFIG
+        n, hq, hk, d, bs = self.n, c["hq"], c["hk"], c["d"], c["block_size"]
+        per_req = [136 * L + 2048 * s + 4 * math.ceil(L / bs) + 2 * n * hq * d
+                   + (4 * n * hk * d if self.has_new else 0)
+                   for L, s in zip(self.histories, staged)]
+        owner = 8 * math.ceil(c["staging_tokens"] / bs) * bs
+        b_main = sum(per_req) + owner
+        b_out = len(self.histories) * n * hq * (2 * d + 4)
+        return b_main, b_main + b_out
 
 
 def time_graph(setup, steps, warmup):
     """Whole-step time: a HIP graph of LAYERS layer steps replayed steps/LAYERS times."""
-    for i in range(max(warmup, LAYERS)):
-        setup.step(i % LAYERS)
+    nl = len(setup.layers)
+    for i in range(max(warmup, nl)):
+        setup.step(i % nl)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
-            for layer in range(LAYERS):
+            for layer in range(nl):
                 setup.step(layer)
     torch.cuda.current_stream().wait_stream(stream)
     graph.replay()
     torch.cuda.synchronize()
-    reps = max(1, steps // LAYERS)
+    reps = max(1, steps // nl)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -201,25 +230,178 @@ def time_graph(setup, steps, warmup):
     t1.record()
     torch.cuda.synchronize()
     wall = t0.elapsed_time(t1)
-    return wall / (reps * LAYERS), reps * LAYERS
+    return wall / (reps * nl), reps * nl
 
 
-def time_main_kernel(setup, reps=8):
-    """Average duration of attn_main alone: a spin kernel keeps the stream busy while the
-    host enqueues event -> kernel -> event, so the pair brackets only the kernel."""
+def time_main_kernel(setup, reps=10):
+    """Average attn_main duration: a HIP graph of the split-K pass over every layer,
+    replayed back to back and bracketed by events on the launch stream (the per-launch
+    period includes the short gap between graph nodes)."""
+    nl = len(setup.layers)
+    for layer in range(nl):
+        setup.attention(layer, phases=1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for layer in range(nl):
+                setup.attention(layer, phases=1)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) / nl)
+    per = np.array(per)
+    return float(np.median(per)), float(per.mean())
+
+
+def event_ms(fn, reps=20, warm=3):
+    """Median duration (ms) of fn(r) bracketed by events behind a spin kernel."""
     durs = []
-    for r in range(reps):
-        for layer in range(LAYERS):
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda._sleep(2_000_000)
-            e0.record()
-            setup.attention(layer, phases=1)
-            e1.record()
-            e1.synchronize()
+    for r in range(reps + warm):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
+        e0.record()
+        fn(r)
+        e1.record()
+        e1.synchronize()
+        if r >= warm:
             durs.append(e0.elapsed_time(e1))
-    durs = np.array(durs[LAYERS:])  # first pass over the layers is warm-up
-    return float(np.median(durs)), float(durs.mean())
+    return float(np.median(durs))
+
+
+def config_decode(dev, name, histories, q_len, has_new, layers, steps, warmup):
+    """Decode-shaped configs (3, 4b): whole-step KV-token throughput + attn_main roofline."""
+    setup = Setup(dev, histories, q_len, has_new, layers)
+    staged = setup.staged_counts()
+    b_main, _ = setup.algorithmic_bytes(staged)
+    ms_step, nsteps = time_graph(setup, steps, warmup)
+    med_ms, _ = time_main_kernel(setup)
+    achieved = b_main / (med_ms * 1e-3) / 1e9
+    kv_tokens = sum(setup.seqs)
+    return {"metric": f"INT2-KV attention tokens/s, {name}, one MI355X", "value": kv_tokens / (ms_step * 1e-3),
+            "unit": "KV-tokens/s", "n_gpus": 1, "steps": nsteps, "warmup": warmup, "ms_per_step": ms_step,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int2-kv/bf16",
+            "data": "synthetic",
+            "config": {"workload": name, "requests": len(histories), "history_total": sum(histories),
+                       "q_len": q_len, "has_new": has_new, "layers_cycled": layers,
+                       "staged_total": sum(staged)},
+            "roofline": {"bound": "hbm", "kernel": "attn_main_kernel<256>", "achieved": achieved,
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+                         "algorithmic_bytes": b_main, "kernel_us": med_ms * 1e3, "traffic": None}}
+
+
+def config_store(dev, reps=20, layers=4):
+    """Config 2: rotate + INT2 quantize + pack + scatter + FP32 window of 15360 tokens
+    (Hk 1, D 256) through a seeded shuffled slot_mapping, 5 % -1 and 2 % rewrites."""
+    from oscar_amd import ops
+    from oscar_amd._lib import STAGE_WRITE
+
+    c = CONFIG
+    N, hk, d, bs = 15360, 1, 256, c["block_size"]
+    gen = torch.Generator(device=dev).manual_seed(20261202)
+    g = np.random.default_rng(20261202)
+    nb = 2 * math.ceil(N / bs)
+    slots = g.permutation(nb * bs)[:N].astype(np.int64)
+    slots[g.random(N) < 0.05] = -1
+    for i in np.nonzero(g.random(N) < 0.02)[0]:
+        if i > 0:
+            slots[i] = slots[g.integers(0, i)]
+    k, v = outlier_kv(N, hk, d, gen, dev), outlier_kv(N, hk, d, gen, dev)
+    rk, rv = hadamard_rotation(d, gen, dev), hadamard_rotation(d, gen, dev).flip(0).contiguous()
+    rows = max(math.ceil(c["staging_tokens"] / bs), math.ceil(c["recent_tokens"] / bs) + 3)
+    sink_eff = (c["sink_tokens"] // bs) * bs
+    sl = torch.from_numpy(slots).to(dev)
+    qsl = torch.tensor([0, N], dtype=torch.int32, device=dev)
+    seqs = torch.tensor([N], dtype=torch.int32, device=dev)
+    caches = []
+    for _ in range(layers):
+        kc = torch.zeros(nb, bs, hk, d, dtype=torch.int8, device=dev)
+        caches.append((kc, torch.zeros_like(kc),
+                       (torch.zeros(rows, bs, hk, d, dtype=torch.float32, device=dev),
+                        torch.zeros(rows, bs, hk, d, dtype=torch.float32, device=dev),
+                        torch.full((rows, bs), -1, dtype=torch.int64, device=dev))))
+
+    def call(r):
+        kc, vc, stage = caches[r % layers]
+        ops.store(k, v, kc, vc, sl, head_dim=d, rk=rk, rv=rv, stage=stage, stage_mode=STAGE_WRITE,
+                  qsl_dev=qsl, seqs_dev=seqs, num_reqs=1, recent_tokens=c["recent_tokens"],
+                  sink_tokens_eff=sink_eff)
+
+    ms = event_ms(call, reps)
+    valid = slots >= 0
+    uniq = len(np.unique(slots[valid]))
+    # kept seats: the last writer of each seat is in the recent window (positions >= N - 256)
+    seat = (slots // bs % rows) * bs + slots % bs
+    last = {}
+    for t in np.nonzero(valid)[0]:
+        last[int(seat[t])] = t
+    kept = sum(1 for t in last.values() if t >= N - c["recent_tokens"] or t < sink_eff)
+    b_alg = 2 * N * 512 + 2 * d * d * 4 + 8 * N + 136 * uniq + 8 * uniq + 2048 * kept
+    flops = 2 * N * 2 * d * d
+    t = ms * 1e-3
+    return {"metric": "KV store tokens/s (rotate + INT2 pack + scatter + window), config 2, one MI355X",
+            "value": N / t, "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp64-accumulated rotation, int2 out",
+            "data": "synthetic",
+            "config": {"workload": "config 2: 15360 tokens, 5% -1 slots, 2% rewrites, window write",
+                       "unique_slots": uniq, "kept_window_seats": kept},
+            "roofline": {"bound": "fp64", "kernel": "store_rotate_kernel + store_quant_kernel",
+                         "achieved": flops / t / 1e12, "peak": 78.6, "unit": "TFLOP/s",
+                         "frac": flops / t / 1e12 / 78.6, "hbm_gbs": b_alg / t / 1e9,
+                         "hbm_frac": b_alg / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b_alg}}
+
+
+def config_prefill(dev, reps=5, layers=2):
+    """Config 5: long continuation (15360 INT2 history + 9256-token causal chunk, MFMA
+    path) and the history-free 2048-token prefill."""
+    from oscar_amd import ops
+
+    c = CONFIG
+    hist, nq, hq, hk, d = 15360, 9256, c["hq"], c["hk"], c["d"]
+    setup = Setup(dev, [hist], q_len=1, has_new=True, layers=layers, seed=20261205)
+    gen = torch.Generator(device=dev).manual_seed(20261206)
+    q = torch.randn(nq, hq, d, generator=gen, device=dev).bfloat16()
+    k, v = outlier_kv(nq, hk, d, gen, dev), outlier_kv(nq, hk, d, gen, dev)
+    out = torch.empty(nq, hq, d, dtype=torch.float32, device=dev)
+    lse = torch.empty(nq, hq, dtype=torch.float32, device=dev)
+    bs = c["block_size"]
+    row = torch.zeros(math.ceil((hist + nq) / bs), dtype=torch.int32, device=dev)
+    row[:setup.bt.shape[1]] = setup.bt[0]
+
+    def cont(r):
+        kc, vc, stage = setup.layers[r % layers]
+        ops.attention_prefill(q, k, v, setup.scale, head_dim=d, history=hist, k_cache=kc, v_cache=vc,
+                              block_table_row=row, stage=stage, out=out, lse=lse)
+
+    ms = event_ms(cont, reps, warm=1)
+    flops = 4 * d * hq * (nq * hist + nq * (nq + 1) // 2)
+    nf = 2048
+    qf = torch.randn(nf, hq, d, generator=gen, device=dev).bfloat16()
+    kf, vf = outlier_kv(nf, hk, d, gen, dev), outlier_kv(nf, hk, d, gen, dev)
+    outf = torch.empty(nf, hq, d, dtype=torch.bfloat16, device=dev)
+    ms_f = event_ms(lambda r: ops.attention_prefill(qf, kf, vf, setup.scale, head_dim=d, out=outf), reps, warm=1)
+    flops_f = 4 * d * hq * (nf * (nf + 1) // 2)
+    t = ms * 1e-3
+    return {"metric": "continuation prefill TFLOP/s (15360 INT2 history + 9256 causal), config 5, one MI355X",
+            "value": flops / t / 1e12, "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "config 5: continuation 15360 + 9256; fresh-only 2048",
+                       "fresh_2048_ms": ms_f, "fresh_2048_tflops": flops_f / (ms_f * 1e-3) / 1e12},
+            "roofline": {"bound": "mfma", "kernel": "prefill_kernel<256>", "achieved": flops / t / 1e12,
+                         "peak": 2500.0, "unit": "TFLOP/s", "frac": flops / t / 1e12 / 2500.0,
+                         "algorithmic_flops": flops}}
 
 
 def cpu_baseline(setup, budget_s=25.0, max_cores=16):
@@ -333,6 +515,9 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=320)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--config", default="4a", choices=["4a", "2", "3", "4b", "5"],
+                    help="4a (default, the headline metric); 2 store; 3 single-request MTP; "
+                         "4b 64 cache-only decodes; 5 continuation prefill")
     ap.add_argument("--profile-main", action="store_true",
                     help="only run attn_main over the layer caches plus a calibration copy "
                          "(the workload of the rocprofv3 --pmc passes)")
@@ -363,13 +548,27 @@ def main(argv=None):
 
     _lib.load()
     dev = torch.device("cuda", 0)
+    if args.config != "4a":
+        if args.config == "2":
+            rec = config_store(dev)
+        elif args.config == "3":
+            rec = config_decode(dev, "config 3: 1 x (24576 INT2 history + 4-token MTP)", [24576], 4,
+                                True, LAYERS, args.steps, args.warmup)
+        elif args.config == "4b":
+            hist = np.random.default_rng(20261204).integers(1024, 32769, 64).tolist()
+            rec = config_decode(dev, "config 4b: 64 cache-only 1-token decodes, history U[1024, 32768]",
+                                hist, 1, False, 4, args.steps, args.warmup)
+        else:
+            rec = config_prefill(dev)
+        print(json.dumps(rec), flush=True)
+        return 0
     log("building 16 layer caches (history store)")
     setup = Setup(dev)
     if args.profile_main:
         profile_main(setup)
         return 0
     staged = setup.staged_counts()
-    b_main, b_op = algorithmic_bytes(staged)
+    b_main, b_op = setup.algorithmic_bytes(staged)
     log(f"staged history tokens per request: {staged}; B_main={b_main} B_op={b_op}")
     ms_step, steps = time_graph(setup, args.steps, args.warmup)
     log(f"step {ms_step * 1e3:.2f} us ({steps} steps)")
