@@ -213,8 +213,13 @@ typedef struct oscar_prefill_args_v1 {
   void* out;                    /* [n, Hq, D]: bf16 when history == 0, else fp32 rotated */
   int64_t out_stride_token;
   float* lse;                   /* [n, Hq] or NULL */
+  /* history > 0: 16-byte aligned scratch for the history's bf16 K/V values,
+   * >= oscar_prefill_workspace_bytes_v1(history, num_kv_heads, head_dim) */
+  void* workspace;
+  int64_t workspace_bytes;
 } oscar_prefill_args_v1;
 
+int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim);
 int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream);
 
 const char* oscar_last_error(void);

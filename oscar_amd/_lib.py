@@ -74,7 +74,7 @@ class PrefillArgs(C.Structure):
         ("num_tokens", i64), ("num_q_heads", i64), ("num_kv_heads", i64), ("head_dim", i64),
         ("history", i64), ("cache", Cache), ("block_table_row", vp),
         ("staging", C.POINTER(Staging)), ("scale", f32), ("out", vp),
-        ("out_stride_token", i64), ("lse", vp),
+        ("out_stride_token", i64), ("lse", vp), ("workspace", vp), ("workspace_bytes", i64),
     ]
 
 
@@ -89,6 +89,7 @@ SIGNATURES = {
                                      i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
                                      C.POINTER(Plan)]),
     "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),
     "oscar_attn_prefill_v1": (C.c_int, [C.POINTER(PrefillArgs), vp]),
 }
 

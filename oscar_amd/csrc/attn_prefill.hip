@@ -5,14 +5,23 @@
 // and the long-continuation use of slab_attention.py:376-476 (history waves plus
 // the causal current chunk, rotated domain, fp32 out + LSE).
 //
-// Query i (0-based in the chunk) sees keys [0, history + i + 1).  A workgroup of
-// four waves owns 128 query rows (rows = tokens x heads of one KV head, GQA
-// packed); key tiles of 32 are staged in LDS as bf16 values with the reference
-// rounding (history: q_dtype(fp16(code*scale + zero)) or the staged fp32 value when
-// the seat's owner tag matches; current chunk: the given bf16 values) and shared
-// by the four waves.  Each wave: S^T = K Q^T (v_mfma_f32_32x32x16_bf16), online
-// softmax in fp32 (log2 domain), O^T += V^T P^T with V^T read from LDS by
-// ds_read_b64_tr_b16.
+// Query i (0-based in the chunk) sees keys [0, history + i + 1).
+//
+// Two launches when there is a history:
+//   history_bf16_kernel  the history's K/V values with the reference rounding
+//                        (q_dtype(fp16(code*scale + zero)), or the staged fp32 value
+//                        when the seat's owner tag matches, prepare_kv.py:77) into a
+//                        caller-provided bf16 workspace, once per call: every query
+//                        tile of a long chunk reuses them;
+//   prefill_kernel       flash attention over [workspace history | current chunk].
+//                        A workgroup of four waves owns 128 query rows (tokens x heads
+//                        of one KV head, GQA packed; Q^T operands in LDS).  Key tiles of
+//                        32 are double-buffered in LDS: each thread prefetches its
+//                        share of tile t+2 into registers while tile t is computed, so
+//                        one barrier per tile separates the buffers.  Per wave:
+//                        S^T = K Q^T (v_mfma_f32_32x32x16_bf16), online softmax in fp32
+//                        (log2 domain) with a lazy reference max, O^T += V^T P^T with
+//                        V^T read from LDS by ds_read_b64_tr_b16.
 #include "common.h"
 
 namespace oscar {
@@ -25,7 +34,11 @@ constexpr int kKeys = 32;
 constexpr int kRows = 128;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazy = 8.f;  // max drift (log2 units) before O is rescaled
+constexpr int kQK = 4;        // QK K-steps whose LDS operands are read together
 typedef short __attribute__((ext_vector_type(4))) i16x4;
+typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
+typedef float __attribute__((ext_vector_type(2))) f32x2;
 
 __device__ __forceinline__ float round_hist_bf16(float x) {
   float h = __half2float(__float2half_rn(x));
@@ -37,8 +50,70 @@ struct PrefillParams {
   oscar_staging_v1 st;
   int has_stage;
   int group;
-  int qtok;  // query tokens per workgroup
+  int qtok;            // query tokens per workgroup
+  uint16_t* hist_k;    // [history][Hk][D] bf16 history values (workspace)
+  uint16_t* hist_v;
 };
+
+// one wave per (history token, kv head): lane l holds elements E*l .. E*l+E-1
+template <int D>
+__global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
+  constexpr int E = D / 64;
+  const oscar_prefill_args_v1& A = P.a;
+  const int64_t hk = A.num_kv_heads;
+  const int64_t vec = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (vec >= A.history * hk) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t p = vec / hk, h = vec % hk;
+  const int64_t bs = A.cache.block_size;
+  int64_t blk = A.block_table_row[p / bs];
+  if (blk < 0 || blk >= A.cache.num_blocks) blk = 0;  // host validates; never fault
+  const int64_t off = p % bs;
+  int64_t seat = 0;
+  bool staged = false;
+  if (P.has_stage) {
+    seat = (blk % P.st.rows) * bs + off;
+    staged = P.st.owner[seat] == blk;
+  }
+  float kv[E], vv[E];
+  if (staged) {
+    const float* sk = P.st.stage_k + (seat * hk + h) * D + E * lane;
+    const float* sv = P.st.stage_v + (seat * hk + h) * D + E * lane;
+#pragma unroll
+    for (int i = 0; i < E; ++i) { kv[i] = sk[i]; vv[i] = sv[i]; }
+  } else {
+    const uint8_t* ks = A.cache.k + blk * A.cache.k_stride[0] + off * A.cache.k_stride[1] + h * A.cache.k_stride[2];
+    const uint8_t* vs = A.cache.v + blk * A.cache.v_stride[0] + off * A.cache.v_stride[1] + h * A.cache.v_stride[2];
+    const unsigned m0 = *(const unsigned*)ks, m1 = *(const unsigned*)(ks + 4);
+    const float sk = f16_bits_to_f32(m0 & 0xffff), zk = f16_bits_to_f32(m0 >> 16);
+    const float sv = f16_bits_to_f32(m1 & 0xffff), zv = f16_bits_to_f32(m1 >> 16);
+    const int e0 = E * lane;  // element e sits in byte e / 4, bits 2 (e % 4)
+    const unsigned kb = ks[32 + e0 / 4], vb = vs[e0 / 4];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int sh = 2 * ((e0 + i) & 3);
+      kv[i] = __fadd_rn(__fmul_rn((float)((kb >> sh) & 3u), sk), zk);
+      vv[i] = __fadd_rn(__fmul_rn((float)((vb >> sh) & 3u), sv), zv);
+    }
+  }
+  unsigned kw[E / 2], vw[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 2; ++i) {
+    kw[i] = (unsigned)f32_to_bf16_bits(round_hist_bf16(kv[2 * i])) |
+            ((unsigned)f32_to_bf16_bits(round_hist_bf16(kv[2 * i + 1])) << 16);
+    vw[i] = (unsigned)f32_to_bf16_bits(round_hist_bf16(vv[2 * i])) |
+            ((unsigned)f32_to_bf16_bits(round_hist_bf16(vv[2 * i + 1])) << 16);
+  }
+  uint16_t* dk = P.hist_k + vec * D + E * lane;
+  uint16_t* dv = P.hist_v + vec * D + E * lane;
+  if constexpr (E == 4) {
+    *(u32x2*)dk = u32x2{kw[0], kw[1]};
+    *(u32x2*)dv = u32x2{vw[0], vw[1]};
+  } else {
+    *(unsigned*)dk = kw[0];
+    *(unsigned*)dv = vw[0];
+  }
+}
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
@@ -53,10 +128,53 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   const int64_t q1 = (q0 + P.qtok < A.num_tokens) ? q0 + P.qtok : A.num_tokens;
   const int64_t hist = A.history;
   const int64_t nkeys = hist + q1;  // keys visible to the last query of the tile
+  const int64_t hk = A.num_kv_heads;
 
-  // rows padded by 16 bytes so that 16-byte reads of consecutive keys hit distinct banks
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kKeys][D + 8];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[kKeys][D + 8];
+  // double-buffered key tiles.  K rows are padded by 16 bytes (row-per-lane 16-byte
+  // reads of 8 consecutive keys cover all banks), V rows by 32 bytes (the transpose
+  // reads of 4 consecutive keys x 32 bytes cover all banks)
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKeys][D + 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKeys][D + 16];
+  // each wave's Q^T operands (K-step j, lane l), read at each use
+  __shared__ __attribute__((aligned(16))) u32x4 s_q[kWaves][D / 16][64];
+
+  // fill mapping: pass i, thread -> key i * KPP + tid / CPR, 16-byte column tid % CPR,
+  // so that a wave reads (and stores to LDS) whole contiguous key rows
+  constexpr int CPR = D / 8;              // 16-byte columns per key row
+  constexpr int KPP = kThreads / CPR;     // keys per pass
+  constexpr int NPASS = kKeys / KPP;
+  const int fkey = tid / CPR, fcol = tid % CPR;
+  u32x4 kr[NPASS], vr[NPASS];
+  // branch-free, 32-bit element offsets (the host checks they fit): keys past the
+  // chunk read current-chunk row 0, finite data whose scores the causal mask removes
+  const uint16_t* hk_base = P.hist_k + kvh * D + 8 * fcol;
+  const uint16_t* hv_base = P.hist_v + kvh * D + 8 * fcol;
+  const uint16_t* ck_base = (const uint16_t*)A.k + kvh * D + 8 * fcol;
+  const uint16_t* cv_base = (const uint16_t*)A.v + kvh * D + 8 * fcol;
+  const int hrow = (int)(hk * D), crow = (int)A.kv_stride_token;
+  const int ihist = (int)hist, ikeys = (int)nkeys;
+  auto fetch = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+      const int p = kt * kKeys + i * KPP + fkey;
+      const bool in_hist = p < ihist;
+      const int ci = (in_hist || p >= ikeys) ? 0 : p - ihist;  // current-chunk index
+      const uint16_t* ks = in_hist ? hk_base + (unsigned)(p * hrow) : ck_base + (unsigned)(ci * crow);
+      const uint16_t* vs = in_hist ? hv_base + (unsigned)(p * hrow) : cv_base + (unsigned)(ci * crow);
+      kr[i] = *(const u32x4*)ks;
+      vr[i] = *(const u32x4*)vs;
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+      *(u32x4*)&s_k[buf][i * KPP + fkey][8 * fcol] = kr[i];
+      *(u32x4*)&s_v[buf][i * KPP + fkey][8 * fcol] = vr[i];
+    }
+  };
+
+  const int ktiles = (int)((nkeys + kKeys - 1) / kKeys);
+  fetch(0);
 
   // this lane's row
   const int n = wave * 32 + m;
@@ -64,12 +182,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   const bool row_ok = (n < P.qtok * G) && (qi < q1);
   const int head = kvh * G + n % G;
   const uint16_t* qrow = (const uint16_t*)A.q + (row_ok ? qi : 0) * A.q_stride_token + (int64_t)head * D;
-  bf16x8 qb[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      qb[j][e] = __builtin_bit_cast(__bf16, (unsigned short)(row_ok ? qrow[16 * j + 8 * g + e] : 0));
+    s_q[wave][j][lane] = row_ok ? *(const u32x4*)(qrow + 16 * j + 8 * g) : u32x4{0u, 0u, 0u, 0u};
   const float c = A.scale * kLog2e;
   const int64_t limit = hist + qi + 1;  // keys [0, limit) visible to this row
 
@@ -80,127 +195,117 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[b][r] = 0.f;
 
-  const int64_t bs = A.cache.block_size;
-  const int64_t hk = A.num_kv_heads;
-  const int ktiles = (int)((nkeys + kKeys - 1) / kKeys);
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int64_t k0 = (int64_t)kt * kKeys;
-    __syncthreads();
-    // ---- fill: thread -> (key, 8 d-chunks of D/8)
-    {
-      const int kk = tid >> 3, dc = tid & 7;
-      const int64_t p = k0 + kk;
-      constexpr int W = D / 8;
-      float kv[W], vv[W];
-      if (p < hist) {
-        int64_t blk = A.block_table_row[p / bs];
-        if (blk < 0 || blk >= A.cache.num_blocks) blk = 0;  // host validates; never fault
-        const int64_t off = p % bs;
-        bool staged = false;
-        const int64_t seat = P.has_stage ? (blk % P.st.rows) * bs + off : 0;
-        if (P.has_stage) staged = P.st.owner[seat] == blk;
-        if (staged) {
-          const float* sk = P.st.stage_k + (seat * hk + kvh) * D + dc * W;
-          const float* sv = P.st.stage_v + (seat * hk + kvh) * D + dc * W;
+  stash(0);
+  if (ktiles > 1) fetch(1);
+  __syncthreads();
+  // The tile loop does no VALU work on O (kept in AGPRs by the MFMAs): a tile whose
+  // row max drifts more than kLazy above the reference leaves the loop, O and l are
+  // rescaled once, and the loop resumes at that tile (its QK is recomputed).
+  int kt = 0;
+  float m_move = -INFINITY;  // per row: the max that forced the exit
+  while (true) {
+    for (; kt < ktiles; ++kt) {
+      const int buf = kt & 1;
+      const int64_t k0 = (int64_t)kt * kKeys;
+      // ---- S^T = K Q^T; the operands of kQK K-steps are read from LDS together so
+      // that one LDS latency covers kQK MFMAs
+      f32x16 S = {};
 #pragma unroll
-          for (int i = 0; i < W; ++i) { kv[i] = round_hist_bf16(sk[i]); vv[i] = round_hist_bf16(sv[i]); }
-        } else {
-          const uint8_t* ks = A.cache.k + blk * A.cache.k_stride[0] + off * A.cache.k_stride[1] + kvh * A.cache.k_stride[2];
-          const uint8_t* vs = A.cache.v + blk * A.cache.v_stride[0] + off * A.cache.v_stride[1] + kvh * A.cache.v_stride[2];
-          const unsigned m0 = *(const unsigned*)ks, m1 = *(const unsigned*)(ks + 4);
-          const float sk = f16_bits_to_f32(m0 & 0xffff), zk = f16_bits_to_f32(m0 >> 16);
-          const float sv = f16_bits_to_f32(m1 & 0xffff), zv = f16_bits_to_f32(m1 >> 16);
+      for (int j0 = 0; j0 < D / 16; j0 += kQK) {
+        bf16x8 ka[kQK], qa[kQK];
 #pragma unroll
-          for (int i = 0; i < W; i += 4) {
-            const unsigned kb = ks[32 + (dc * W + i) / 4], vb = vs[(dc * W + i) / 4];
+        for (int j = 0; j < kQK; ++j) {
+          ka[j] = *(const bf16x8*)&s_k[buf][m][16 * (j0 + j) + 8 * g];
+          qa[j] = __builtin_bit_cast(bf16x8, s_q[wave][j0 + j][lane]);
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              kv[i + j] = round_hist_bf16(__fadd_rn(__fmul_rn((float)((kb >> (2 * j)) & 3u), sk), zk));
-              vv[i + j] = round_hist_bf16(__fadd_rn(__fmul_rn((float)((vb >> (2 * j)) & 3u), sv), zv));
+        for (int j = 0; j < kQK; ++j) S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], S, 0, 0, 0);
+        // keep the group's LDS reads ahead of its MFMAs (one latency per group)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQK, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kQK, 0);
+      }
+      const bool full = (k0 + kKeys <= hist + q0 + 1);  // visible to every row of the tile
+      // masked keys get -inf scores (boundary tiles only).  Padding rows have zero
+      // queries and are never written, so they need no mask.
+      if (!full) {
+        const int lim = (int)(limit - k0);  // keys of the tile visible to this row
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int pk = 8 * (r >> 2) + 4 * g + (r & 3);
+          S[r] = pk >= lim ? -INFINITY : S[r];
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[r]);
+      {
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;  // c > 0
+      }
+      // a row's first visible key sets its reference (O and l are still zero there)
+      if (m_run == -INFINITY) m_run = mx;
+      if (__any(mx > m_run + kLazy)) {
+        m_move = mx;
+        break;
+      }
+      // p = 2^(S c - m) (exp2 of -inf is 0); rows with no key yet keep m = -inf and p = 0
+      const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
+      bf16x8 pb[2];
+      float lsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(S[r], c, nm));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(S[r + 1], c, nm));
+        lsum += p0 + p1;
+        const bf16x2 h = __builtin_convertvector(f32x2{p0, p1}, bf16x2);
+        pb[r >> 3][r & 7] = h[0];
+        pb[r >> 3][(r & 7) + 1] = h[1];
+      }
+      l_run += lsum;
+      // ---- O^T += V^T P^T; the V^T operands of two output blocks (8 transpose reads)
+      // are read together
+      const int G16 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+      for (int b0 = 0; b0 < D / 32; b0 += 2) {
+        bf16x8 va[2][2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
+              const uint16_t* addr = &s_v[buf][key][32 * (b0 + bb) + 16 * (G16 & 1) + 4 * (i16 & 3)];
+              auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) va[bb][s][4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
             }
-          }
-        }
-      } else if (p < nkeys) {
-        const int64_t ci = p - hist;  // current-chunk index
-        const uint16_t* kn = (const uint16_t*)A.k + ci * A.kv_stride_token + kvh * D + dc * W;
-        const uint16_t* vn = (const uint16_t*)A.v + ci * A.kv_stride_token + kvh * D + dc * W;
 #pragma unroll
-        for (int i = 0; i < W; ++i) { kv[i] = bf16_bits_to_f32(kn[i]); vv[i] = bf16_bits_to_f32(vn[i]); }
-      } else {
+        for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-        for (int i = 0; i < W; ++i) { kv[i] = 0.f; vv[i] = 0.f; }
+          for (int s = 0; s < 2; ++s)
+            O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
       }
-#pragma unroll
-      for (int i = 0; i < W; i += 8) {
-        u32x4 kw, vw;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          kw[j] = (unsigned)f32_to_bf16_bits(kv[i + 2 * j]) | ((unsigned)f32_to_bf16_bits(kv[i + 2 * j + 1]) << 16);
-          vw[j] = (unsigned)f32_to_bf16_bits(vv[i + 2 * j]) | ((unsigned)f32_to_bf16_bits(vv[i + 2 * j + 1]) << 16);
-        }
-        *(u32x4*)&s_k[kk][dc * W + i] = kw;
-        *(u32x4*)&s_v[kk][dc * W + i] = vw;
+      // the prefetched tile kt+1 goes to the other buffer (last read before the previous
+      // barrier), then tile kt+2 is prefetched; one barrier per tile
+      if (kt + 1 < ktiles) {
+        stash(buf ^ 1);
+        if (kt + 2 < ktiles) fetch(kt + 2);
       }
+      __syncthreads();
     }
-    __syncthreads();
-    // ---- S^T = K Q^T
-    f32x16 S = {};
+    if (kt >= ktiles) break;
+    // rare: rescale to the new reference and redo tile kt (its buffers are intact)
+    const bool move = m_move > m_run + kLazy;
+    const float f = move ? exp2f(m_run - m_move) : 1.f;
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-      const bf16x8 ka = *(const bf16x8*)&s_k[m][16 * j + 8 * g];
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[j], S, 0, 0, 0);
-    }
-    const bool full = (k0 + kKeys <= hist + q0 + 1);  // visible to every row of the tile
-    float xs[16];
-    float mx = -INFINITY;
+    for (int b = 0; b < D / 32; ++b)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t p = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-      const bool vis = row_ok && (full || p < limit);
-      xs[r] = vis ? S[r] * c : -INFINITY;
-      mx = fmaxf(mx, xs[r]);
-    }
-    {
-      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    const float m_new = fmaxf(m_run, mx);
-    if (__any(m_new > m_run)) {
-      const float f = (m_new == m_run) ? 1.f : (m_run == -INFINITY ? 0.f : exp2f(m_run - m_new));
-#pragma unroll
-      for (int b = 0; b < D / 32; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) O[b][r] *= f;
-      l_run *= f;
-    }
-    m_run = m_new;
-    bf16x8 pb[2];
-    float lsum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pr = (xs[r] == -INFINITY) ? 0.f : exp2f(xs[r] - m_run);
-      lsum += pr;
-      pb[r >> 3][r & 7] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(pr));
-    }
-    l_run += lsum;
-    // ---- O^T += V^T P^T; A operand (V^T) via transpose reads of s_v
-    const int G16 = lane >> 4, i16 = lane & 15;
-#pragma unroll
-    for (int b = 0; b < D / 32; ++b) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        bf16x8 va;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
-          const uint16_t* addr = &s_v[key][32 * b + 16 * (G16 & 1) + 4 * (i16 & 3)];
-          auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) va[4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
-        }
-        O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[s], O[b], 0, 0, 0);
-      }
-    }
+      for (int r = 0; r < 16; ++r) O[b][r] *= f;
+    l_run *= f;
+    if (move) m_run = m_move;
   }
   // ---- finalize: row n = lane's row; O^T block b register r holds d = 32b + out_row(r, g)
   float l_tot;
@@ -230,6 +335,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
 
 using namespace oscar;
 
+extern "C" int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim) {
+  if (history <= 0) return 0;
+  return 2 * history * num_kv_heads * head_dim * (int64_t)sizeof(uint16_t);
+}
+
 extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream) {
   if (!args) return fail(-22, "oscar_attn_prefill_v1: null args");
   const oscar_prefill_args_v1& a = *args;
@@ -244,15 +354,37 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
   if (a.history < 0) return fail(-22, "oscar_attn_prefill_v1: negative history");
   if (a.history > 0 && (!a.cache.k || !a.cache.v || !a.block_table_row || a.cache.head_dim != D))
     return fail(-22, "oscar_attn_prefill_v1: history needs the cache and the block-table row");
+  // q/k/v rows and the history workspace are read as 16-byte vectors
+  if ((((uintptr_t)a.q) & 15) || (((uintptr_t)a.k) & 15) || (((uintptr_t)a.v) & 15) ||
+      ((a.q_stride_token * 2) & 15) || ((a.kv_stride_token * 2) & 15))
+    return fail(-22, "oscar_attn_prefill_v1: q/k/v rows must be 16-byte aligned");
+  // the prefill kernel addresses history and chunk rows with 32-bit element offsets
+  if ((a.history + 64) * a.num_kv_heads * D >= (1ll << 31) ||
+      (a.num_tokens + 64) * a.kv_stride_token >= (1ll << 31))
+    return fail(-22, "oscar_attn_prefill_v1: history or chunk too large for one call");
+  const int64_t need = oscar_prefill_workspace_bytes_v1(a.history, a.num_kv_heads, D);
+  if (a.history > 0 &&
+      (a.workspace == nullptr || a.workspace_bytes < need || (((uintptr_t)a.workspace) & 15)))
+    return fail(-22, "oscar_attn_prefill_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
   PrefillParams p{};
   p.a = a;
   p.has_stage = a.staging != nullptr;
   if (a.staging) p.st = *a.staging;
   p.group = G;
   p.qtok = kRows / G;
+  if (a.history > 0) {
+    p.hist_k = (uint16_t*)a.workspace;
+    p.hist_v = p.hist_k + a.history * a.num_kv_heads * D;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (a.history > 0) {
+    const unsigned hb = (unsigned)((a.history * a.num_kv_heads + 3) / 4);
+    if (D == 256) hipLaunchKernelGGL(history_bf16_kernel<256>, dim3(hb), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(history_bf16_kernel<128>, dim3(hb), dim3(256), 0, s, p);
+    OSCAR_CHECK_LAUNCH("history_bf16_kernel");
+  }
   const int ntq = (int)((a.num_tokens + p.qtok - 1) / p.qtok);
   dim3 grid(ntq, (unsigned)a.num_kv_heads);
-  hipStream_t s = (hipStream_t)stream;
   if (D == 256) hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(kThreads), 0, s, p);
   else hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, s, p);
   OSCAR_CHECK_LAUNCH("prefill_kernel");

@@ -74,6 +74,7 @@ class DeviceScratch:
         self.seat_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.store_ws = torch.empty(0, dtype=torch.uint8, device=device)
         self.attn_ws = torch.empty(0, dtype=torch.uint8, device=device)
+        self.prefill_ws = torch.empty(0, dtype=torch.uint8, device=device)
 
     @classmethod
     def get(cls, device: torch.device) -> "DeviceScratch":
@@ -97,6 +98,11 @@ class DeviceScratch:
         if self.store_ws.numel() < nbytes:
             self.store_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self.store_ws
+
+    def prefill_workspace(self, nbytes: int) -> torch.Tensor:
+        if self.prefill_ws.numel() < nbytes:
+            self.prefill_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.prefill_ws
 
     def attn_workspace(self, nbytes: int) -> torch.Tensor:
         if self.attn_ws.numel() < nbytes:
@@ -343,5 +349,9 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
     if lse is not None:
         a.lse = lse.data_ptr()
     lib = _lib.load()
+    if history > 0:
+        ws = DeviceScratch.get(q.device).prefill_workspace(
+            lib.oscar_prefill_workspace_bytes_v1(history, hk, head_dim))
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.oscar_attn_prefill_v1(C.byref(a), C.c_void_p(_stream(q.device))), "oscar_attn_prefill_v1")
     return out

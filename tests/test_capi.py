@@ -34,7 +34,7 @@ def header_functions() -> set:
 
 def test_library_exports_every_header_symbol(lib):
     names = header_functions()
-    assert len(names) == 8, names
+    assert len(names) == 9, names
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES)
