@@ -462,6 +462,9 @@ def profile_main(setup, reps=3, copy_mib=1024):
     caches, then two device copies of copy_mib MiB that calibrate FETCH/WRITE_SIZE: the
     runtime's blit copy and torch's vectorized elementwise kernel (16-byte lane loads
     and stores, the access width attn_main uses)."""
+    for layer in range(LAYERS):  # one full step per layer: rotated q / k / v and the window
+        setup.step(layer)
+    torch.cuda.synchronize()
     for r in range(reps):
         for layer in range(LAYERS):
             setup.attention(layer, phases=1)

@@ -9,37 +9,43 @@
 // block (then the FP32 staged value is used); keys >= the history length come from
 // the current (rotated, unquantized) chunk.
 //
-// Work decomposition: the host plan (oscar_attn_plan_v1) cuts every (request,
-// kv-head) key range into items of whole 32-token tiles, interleaved so that all
-// items of a group land on the same XCD.  One 256-thread workgroup (4 waves, one
-// per SIMD) per item; wave w takes tiles w, w+4, ...  Pages hold a multiple of 32
-// tokens, so a tile never straddles a page: its block id, seat row and in-page
-// offset are wave-uniform scalars.  The four wave partials are merged in LDS and
-// the item partial (normalised O in MFMA register order, natural-log LSE) goes to
-// the workspace with coalesced 16-byte stores; attn_merge_kernel combines the items
-// of each group (FP32 LSE merge, slab_attention.py:341-356) into out_rot / lse.
+// Work decomposition: the host plan (oscar_attn_plan_v1) deals the 32-token key
+// tiles of every (request, kv-head) group round-robin to items of at most T tiles
+// (T the smallest bound that fits the target item count).  One 512-thread
+// workgroup (8 waves, two per SIMD) per item; wave w takes item tiles w, w + 8, ...
+// Pages hold a multiple of 32 tokens, so a tile never straddles a page: its block
+// id, seat row and in-page offset are wave-uniform scalars.  The eight wave
+// partials are merged in LDS and the item partial (normalised O in MFMA register
+// order, natural-log LSE) goes to the workspace with coalesced 16-byte stores;
+// attn_merge_kernel combines the items of each group (FP32 LSE merge,
+// slab_attention.py:341-356) into out_rot / lse.
 //
-// Memory pipeline: each wave keeps kDepth tiles of packed data in flight (codes,
-// scales/zeros and owner tags of its next tiles are loaded into registers while the
-// current tile is computed), so HBM latency is paid once per wave, not per tile.
+// Prologue: the item record, then one round of loads for the page ids (lane i of a
+// wave: the wave's tile i) and the queries, then the first two tiles of every wave
+// and the owner tags of all its tiles.  The tags give each tile's staged-token mask
+// (owner tag == block); tiles with a staged token or past the fast range (current
+// chunk, causal boundary, ragged end) form the slow set.
 //
-// Tile math (one wave, 32 tokens x 32 rows, S^T = K Q^T then O^T += V^T P^T):
+// Fast tiles (INT2 history only, no staged token, no mask; one wave, 32 tokens x 32
+// rows, S^T = K Q^T then O^T += V^T P^T), with the next two tiles of the wave in
+// flight in two register slots:
 //  * QK (bf16 MFMA 32x32x16): the K operand holds exactly the reference's history
 //    values bf16(fp16(code*scale + zero)).  A token has only four of them; they form
-//    an 8-byte table and one v_perm_b32 per bf16 pair looks the codes up (selector
-//    2*code, 2*code+1), so scores and LSE carry the reference rounding.
-//  * PV fast tiles (INT2 history, no staged token, no mask; fp16 MFMA): V codes go
-//    to LDS in their natural layout and come back transposed with ds_read_b64_tr_b8
-//    (8 tokens x 1 byte = 4 codes per lane); one v_perm and one AND per fp16 pair
-//    give the subnormal c*2^(2k-24) for code bits 2k..2k+1, the B operand is
-//    P' = p*s_V (fp16, round to nearest) and sum_t p*z_V accumulates on the VALU.
-//  * slow tiles (staged tokens, current chunk, causal boundary, ragged end, or a
-//    score max far above the wave's reference max) are deferred until the fast
-//    tiles are done and the accumulators are in value units.  Their K/V values
-//    (rounded as the reference does) are built from the codes, the FP32 staged rows
-//    (loaded in batched rounds) and the current chunk (copied to LDS once per
-//    workgroup); V goes through LDS and is read transposed with ds_read_b64_tr_b16;
-//    P is split into bf16 hi + lo parts.
+//    byte tables and v_perm_b32 lookups turn 4 codes into 4 values, so scores and
+//    LSE carry the reference rounding.
+//  * PV (fp16 MFMA): V codes go to LDS in their natural layout and come back
+//    transposed with ds_read_b64_tr_b8 (8 tokens x 1 byte = 4 codes per lane); one
+//    v_perm and one AND per fp16 pair give the subnormal c*2^(2k-24) for code bits
+//    2k..2k+1, the B operand is P' = p*s_V (fp16, round to nearest) and
+//    sum_t p*z_V accumulates on the VALU.
+//  * softmax against a lazy reference max per row: it moves (rescaling O, l, z) only
+//    when a tile's max exceeds it by more than kLazy, so p <= 2^kLazy.
+//
+// Slow tiles run after the fast tiles, one at a time by the whole workgroup: the
+// staged FP32 rows go straight to LDS (global_load_lds; the first slow tile's while
+// the fast tiles run), all threads build the tile's K operands and V values in LDS
+// (staged rows, codes or current chunk, rounded as the reference does), and one
+// wave adds the tile to its softmax state with P split into bf16 hi + lo parts.
 #include <vector>
 
 #include "common.h"
@@ -50,10 +56,8 @@ namespace {
 
 constexpr int kWaves = 8;            // two waves per SIMD
 constexpr int kThreads = kWaves * 64;
-constexpr int kSlowWaves = 4;        // waves that run the queued slow tiles
 constexpr int kTile = 32;
-constexpr int kMaxCur = 32;          // current-chunk tokens of a request (rows <= 32)
-constexpr int kMaxItemTokens = 8192; // keys per item (64 tiles per wave)
+constexpr int kMaxItemTokens = 8192; // keys per item (32 tiles per wave)
 constexpr int kMaxPages = kMaxItemTokens / kTile + 2;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -71,7 +75,8 @@ struct Cfg {
   static constexpr int NB = D / 4;       // code bytes per token
   static constexpr int MBLK = D / 32;    // PV output blocks (32 d each)
   static constexpr int VROW = D + 8;     // bf16 per row of the slow-tile V buffer
-  static constexpr int CPR = 1;          // chunks per staged-row load round
+  static constexpr int TPR = 256 / D;     // tokens per 1-KB row of the slow-tile staged rows
+  static constexpr int SROW = 260;        // fp32 per such row (16-byte pad)
   static constexpr int NV = MBLK * 4 * 64;  // f32x4 of one item partial (register order)
 };
 
@@ -197,7 +202,6 @@ struct TileRegs {
   u32x4 k[Cfg<D>::NQ];  // this lane's half of the K codes
   u32x4 v[Cfg<D>::NQ];  // this lane's half of the V codes
   u32x2 meta;           // K scale, K zero, V scale, V zero (fp16)
-  int64_t own;          // owner tag of the token's staging seat
   int blk;              // physical block of the tile (0 off the history)
 };
 
@@ -237,16 +241,24 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // LDS
   __shared__ int32_t s_blk[kMaxPages];                 // block ids of the item's pages
   __shared__ int32_t s_seat[kMaxPages];                // their seat-row base (blk % rows) * bs
-  __shared__ __attribute__((aligned(16))) uint8_t s_vcode[kWaves][kTile * C::NB];
   __shared__ __attribute__((aligned(16))) float s_cst[kWaves][2][kTile];
   __shared__ __attribute__((aligned(16))) float s_ml[kWaves][2][32];
-  __shared__ __attribute__((aligned(16))) uint16_t s_cur[2][kMaxCur][D];  // current K / V
   __shared__ __attribute__((aligned(16))) u32x4 s_q[C::KSTEPS][64];        // Q^T operand
-  __shared__ int32_t s_nslow[kWaves];
-  __shared__ int16_t s_slow[kMaxItemTokens / kTile];   // queued slow tiles of all waves
-  // union: slow-tile V values (bf16, permuted columns) / cross-wave merge rounds
-  constexpr int kMergeBytes = kWaves * 2 * 4 * 64 * 16, kSlowBytes = kSlowWaves * kTile * C::VROW * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t s_big[kMergeBytes > kSlowBytes ? kMergeBytes : kSlowBytes];
+  __shared__ uint64_t s_slowset[kMaxItemTokens / kTile / 64];  // slow-set bits of the item tiles
+  __shared__ int16_t s_slow[kMaxItemTokens / kTile];             // the slow tiles, ascending
+  __shared__ uint32_t s_tmask[kMaxItemTokens / kTile]; // staged-token mask of every item tile
+  // union of the phases: V codes of each wave's current fast tile
+  // [kWaves][kTile * NB], then the slow tiles' staged FP32 K / V rows
+  // [2][kTile / TPR][SROW] (loaded while the fast tiles run), K operands (bf16 pairs
+  // in MFMA order) [kTile][2][NCH][8] and V values (bf16, permuted columns)
+  // [kTile][VROW]; after them, the cross-wave merge rounds of two output blocks
+  // [kWaves][2][4][64] f32x4 from the start
+  constexpr int kVcodeBytes = kWaves * kTile * C::NB;
+  constexpr int kRowsBytes = 2 * (kTile / C::TPR) * C::SROW * 4, kKopBytes = kTile * 2 * C::NCH * 8 * 4;
+  constexpr int kSlowBytes = kVcodeBytes + kRowsBytes + kKopBytes + kTile * C::VROW * 2;
+  constexpr int kMergeBytes = kWaves * 2 * 4 * 64 * 16;
+  __shared__ __attribute__((aligned(16))) uint8_t s_u[kSlowBytes > kMergeBytes ? kSlowBytes : kMergeBytes];
+  uint8_t (*s_vcode)[kTile * C::NB] = (uint8_t (*)[kTile * C::NB])s_u;
   const unsigned st_rows = (unsigned)P.st.rows;
 
   // wave w takes item tiles j = w + kWaves * i, i < my (my <= 32)
@@ -257,23 +269,33 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const int64_t vs0 = A.cache.v_stride[0], vs1 = A.cache.v_stride[1];
   const int64_t* owner = P.st.owner;
 
-  // ---- prologue.  Lane i < my of each wave fetches the page of the wave's tile i
-  // (kept in a register for the fast pass, and in LDS for the slow pass, which may
-  // run the tile on another wave), so the first tile loads go out before the
-  // workgroup barrier that publishes the queries and the current chunk.
+  // ---- prologue.  Three rounds of global loads, issued so that no wait queues
+  // behind a later round: (1) lane i < my of each wave loads the page of the wave's
+  // tile i (kept in a register for the fast pass, and in LDS for the slow pass, which
+  // may run the tile on another wave) and wave 0 loads the queries; (2) once the
+  // pages are in, the first two tiles of every wave; (3) the queries go to LDS while
+  // the tiles are in flight.
   int wblk = 0, wseat = 0;
   if (lane < my) {
-    const int j = wave + kWaves * lane;
-    const int t0 = tile_t0(j);
-    if (t0 < hist) {
-      const int32_t b = A.block_table[(int64_t)req * A.block_table_stride + t0 / bs];
-      // ids outside the cache are clamped (the host validates tables; this keeps a
-      // bad table from faulting)
-      wblk = (b < 0 || b >= A.cache.num_blocks) ? 0 : b;
-    }
+    const int t0 = tile_t0(wave + kWaves * lane);
+    if (t0 < hist) wblk = A.block_table[(int64_t)req * A.block_table_stride + t0 / bs];
+  }
+  const int n = m;
+  const bool row_ok = n < nrows;
+  u32x4 qv[2 * C::NCH];
+  if (wave == 0) {
+    const int qtok = qa + (row_ok ? n / G : 0);
+    const int qhead = kvh * G + (row_ok ? n % G : 0);
+    const uint16_t* qrow = (const uint16_t*)A.q + (int64_t)qtok * A.q_stride_token + (int64_t)qhead * D + g * (D / 2);
+#pragma unroll
+    for (int c = 0; c < 2 * C::NCH; ++c) qv[c] = *(const u32x4*)(qrow + 8 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep round 1 ahead of round 2
+  if (lane < my) {
+    // ids outside the cache are clamped (the host validates tables; this keeps a
+    // bad table from faulting)
+    wblk = (wblk < 0 || wblk >= A.cache.num_blocks) ? 0 : wblk;
     wseat = P.has_stage ? (int)((unsigned)wblk % st_rows) * bs : 0;
-    s_blk[j] = wblk;
-    s_seat[j] = wseat;
   }
 
   // page of item tile j < count, first key t0 (wave-uniform): block, in-page offset
@@ -298,7 +320,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     const bool real = j < count && t0 < hist;
     const int off0 = real ? t0 % bs : 0;
     r.blk = real ? __builtin_amdgcn_readlane(wblk, ti) : 0;
-    const int seat0 = real ? __builtin_amdgcn_readlane(wseat, ti) : 0;
     const int off = off0 + m;
     const uint8_t* ks = kbase + (int64_t)r.blk * ks0 + (int64_t)off * ks1;
     const uint8_t* vs = vbase + (int64_t)r.blk * vs0 + (int64_t)off * vs1;
@@ -308,42 +329,45 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       r.v[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
     }
     r.meta = *(const u32x2*)ks;
-    // without a staging arena the tag is read from the item record (never matches)
-    const int64_t* op = P.has_stage ? owner + seat0 + off : (const int64_t*)it;
-    r.own = *op;
   };
 
-  // the wave's first two tiles (register slots A and B, see the main loop)
+  // round 2: the wave's first two tiles (register slots A and B, see the main loop)
+  // and the owner tags of the wave's tiles (lanes 0-31 the even tiles, 32-63 the
+  // odd ones), whose low words decide (tags are -1 or block ids < 2^31)
   const int last = my > 0 ? my - 1 : 0;
   TileRegs<D> RA, RB;
   load_tile(0, RA);
   load_tile(1 < last ? 1 : last, RB);
-
-  // current chunk (tail items) and queries to LDS
-  bool any_cur_tile = false;
-  if (count > 0) any_cur_tile = has_new && tile_t0(count - 1) + kTile > hist;  // tiles ascend
-  if (any_cur_tile) {
-    constexpr int V8 = D / 8;
-    for (int e = tid; e < nq * V8; e += kThreads) {
-      const int t = e / V8, col = (e % V8) * 8;
-      const int64_t src = (int64_t)(qa + t) * A.kv_new_stride_token + (int64_t)kvh * D + col;
-      *(u32x4*)&s_cur[0][t][col] = *(const u32x4*)((const uint16_t*)A.k_new + src);
-      *(u32x4*)&s_cur[1][t][col] = *(const u32x4*)((const uint16_t*)A.v_new + src);
+  constexpr int kTagRounds = kMaxItemTokens / kTile / kWaves / 2;  // 16
+  int32_t tag[kTagRounds];
+  {
+    const int32_t* own32 = (const int32_t*)P.st.owner;
+#pragma unroll
+    for (int ii = 0; ii < kTagRounds; ++ii) {
+      tag[ii] = -1;
+      if (2 * ii < my) {
+        const int i = 2 * ii + g;
+        const int seat = __builtin_amdgcn_readlane(wseat, 2 * ii + 1 < my ? 2 * ii + 1 : 2 * ii);
+        const int seat_e = __builtin_amdgcn_readlane(wseat, 2 * ii);
+        const int t0 = tile_t0(wave + kWaves * i);
+        if (P.has_stage && i < my && t0 < hist) tag[ii] = own32[2 * ((int64_t)(g ? seat : seat_e) + t0 % bs + m)];
+      }
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // round 2 goes out before the LDS writes wait for round 1
+
+  if (lane < my) {
+    const int j = wave + kWaves * lane;
+    s_blk[j] = wblk;
+    s_seat[j] = wseat;
   }
   // queries: lane (row n = m, half g) holds q[n][g*D/2 .. +D/2) in the K-step order
   // of the code lookup (kpairs16); the Q^T operand of K-step j for lane l lives at
   // s_q[j][l] (shared by the waves)
-  const int n = m;
-  const bool row_ok = n < nrows;
   if (wave == 0) {
-    const int qtok = qa + (row_ok ? n / G : 0);
-    const int qhead = kvh * G + (row_ok ? n % G : 0);
-    const uint16_t* qrow = (const uint16_t*)A.q + (int64_t)qtok * A.q_stride_token + (int64_t)qhead * D + g * (D / 2);
 #pragma unroll
     for (int c = 0; c < C::NCH; ++c) {
-      u32x4 lo = *(const u32x4*)(qrow + 16 * c);
-      u32x4 hi = *(const u32x4*)(qrow + 16 * c + 8);
+      u32x4 lo = qv[2 * c], hi = qv[2 * c + 1];
       if (!row_ok) lo = hi = u32x4{0u, 0u, 0u, 0u};
       unsigned o[8];
       kpairs16(lo, hi, o);
@@ -368,7 +392,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 
   // Lazy: the reference max of a row only moves when a tile's max exceeds it by
   // more than kLazy (log2 units), so probabilities stay <= 2^kLazy and the O
-  // accumulators (kept in AGPRs by the MFMAs) are touched by the VALU only then.
+  // accumulators are touched by the VALU only then.
   auto update_max = [&](float mx) {
     const bool move = mx > m_run + kLazy;  // also true for the first finite max
     if (__any(move)) {
@@ -386,15 +410,246 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     }
   };
 
+  // ---------------------------------------------------------------- slow tiles
+  // The slow set: tiles with a staged token (owner tag == block, from the tags
+  // loaded in the prologue) or past the fast range (current chunk, causal
+  // boundary, ragged end).  The fast tiles skip them; they run after the fast
+  // tiles, one at a time by the whole workgroup: (1) the staged FP32 rows of the
+  // tile's staged tokens go straight to LDS (for the first slow tile while the fast
+  // tiles run), and every
+  // thread loads the codes, constants or current-chunk values of its share (token
+  // tid / 16); (2) the threads build the tile's K operands and V values into LDS
+  // with the reference rounding; (3) one wave (round-robin) adds the tile to its
+  // softmax state (the wave states are merged at the end).
+#pragma unroll
+  for (int ii = 0; ii < kTagRounds; ++ii) {
+    if (2 * ii >= my) break;
+    const int i = 2 * ii + g, j = wave + kWaves * i;
+    const int blk_e = __builtin_amdgcn_readlane(wblk, 2 * ii);
+    const int blk_o = __builtin_amdgcn_readlane(wblk, 2 * ii + 1 < my ? 2 * ii + 1 : 2 * ii);
+    const bool staged = i < my && tile_t0(j) + m < hist && tag[ii] == (g ? blk_o : blk_e);
+    const uint64_t b = __ballot(staged);
+    if (lane == 0) {
+      s_tmask[wave + kWaves * 2 * ii] = (uint32_t)b;
+      if (2 * ii + 1 < my) s_tmask[wave + kWaves * (2 * ii + 1)] = (uint32_t)(b >> 32);
+    }
+  }
+  __syncthreads();
+  if (wave < (kMaxItemTokens / kTile) / 64) {
+    const int j = 64 * wave + lane;
+    const bool slow = j < count && (s_tmask[j] != 0 || tile_t0(j) + kTile > fast_end);
+    const uint64_t b = __ballot(slow);
+    if (lane == 0) s_slowset[wave] = b;
+  }
+  __syncthreads();
+  // the slow list (ascending tile order), and bit i of myslow = slow tile i of
+  // this wave (tile wave + kWaves * i)
+  int nslow = 0;
+#pragma unroll
+  for (int w = 0; w < (kMaxItemTokens / kTile) / 64; ++w) {
+    const uint64_t word = s_slowset[w];
+    if (tid >> 6 == w && ((word >> lane) & 1ull)) s_slow[nslow + __popcll(word & ((1ull << lane) - 1ull))] = (int16_t)tid;
+    nslow += __popcll(word);
+  }
+  nslow = __builtin_amdgcn_readfirstlane(nslow);
+  const int jl = (wave + kWaves * lane) & (kMaxItemTokens / kTile - 1);  // lanes >= my: any in-range index
+  const uint32_t myslow = (uint32_t)__ballot(lane < my && ((s_slowset[jl >> 6] >> (jl & 63)) & 1ull));
+  __syncthreads();
+  float* s_rows = (float*)(s_u + kVcodeBytes);                            // [2][kTile / TPR][SROW]
+  u32x4* s_kop = (u32x4*)(s_u + kVcodeBytes + kRowsBytes);                 // [kTile][2][NCH][2]
+  uint16_t* s_slowv = (uint16_t*)(s_u + kVcodeBytes + kRowsBytes + kKopBytes);  // [kTile][VROW]
+  // builder share: token bt of the tile, units uid = bpart + 16 u (u < NU) of the
+  // 4 * NCH (K|V, half, 16-element chunk) units of the token
+  constexpr int NU = C::NCH / 4;
+  const int bt = tid >> 4, bpart = tid & 15;
+  // staged rows of slow tile j straight to LDS (all threads): lane l moves the
+  // 16-byte chunk l % (D / 4) of the row of seat l / (D / 4) of the TPR seats
+  const char* lane_row = (const char*)P.st.stage_k + 16 * (lane % (D / 4)) + (int64_t)(lane / (D / 4)) * hk * D * 4;
+  const int64_t vdelta = (const char*)P.st.stage_v - (const char*)P.st.stage_k;
+  auto issue_rows = [&](int j) {
+    // an opaque copy of the lane base: the per-row sums stay in the loop (one
+    // 64-bit add each) instead of being hoisted into eight live register pairs
+    const char* lrow = lane_row;
+    asm volatile("" : "+v"(lrow));
+    const uint32_t smask = s_tmask[j];
+    const int t0 = tile_t0(j);
+    int blk, off0, seat0;
+    tile_page(j, t0, blk, off0, seat0);
+    if (smask != 0) {
+      // row r = wave + kWaves * i: K (r < R) or V rows of tokens TPR * (r % R) + u,
+      // u < TPR; lane l moves the 16-byte chunk l of the row straight to LDS (tokens
+      // outside the mask are skipped)
+      constexpr int R = kTile / C::TPR, CPT = D / 4;
+#pragma unroll
+      for (int i = 0; i < 2 * R / kWaves; ++i) {
+        const int r = wave + kWaves * i, kv = r / R;
+        const int tok = C::TPR * (r % R) + lane / CPT;
+        if ((smask >> tok) & 1u) {
+          // one per-lane base plus wave-uniform byte offsets (nothing kept per row)
+          const int64_t seat = (int64_t)seat0 + off0 + C::TPR * (r % R);
+          const int64_t uoff = (kv ? vdelta : 0) + ((seat * hk + kvh) * D) * 4;
+          __builtin_amdgcn_global_load_lds(lrow + uoff,
+                                           (__attribute__((address_space(3))) void*)(s_rows + r * C::SROW), 16, 0, 0);
+        }
+      }
+    }
+  };
+  // slow tile j (its rows already issued): loads, build, then wave `runner` adds it
+  auto run_slow = [&](int j, int runner) {
+      const uint32_t smask = s_tmask[j];
+      const int t0 = tile_t0(j);
+      int blk, off0, seat0;
+      tile_page(j, t0, blk, off0, seat0);
+      const int bp = t0 + bt;
+      const bool b_staged = (smask >> bt) & 1u;
+      const bool b_codes = bp < hist && !b_staged;
+      const bool b_cur = has_new && bp >= hist && bp < seq;
+      const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)(off0 + bt) * ks1;
+      const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)(off0 + bt) * vs1;
+      const int64_t cur_off = (int64_t)(qa + (b_cur ? bp - hist : 0)) * A.kv_new_stride_token + (int64_t)kvh * D;
+      uint32_t cw[NU] = {};
+      u32x4 clo[NU] = {}, chi[NU] = {};
+      u32x2 meta = {0u, 0u};
+      if (b_codes) meta = *(const u32x2*)ks;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
+        if (b_codes) cw[u] = *(const uint32_t*)((kv ? vs : ks + 32) + hg * (D / 8) + 4 * c);
+        if (b_cur) {
+          const uint16_t* src = (const uint16_t*)(kv ? A.v_new : A.k_new) + cur_off + hg * (D / 2) + 16 * c;
+          clo[u] = *(const u32x4*)src;
+          chi[u] = *(const u32x4*)(src + 8);
+        }
+      }
+      // a unit's values: staged tokens from the LDS rows (after the barrier), the
+      // others from the codes / current chunk in registers (before it, while the row
+      // loads land)
+      auto build = [&](int u, bool staged_pass) {
+        const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
+        unsigned o[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if (staged_pass) {
+          const float* row = s_rows + (kv * (kTile / C::TPR) + bt / C::TPR) * C::SROW + (bt % C::TPR) * D +
+                             hg * (D / 2) + 16 * c;
+          f32x4 f[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) f[x] = *(const f32x4*)(row + 4 * x);
+          if (kv == 0) {
+            // K operand pairs in the lookup's order (e, e+4) / (e+8, e+12)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+              o[x] = hist_pair(f[0][x], f[1][x]);
+              o[4 + x] = hist_pair(f[2][x], f[3][x]);
+            }
+          } else {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) o[x] = hist_pair(f[x >> 2][x & 3], f[2 + (x >> 2)][x & 3]);
+          }
+        } else if (kv == 0) {
+          if (b_cur) {
+            kpairs16(clo[u], chi[u], o);
+          } else if (b_codes) {
+            unsigned t_lo, t_hi;
+            byte_tables(meta[0], t_lo, t_hi);
+            lut16(cw[u], t_lo, t_hi, o);
+          }
+        } else {
+          // V values as (e, e+8) pairs
+          if (b_cur) {
+            interleave8(clo[u], chi[u], o);
+          } else if (b_codes) {
+            unsigned vlo, vhi;
+            value_table(meta[1], vlo, vhi);
+            table_pairs(cw[u], vlo, vhi, o);
+          }
+        }
+        if (kv == 0) {
+          u32x4* dst = s_kop + ((bt * 2 + hg) * C::NCH + c) * 2;
+          dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+          dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+        } else {
+          // to the V buffer, columns permuted so that MFMA row i of output block b
+          // reads column 32 b + i (d = pv_d(b, i))
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u32x2 w = {__builtin_amdgcn_perm(o[q + 4], o[q], 0x05040100u),
+                             __builtin_amdgcn_perm(o[q + 4], o[q], 0x07060302u)};
+            *(u32x2*)&s_slowv[bt * C::VROW + vbuf_col<D>(hg, q, c)] = w;
+          }
+        }
+      };
+      if (!b_staged) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) build(u, false);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's loads (and its row loads into LDS) are in
+      __syncthreads();
+      if (b_staged) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) build(u, true);
+      }
+      __syncthreads();
+      if (wave == runner) {
+        f32x16 S = {};
+#pragma unroll
+        for (int c = 0; c < C::NCH; ++c) {
+          const u32x4* src = s_kop + ((m * 2 + g) * C::NCH + c) * 2;
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, src[0]), qop(2 * c), S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, src[1]), qop(2 * c + 1), S, 0, 0, 0);
+        }
+        // masked scores
+        float xs[16];
+        float mx = -INFINITY;
+        const int limit = seq - nq + (row_ok ? n / G : 0) + 1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tp = t0 + out_tok(r, g);
+          const bool vis = row_ok && tp < limit;  // limit <= seq
+          xs[r] = vis ? S[r] * c_score : -INFINITY;
+          mx = fmaxf(mx, xs[r]);
+        }
+        mx = fmaxf(mx, swap_halves(mx));
+        update_max(mx);
+        // P = hi + lo, both bf16
+        u32x4 ph[2], pl[2];
+        float lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = (xs[r] == -INFINITY) ? 0.f : exp2f(xs[r] - m_run);
+          const float p1 = (xs[r + 1] == -INFINITY) ? 0.f : exp2f(xs[r + 1] - m_run);
+          lsum += p0 + p1;
+          const unsigned hb = bf16_pair(p0, p1);
+          ph[r >> 3][(r & 7) >> 1] = hb;
+          pl[r >> 3][(r & 7) >> 1] = bf16_pair(p0 - __uint_as_float(hb << 16), p1 - __uint_as_float(hb & 0xffff0000u));
+        }
+        l_run += lsum;
+        const int G16 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+        for (int b = 0; b < C::MBLK; ++b) {
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            bf16x8 va;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
+              const uint16_t* addr = &s_slowv[key * C::VROW + 32 * b + 16 * (G16 & 1) + 4 * (i16 & 3)];
+              auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) va[4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
+            }
+            O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, ph[s]), O[b], 0, 0, 0);
+            O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, pl[s]), O[b], 0, 0, 0);
+          }
+        }
+      }
+      __syncthreads();  // the LDS buffers are rewritten by the next tile
+  };
+  if (nslow > 0) issue_rows(__builtin_amdgcn_readfirstlane(s_slow[0]));  // lands during the fast tiles
+
   // ---------------------------------------------------------------- fast tiles
-  // Phase 1 (QK) of tile ti: decides whether the tile is fast (INT2 history only,
-  // no staged token, no mask); if so, its V codes and V constants go to this wave's
-  // LDS slots and S^T = K Q^T runs with the exact history values looked up per code.
-  auto qk_tile = [&](int ti, const TileRegs<D>& r, f32x16& S) -> bool {
-    const int t0 = tile_t0(wave + kWaves * ti);
-    const int p = t0 + m;
-    const bool staged = P.has_stage && p < hist && r.own == (int64_t)r.blk;
-    if (!((t0 + kTile <= fast_end) && !__any(staged))) return false;
+  // Phase 1 (QK) of a fast tile (INT2 history only, no staged token, no mask): its
+  // V codes and V constants go to this wave's LDS slots and S^T = K Q^T runs with
+  // the exact history values looked up per code.
+  auto qk_tile = [&](const TileRegs<D>& r, f32x16& S) {
 #pragma unroll
     for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
     s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
@@ -412,25 +667,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]}),
                                                   qop(2 * i + 1), S, 0, 0, 0);
     }
-    return true;
   };
 
-  // Phase 2: softmax against the wave's reference max and O^T += V^T P'^T.  Returns
-  // false (nothing accumulated) when a row's max drifts more than kLazy above it.
+  // Phase 2: softmax against the wave's reference max (moved, with O, l and z
+  // rescaled, only when a row's max drifts more than kLazy above it) and
+  // O^T += V^T P'^T.
   // P' = p * s_V (fp16) is the B operand; V^T comes from LDS by transpose reads as
   // the subnormals c * 2^(2k-24); sum p and sum p * z_V accumulate on the VALU.
-  auto pv_tile = [&](const f32x16& S) -> bool {
+  auto pv_tile = [&](const f32x16& S) {
     wait_lds();
     __builtin_amdgcn_wave_barrier();
     float mx = -INFINITY;
 #pragma unroll
     for (int r2 = 0; r2 < 16; ++r2) mx = fmaxf(mx, S[r2]);
     mx = fmaxf(mx, swap_halves(mx)) * c_score;  // c_score > 0
-    // the first fast tile sets the reference max (O, l, z are still zero); the
-    // state is uniform across the wave's rows until the slow pass
-    const bool first = m_run == -INFINITY;
-    if (!first && __any(mx > m_run + kLazy)) return false;
-    if (first) m_run = mx;
+    update_max(mx);
     const float nm = -m_run;
     u32x4 pb[2];
     float lsum = 0.f, zsum = 0.f;
@@ -479,29 +730,28 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       }
     }
     __builtin_amdgcn_wave_barrier();  // the LDS slots are rewritten by the next tile
-    return true;
   };
 
   // Two register slots hold the packed data of the wave's next tiles: slot A the
   // even tiles, slot B the odd ones.  A slot is refilled (index clamped to the last
   // tile, so every path issues the same loads) as soon as its tile's QK has consumed
   // it, so the next two tiles are in flight while a tile is computed.
-  uint32_t slow_bits = 0;  // wave tiles (index i) queued for the slow pass
-  {
-    for (int i = 0; i < my; i += 2) {
-      {
-        f32x16 S;
-        const bool fast = qk_tile(i, RA, S);
-        load_tile(i + 2 < last ? i + 2 : last, RA);
-        if (!(fast && pv_tile(S))) slow_bits |= 1u << i;
-      }
-      const bool second = i + 1 < my;
+  // Tiles of the slow set were run before the loop: their slots are refilled
+  // without compute.
+  auto is_slow = [&](int i) { return ((myslow >> i) & 1u) != 0; };
+  for (int i = 0; i < my; i += 2) {
+    {
+      const bool fast = !is_slow(i);
       f32x16 S;
-      bool fast = false;
-      if (second) fast = qk_tile(i + 1, RB, S);
-      load_tile(i + 3 < last ? i + 3 : last, RB);
-      if (second && !(fast && pv_tile(S))) slow_bits |= 2u << i;
+      if (fast) qk_tile(RA, S);
+      load_tile(i + 2 < last ? i + 2 : last, RA);
+      if (fast) pv_tile(S);
     }
+    const bool fast = i + 1 < my && !is_slow(i + 1);
+    f32x16 S;
+    if (fast) qk_tile(RB, S);
+    load_tile(i + 3 < last ? i + 3 : last, RB);
+    if (fast) pv_tile(S);
   }
 
   // ---- fast-tile accumulators to value units: O = O * 2^(24-2k) + z
@@ -516,160 +766,18 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     z_run = 0.f;
   }
 
-  // ---------------------------------------------------------------- slow tiles
-  // Every wave's queued tiles go to one list; waves 0..kSlowWaves-1 take them in
-  // turn (a wave may add any tile of the item to its own softmax state: the wave
-  // states are merged below).
-  if (lane == 0) s_nslow[wave] = __popc(slow_bits);
-  __syncthreads();
-  int nslow = 0, slot0 = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int c = s_nslow[w];
-    slot0 += w < wave ? c : 0;
-    nslow += c;
-  }
-  for (uint32_t bits = slow_bits; bits; bits &= bits - 1, ++slot0)
-    if (lane == 0) s_slow[slot0] = (int16_t)(wave + kWaves * __builtin_ctz(bits));
-  __syncthreads();
-  uint16_t* s_slowv = (uint16_t*)s_big + (wave % kSlowWaves) * (kTile * C::VROW);
-  for (int k = wave; wave < kSlowWaves && k < nslow; k += kSlowWaves) {
-    const int j = s_slow[k];
-    const int t0 = tile_t0(j);
-    const int p = t0 + m;
-    const bool hist_tok = p < hist;
-    const bool cur_tok = has_new && p < seq && p >= hist;
-    int blk, off0, seat0;
-    tile_page(j, t0, blk, off0, seat0);
-    const int off = off0 + m;
-    const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)off * ks1;
-    const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)off * vs1;
-    u32x4 kc[C::NQ], vc[C::NQ];
-#pragma unroll
-    for (int i = 0; i < C::NQ; ++i) {
-      kc[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
-      vc[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
-    }
-    const u32x2 meta = *(const u32x2*)ks;
-    const int64_t own = P.has_stage ? owner[seat0 + off] : -1;
-    const bool staged = P.has_stage && hist_tok && own == (int64_t)blk;
-    const bool any_st = __any(staged), any_cur = __any(cur_tok);
-    // FP32 staged rows of this lane's token (seat row 0 for lanes without one)
-    const int64_t seat = staged ? (int64_t)seat0 + off : 0;
-    const float* sk_row = P.st.stage_k + (seat * hk + kvh) * D + g * (D / 2);
-    const float* sv_row = P.st.stage_v + (seat * hk + kvh) * D + g * (D / 2);
-    const int ci = cur_tok ? p - hist : 0;
-    unsigned kt_lo, kt_hi, vlo, vhi;
-    byte_tables(meta[0], kt_lo, kt_hi);
-    value_table(meta[1], vlo, vhi);
-
-    f32x16 S = {};
-#pragma unroll
-    for (int c0 = 0; c0 < C::NCH; c0 += C::CPR) {
-      f32x4 fk[C::CPR][4], fv[C::CPR][4];
-      if (any_st) {
-#pragma unroll
-        for (int cc = 0; cc < C::CPR; ++cc)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            fk[cc][u] = *(const f32x4*)(sk_row + 16 * (c0 + cc) + 4 * u);
-            fv[cc][u] = *(const f32x4*)(sv_row + 16 * (c0 + cc) + 4 * u);
-          }
-      }
-#pragma unroll
-      for (int cc = 0; cc < C::CPR; ++cc) {
-        const int c = c0 + cc;
-        unsigned ok[8], ov[8];
-        lut16(kc[c >> 2][c & 3], kt_lo, kt_hi, ok);
-        table_pairs(vc[c >> 2][c & 3], vlo, vhi, ov);
-        if (any_st && staged) {
-          // K in the lookup's pair order (e, e+4) / (e+8, e+12); V as (e, e+8)
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            ok[k] = hist_pair(fk[cc][0][k], fk[cc][1][k]);
-            ok[4 + k] = hist_pair(fk[cc][2][k], fk[cc][3][k]);
-          }
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            ov[k] = hist_pair(fv[cc][k >> 2][k & 3], fv[cc][2 + (k >> 2)][k & 3]);
-        }
-        if (any_cur && cur_tok) {
-          const uint16_t* kr = &s_cur[0][ci][g * (D / 2) + 16 * c];
-          const uint16_t* vr = &s_cur[1][ci][g * (D / 2) + 16 * c];
-          kpairs16(*(const u32x4*)kr, *(const u32x4*)(kr + 8), ok);
-          interleave8(*(const u32x4*)vr, *(const u32x4*)(vr + 8), ov);
-        }
-        if (!hist_tok && !cur_tok) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) ok[k] = ov[k] = 0u;
-        }
-        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{ok[0], ok[1], ok[2], ok[3]}),
-                                                    qop(2 * c), S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{ok[4], ok[5], ok[6], ok[7]}),
-                                                    qop(2 * c + 1), S, 0, 0, 0);
-        // V values of this token to the buffer, columns permuted so that MFMA row i
-        // of output block b reads column 32 b + i (d = pv_d(b, i))
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const u32x2 w = {__builtin_amdgcn_perm(ov[q + 4], ov[q], 0x05040100u),
-                           __builtin_amdgcn_perm(ov[q + 4], ov[q], 0x07060302u)};
-          *(u32x2*)&s_slowv[m * C::VROW + vbuf_col<D>(g, q, c)] = w;
-        }
-      }
-    }
-    wait_lds();
-    __builtin_amdgcn_wave_barrier();
-    // masked scores
-    float xs[16];
-    float mx = -INFINITY;
-    const int limit = seq - nq + (row_ok ? n / G : 0) + 1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int tp = t0 + out_tok(r, g);
-      const bool vis = row_ok && tp < limit;  // limit <= seq
-      xs[r] = vis ? S[r] * c_score : -INFINITY;
-      mx = fmaxf(mx, xs[r]);
-    }
-    mx = fmaxf(mx, swap_halves(mx));
-    update_max(mx);
-    // P = hi + lo, both bf16
-    u32x4 ph[2], pl[2];
-    float lsum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const float p0 = (xs[r] == -INFINITY) ? 0.f : exp2f(xs[r] - m_run);
-      const float p1 = (xs[r + 1] == -INFINITY) ? 0.f : exp2f(xs[r + 1] - m_run);
-      lsum += p0 + p1;
-      const unsigned hb = bf16_pair(p0, p1);
-      ph[r >> 3][(r & 7) >> 1] = hb;
-      pl[r >> 3][(r & 7) >> 1] = bf16_pair(p0 - __uint_as_float(hb << 16), p1 - __uint_as_float(hb & 0xffff0000u));
-    }
-    l_run += lsum;
-    const int G16 = lane >> 4, i16 = lane & 15;
-#pragma unroll
-    for (int b = 0; b < C::MBLK; ++b) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        bf16x8 va;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
-          const uint16_t* addr = &s_slowv[key * C::VROW + 32 * b + 16 * (G16 & 1) + 4 * (i16 & 3)];
-          auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) va[4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
-        }
-        O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, ph[s]), O[b], 0, 0, 0);
-        O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, pl[s]), O[b], 0, 0, 0);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
+  // ---- slow tiles, in value units
+#pragma unroll 1
+  for (int k = 0; k < nslow; ++k) {
+    const int j = __builtin_amdgcn_readfirstlane(s_slow[k]);
+    if (k > 0) issue_rows(j);
+    run_slow(j, k % kWaves);
   }
 
   // ---- cross-wave merge: common max M and total L per row, then the wave partials
   // are summed in LDS in MFMA register order, two output blocks per round
   const float l_row = l_run + swap_halves(l_run);
-  __syncthreads();  // every wave is past its slow tiles (s_big is free)
+  __syncthreads();  // every wave is past its fast tiles (s_u is free)
   if (g == 0) { s_ml[wave][0][m] = m_run; s_ml[wave][1][m] = l_row; }
   __syncthreads();
   float M = -INFINITY;
@@ -682,7 +790,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (mw != -INFINITY) L += s_ml[w][1][n] * exp2f(mw - M);
   }
   const float fw = (m_run == -INFINITY || !(L > 0.f)) ? 0.f : exp2f(m_run - M) / L;
-  f32x4* buf = (f32x4*)s_big;  // [kWaves][2 blocks][4][64] f32x4
+  f32x4* buf = (f32x4*)s_u;  // [kWaves][2 blocks][4][64] f32x4
   f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
 #pragma unroll
   for (int rb = 0; rb < C::MBLK / 2; ++rb) {
@@ -710,22 +818,24 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 }
 
 // FP32 LSE merge of a group's items (slab_attention.py:341-356 applied in
-// sequence; empty parts contribute nothing).  One wave per (group, 64-vector chunk
-// of the register-order partial): lane l owns partial vector chunk * 64 + l, i.e.
-// row l % 32, four d values.  Online merge over batches of kBatch items whose
-// partial vectors and LSEs are loaded together.
-constexpr int kBatch = 40;  // one round of loads for up to 40 items
+// sequence; empty parts contribute nothing).  One workgroup of W <= kMergeWaves
+// waves per (group, 64-vector chunk of the register-order partial): lane l of every
+// wave owns partial vector chunk * 64 + l, i.e. row l % 32, four d values.  Wave w
+// merges items w, w + W, ... online (their partial vectors and LSEs loaded in
+// batches of kBatch), then the W wave states (max, sum, vector) are combined in LDS
+// by wave 0.  The host sizes W from the plan's items per group.
+constexpr int kMergeWaves = 8;
+constexpr int kBatch = 16;  // items per load round of a wave
 
 template <int D>
-__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams P) {
+__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams P) {
   using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
   // the group record carries everything the merge needs (no dependent loads)
   const int32_t* grp = A.groups + (int64_t)blockIdx.x * OSCAR_GROUP_INTS;
-  const int req = grp[0], kvh = grp[1], i0 = grp[2], ni = grp[3], a = grp[4], nq = grp[5];
-  (void)req;
+  const int kvh = grp[1], i0 = grp[2], ni = grp[3], a = grp[4], nq = grp[5];
   const int G = P.group;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int n = lane & 31, gg = lane >> 5;
   const int bq = blockIdx.y, b = bq >> 2, q = bq & 3;
   const int e = bq * 64 + lane;  // f32x4 index in the partial
@@ -735,14 +845,15 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams P) {
   float M = -INFINITY, L = 0.f;
   bool nan = false;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < ni; i += kBatch) {
+  for (int i = wave; i < ni; i += W * kBatch) {
     float l[kBatch];
     f32x4 x[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const bool in = i + u < ni;
-      l[u] = in ? pl[(int64_t)(i + u) * 32] : -INFINITY;
-      x[u] = (in && row_ok) ? po[(int64_t)(i + u) * C::NV] : f32x4{0.f, 0.f, 0.f, 0.f};
+      const int it = i + u * W;
+      const bool in = it < ni;
+      l[u] = in ? pl[(int64_t)it * 32] : -INFINITY;
+      x[u] = (in && row_ok) ? po[(int64_t)it * C::NV] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float mb = -INFINITY;
 #pragma unroll
@@ -764,7 +875,37 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams P) {
       M = Mn;
     }
   }
-  if (!row_ok) return;
+  // combine the wave states: common max, rescaled sums (NaN in any wave wins)
+  __shared__ f32x4 s_acc[kMergeWaves][64];
+  __shared__ float s_m[kMergeWaves][64], s_l[kMergeWaves][64];
+  __shared__ int s_nan[kMergeWaves][64];
+  if (wave > 0) {
+    s_acc[wave][lane] = acc;
+    s_m[wave][lane] = M;
+    s_l[wave][lane] = L;
+    s_nan[wave][lane] = nan;
+  }
+  __syncthreads();
+  if (wave > 0 || !row_ok) return;
+  float Mt = M;
+  for (int w = 1; w < W; ++w) {
+    Mt = fmaxf(Mt, s_m[w][lane]);
+    nan |= s_nan[w][lane] != 0;
+  }
+  if (Mt != -INFINITY) {
+    const float f0 = (M == -INFINITY) ? 0.f : expf(M - Mt);
+    acc *= f0;
+    L *= f0;
+    for (int w = 1; w < W; ++w) {
+      const float mw = s_m[w][lane];
+      const float f = (mw == -INFINITY) ? 0.f : expf(mw - Mt);
+      if (f > 0.f) {
+        acc += s_acc[w][lane] * f;
+        L += s_l[w][lane] * f;
+      }
+    }
+  }
+  M = Mt;
   float lse = -INFINITY;
   if (nan) {
     acc = f32x4{NAN, NAN, NAN, NAN};
@@ -789,7 +930,11 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
     OSCAR_CHECK_LAUNCH("attn_main_kernel");
   }
   if (p.a.phases != 1) {
-    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / 64), dim3(64), 0, s, p);
+    // waves per merge workgroup: about kBatch / 2 items per wave, a power of two
+    const int per_group = (p.a.num_items + p.a.num_groups - 1) / p.a.num_groups;
+    int waves = 1;
+    while (waves < kMergeWaves && waves * (kBatch / 2) < per_group) waves *= 2;
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / 64), dim3(waves * 64), 0, s, p);
     OSCAR_CHECK_LAUNCH("attn_merge_kernel");
   }
   return 0;
@@ -814,14 +959,15 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
   if (chunk_tokens < kTile) chunk_tokens = kTile;
   if (chunk_tokens > kMaxItemTokens) chunk_tokens = kMaxItemTokens;
   if (target_items < 1) target_items = 1;
-  // Per (request, kv head) group: body tiles are the full tiles every row sees
-  // (before min(history, seq - n_q + 1)); the tiles after them (current chunk,
-  // causal boundary, ragged end) form one tail item per group.  Body tiles are
-  // dealt to k items round-robin (item j: tiles j, j + k, ...), so a contiguous
-  // run of expensive tiles (the FP32 staging window) spreads over many items.
-  struct Grp { int req, kvh, nbody, ntail, k, first_slot; };
-  int ngroups = 0, ntails = 0;
-  int64_t body_total = 0;
+  // Per (request, kv head) group: the ceil(seq / 32) key tiles are dealt round-robin
+  // to k items (item j: tiles j, j + k, ...), so a contiguous run of expensive tiles
+  // (the FP32 staging window, the current chunk, the causal boundary) spreads over
+  // the group's items.  k is chosen per group so that no item holds more than T
+  // tiles, with T the smallest bound that keeps the total item count within
+  // target_items (one item per group at least; at most chunk_tokens keys per item).
+  struct Grp { int req, kvh, ntiles, k, first_slot; };
+  int ngroups = 0;
+  int64_t tiles_total = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
@@ -836,70 +982,67 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
-    const int seq = seqs[r], hist = has_new ? seq - nq : seq;
-    int fast_end = seq - nq + 1 < hist ? seq - nq + 1 : hist;
-    if (fast_end < 0) fast_end = 0;
-    const int nbody = fast_end / kTile;
-    const int ntail = (seq + kTile - 1) / kTile - nbody;
+    const int ntiles = (seqs[r] + kTile - 1) / kTile;
     for (int h = 0; h < num_kv_heads; ++h) {
-      gl[gi++] = {r, h, nbody, ntail, 0, 0};
-      body_total += nbody;
-      ntails += ntail > 0;
+      gl[gi++] = {r, h, ntiles, 0, 0};
+      tiles_total += ntiles;
     }
   }
-  const int budget = target_items - ntails > ngroups ? target_items - ntails : ngroups;
   const int max_tiles = chunk_tokens / kTile;
+  auto items_for = [&](int64_t T) {
+    int64_t total = 0;
+    for (int q = 0; q < ngroups; ++q) total += gl[q].ntiles > 0 ? (gl[q].ntiles + T - 1) / T : 1;
+    return total;
+  };
+  // smallest T in [ceil(total / target), max_tiles] with items_for(T) <= target
+  int64_t lo = (tiles_total + target_items - 1) / target_items, hi = max_tiles;
+  if (lo < 1) lo = 1;
+  if (lo > hi) lo = hi;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) / 2;
+    if (items_for(mid) <= target_items) hi = mid;
+    else lo = mid + 1;
+  }
+  const int64_t T = lo;
   int nitems = 0, max_k = 0;
   for (int q = 0; q < ngroups; ++q) {
     Grp& G = gl[q];
-    int k = 0;
-    if (G.nbody > 0) {
-      k = (int)(((int64_t)G.nbody * budget * 2 + body_total) / (2 * body_total));
-      if (k < 1) k = 1;
-      if ((G.nbody + k - 1) / k > max_tiles) k = (G.nbody + max_tiles - 1) / max_tiles;
-      if (k > G.nbody) k = G.nbody;
-    }
-    G.k = k;
+    G.k = G.ntiles > 0 ? (int)((G.ntiles + T - 1) / T) : 1;
     G.first_slot = nitems;
-    nitems += k + (G.ntail > 0);
-    if (k > max_k) max_k = k;
+    nitems += G.k;
+    if (G.k > max_k) max_k = G.k;
+    if (nitems > (1 << 26)) return fail(-22, "oscar_attn_plan_v1: too many work items");
   }
   plan->num_items = nitems;
   plan->num_groups = ngroups;
   plan->partial_bytes = (int64_t)nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
   if (items == nullptr || groups == nullptr) return nitems;  // size query
   if (nitems > max_items || ngroups > max_groups) return fail(-28, "oscar_attn_plan_v1: buffers too small");
-  // Launch order: the tail items first (they carry the slow work), then the body
-  // items interleaved over the groups so that consecutive workgroups, which the
-  // hardware deals round-robin to the 8 XCDs, spread every group over the chip.
-  // The partial slots of a group stay contiguous (tail, then body) for the merge.
+  // Launch order: items interleaved over the groups (item j of every group, then
+  // j + 1, ...), so that all groups progress together when there are more items
+  // than compute units.  The partial slots of a group stay contiguous for the merge.
   int idx = 0;
-  auto emit = [&](const Grp& G, int slot, int first, int stride, int count) {
-    int32_t* it = items + (int64_t)idx++ * OSCAR_WORK_INTS;
-    const int nq = qsl[G.req + 1] - qsl[G.req];
-    it[0] = G.req;
-    it[1] = G.kvh | (nq << 16);
-    it[2] = first;
-    it[3] = stride;
-    it[4] = count;
-    it[5] = slot;
-    it[6] = qsl[G.req];
-    it[7] = seqs[G.req];
-  };
-  for (int q = 0; q < ngroups; ++q)
-    if (gl[q].ntail > 0) emit(gl[q], gl[q].first_slot, gl[q].nbody, 1, gl[q].ntail);
   for (int pos = 0; pos < max_k; ++pos)
     for (int q = 0; q < ngroups; ++q) {
       const Grp& G = gl[q];
       if (pos >= G.k) continue;
-      emit(G, G.first_slot + (G.ntail > 0) + pos, pos, G.k, (G.nbody - pos + G.k - 1) / G.k);
+      int32_t* it = items + (int64_t)idx++ * OSCAR_WORK_INTS;
+      const int nq = qsl[G.req + 1] - qsl[G.req];
+      it[0] = G.req;
+      it[1] = G.kvh | (nq << 16);
+      it[2] = pos;
+      it[3] = G.k;
+      it[4] = G.ntiles > pos ? (G.ntiles - pos + G.k - 1) / G.k : 0;
+      it[5] = G.first_slot + pos;
+      it[6] = qsl[G.req];
+      it[7] = seqs[G.req];
     }
   for (int q = 0; q < ngroups; ++q) {
     int32_t* gr = groups + (int64_t)q * OSCAR_GROUP_INTS;
     gr[0] = gl[q].req;
     gr[1] = gl[q].kvh;
     gr[2] = gl[q].first_slot;
-    gr[3] = gl[q].k + (gl[q].ntail > 0);
+    gr[3] = gl[q].k;
     gr[4] = qsl[gl[q].req];
     gr[5] = qsl[gl[q].req + 1] - qsl[gl[q].req];
     gr[6] = gr[7] = 0;

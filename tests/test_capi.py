@@ -109,23 +109,17 @@ def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, 
     assert cnt > 0
     assert sorted(items[:, 5].tolist()) == list(range(cnt))          # partial slots: a permutation
     assert p.partial_bytes == cnt * 32 * (256 + 1) * 4
-    seen_body = False
+    ngroups = hk * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+    assert cnt <= max(256, ngroups)                                  # within the target
     for it in items:
         req, kvh, nq, first, stride, count, part, qa, seq = (it[0], it[1] & 0xFFFF, it[1] >> 16, *it[2:8])
-        hist = seq - nq if has_new else seq
         assert nq == qsl[req + 1] - qsl[req] and qa == qsl[req] and seq == seqs[req]
         assert 0 <= kvh < hk and nq * group <= 32
-        assert 1 <= count <= 8192 // TILE and stride >= 1
-        assert (first + stride * (count - 1)) * TILE < seq               # no tile past the end
-        body = min(hist, seq - nq + 1) // TILE
-        is_tail = first >= body
-        if is_tail:
-            assert not seen_body  # tail items (the slow work) are launched first
-            assert stride == 1 and first == body
-        else:
-            seen_body = True
-            assert first + stride * (count - 1) < body
-    # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous
+        assert 0 <= first < stride or (first == 0 and stride == 1)
+        assert count <= 8192 // TILE
+        assert count == 0 or (first + stride * (count - 1)) * TILE < seq   # no tile past the end
+    # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous,
+    # item sizes within one tile of each other
     for req, kvh, first_slot, nslots, qa, nq, z0, z1 in groups:
         assert qa == qsl[req] and nq == qsl[req + 1] - qsl[req] and z0 == z1 == 0
         rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh)]
@@ -134,13 +128,25 @@ def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, 
         for it in rows:
             np.add.at(cover, it[2] + it[3] * np.arange(it[4]), 1)
         assert (cover == 1).all()
-    assert len(groups) == hk * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+        assert rows[:, 4].max() - rows[:, 4].min() <= 1
+    assert len(groups) == ngroups
+    # balance across groups: the largest item is the smallest bound that fits the target
+    ntiles = [(seqs[r] + TILE - 1) // TILE for r in range(len(seqs)) if qsl[r + 1] > qsl[r] for _ in range(hk)]
+    T = items[:, 4].max()
+    if T > 1:
+        assert sum(-(-n // (T - 1)) for n in ntiles) > 256
+
+
+def test_plan_launch_order_interleaves_groups(lib):
+    _, items, _, _ = plan(lib, [0] + [4 * i for i in range(1, 9)], [24580] * 8)
+    # item j of every group before item j + 1 of any group
+    assert items[:8, 0].tolist() == list(range(8)) and (items[:8, 2] == 0).all()
+    assert (np.diff(items[:, 2]) >= 0).all()
 
 
 def test_plan_splits_long_history_across_items(lib):
     _, items, _, _ = plan(lib, [0, 4], [100003], target=256)
-    body = items[items[:, 4] > 0]
-    assert len(items) > 64 and body[:, 4].max() * TILE <= 8192
+    assert len(items) > 64 and items[:, 4].max() * TILE <= 8192
 
 
 def test_plan_rejects_bad_requests(lib):

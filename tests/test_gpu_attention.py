@@ -24,14 +24,14 @@ def dev(x, dtype=torch.bfloat16):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
 
 
-def run_decode(c, d=256, hk=1, group=6):
+def run_decode(c, d=256, hk=1, group=6, target=256):
     from oscar_amd import ops
 
     kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
     vc = torch.from_numpy(c["v8"]).view(torch.int8).cuda()
     stage = None if c["stage"] is None else tuple(torch.from_numpy(a).cuda() for a in c["stage"])
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=c["k"] is not None, num_kv_heads=hk,
-                           group=group, head_dim=d, device=torch.device("cuda"))
+                           group=group, head_dim=d, device=torch.device("cuda"), target_items=target)
     out, lse = ops.attention_decode(dev(c["q"]), None if c["k"] is None else dev(c["k"]),
                                     None if c["v"] is None else dev(c["v"]),
                                     kc, vc, torch.from_numpy(c["bt"]).cuda(), plan, c["scale"],
@@ -58,6 +58,10 @@ DECODE_CASES = [
     ("cache_only", [0, 257, 3, 263], [1, 1, 4, 5], {"fresh": False}),
     ("no_window", [1025, 2048], [4, 4], {"window": False}),
     ("d128_hk2", [129, 700], [4, 2], {"d": 128, "hk": 2, "group": 4}),
+    # few items of up to 256 tiles: slow tiles (sink/recent window, ragged end, current
+    # chunk) at item-tile indices past 32 and 64
+    ("few_long_items", [9000], [1], {"fresh": False, "target": 2}),
+    ("few_long_items_mtp", [8000, 3001], [4, 2], {"target": 3}),
 ]
 
 
@@ -68,7 +72,7 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     group = opts.get("group", 6)
     c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group,
                         fresh=opts.get("fresh", True), window=opts.get("window", True))
-    out, lse, _ = run_decode(c, d, hk, group)
+    out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256))
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
     check(out, lse, ref_out, ref_lse, name)
@@ -81,7 +85,8 @@ def test_decode_plan_covers_each_history_token_once(cuda):
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=1, group=6,
                            head_dim=256, device=torch.device("cuda"), target_items=256)
     items = np.array(plan.host_items).reshape(-1, 8)
-    assert plan.num_items == 256  # 8 tail items + 248 body items
+    # 769 tiles per group, at most 25 per item (24 would need 264 > 256 items)
+    assert plan.num_items == 248 and max(np.array(plan.host_items).reshape(-1, 8)[:, 4]) == 25
     for r, seq in enumerate(c["seqs"]):
         rows = items[items[:, 0] == r]
         cover = np.zeros((seq + 31) // 32, np.int32)
