@@ -314,32 +314,25 @@ __device__ float clip_threshold(const float* row, int idx, volatile float* slot)
   return *slot;
 }
 
-template <int D, bool SCAN>
-__global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
-  constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
+// Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
+// the last writer of each, and its request's length and query end (for the window
+// rule).  Winners of duplicate slots / seats come from the claims (SCAN false) or
+// from scanning slot_mapping (SCAN true).  Computed by one wave, wave-uniform.
+struct Dest {
+  int64_t slot, seat, seq, end;
+  bool valid, slot_win, seat_win;
+};
+
+template <bool SCAN>
+__device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t, int64_t epoch) {
   const oscar_store_args_v1& a = p.a;
-  const int kind = blockIdx.y;  // K or V
-  const int64_t hk = a.cache.num_kv_heads;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // this call's epoch (word1, set by the rotate launch); word0 takes it for the next
-  // call (no other quant workgroup reads word0).  Scan calls use no claims.
-  int64_t epoch = 0;
-  if constexpr (!SCAN) {
-    epoch = a.epoch_counter[1];
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
-  }
-  const int64_t vec = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (vec >= a.num_tokens * hk) return;
-  const int64_t t = vec / hk, h = vec % hk;
-  const bool active = lane < NL;
+  const int lane = threadIdx.x & 63;
   const int64_t bs = a.cache.block_size;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
-
-  // ---- one round of loads: slot, this vector's row, the request table (and, for a
-  // scan call, every slot of the call)
+  Dest d{};
+  // ---- one round of loads: slot, the request table (and, for a scan call, every
+  // slot of the call)
   const int64_t slot = a.slot_mapping[t];
-  const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
-  const f32x4 x4 = *(const f32x4*)(y + 4 * (active ? lane : 0));
   // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
   // length and query end come from the same loads (qsl is non-decreasing)
   int64_t seq = 0, end = 0;
@@ -359,9 +352,13 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
       }
     }
   }
-  if (slot < 0 || slot >= p.capacity) return;
-  const int64_t blk = slot / bs, off = slot % bs;
+  d.slot = slot;
+  d.seq = seq;
+  d.end = end;
+  d.valid = slot >= 0 && slot < p.capacity;
+  if (!d.valid) return d;
   const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
+  d.seat = seat;
   bool slot_win, seat_win;
   if constexpr (SCAN) {
     // last writer: no later valid token of the call has the same slot / seat
@@ -383,9 +380,28 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
     slot_win = (long long)a.slot_claims[slot] == mine;
     seat_win = window && (long long)a.seat_claims[seat] == mine;
   }
-  __shared__ float rows[kThreads / 64][D];
-  __shared__ float clip_slot[kThreads / 64];
-  float* row = rows[wave];
+  d.slot_win = slot_win;
+  d.seat_win = seat_win;
+  return d;
+}
+
+// Quantize, pack and scatter one rotated vector (kind K or V of token t, kv head h,
+// destination d) held by one wave (lane b < D / 4: elements 4b..4b+3 in x4), with
+// the staging window and owner tag of its seat.
+template <int D>
+__device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t h, const Dest& d, f32x4 x4,
+                             float* row, float* clip_slot) {
+  constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
+  const oscar_store_args_v1& a = p.a;
+  const int64_t hk = a.cache.num_kv_heads;
+  const int lane = threadIdx.x & 63;
+  const bool active = lane < NL;
+  const int64_t bs = a.cache.block_size;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  if (!d.valid) return;
+  const int64_t slot = d.slot, seat = d.seat, seq = d.seq, end = d.end;
+  const bool slot_win = d.slot_win, seat_win = d.seat_win;
+  const int64_t blk = slot / bs, off = slot % bs;
   if (active) *(f32x4*)&row[4 * lane] = x4;
 
   if (window && seat_win) {
@@ -406,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
     __builtin_amdgcn_wave_barrier();
     int idx = (int)(clip * (float)D);
     if (idx > D - 1) idx = D - 1;
-    thr = clip_threshold<D>(row, idx, &clip_slot[wave]);
+    thr = clip_threshold<D>(row, idx, clip_slot);
   }
   // lane b handles byte b = elements 4b..4b+3
   float x[4];
@@ -444,6 +460,166 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   }
 }
 
+template <int D, bool SCAN>
+__global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
+  const oscar_store_args_v1& a = p.a;
+  const int kind = blockIdx.y;  // K or V
+  const int64_t hk = a.cache.num_kv_heads;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // this call's epoch (word1, set by the rotate launch); word0 takes it for the next
+  // call (no other quant workgroup reads word0).  Scan calls use no claims.
+  int64_t epoch = 0;
+  if constexpr (!SCAN) {
+    epoch = a.epoch_counter[1];
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
+  }
+  const int64_t vec = (int64_t)blockIdx.x * (kThreads / 64) + wave;
+  if (vec >= a.num_tokens * hk) return;
+  const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
+  const f32x4 x4 = *(const f32x4*)(y + 4 * (lane < D / 4 ? lane : 0));
+  __shared__ float rows[kThreads / 64][D];
+  __shared__ float clip_slot[kThreads / 64];
+  const Dest d = vector_dest<SCAN>(p, kind, vec / hk, epoch);
+  quant_vector<D>(p, kind, vec / hk, vec % hk, d, x4, rows[wave], &clip_slot[wave]);
+}
+
+// Calls of at most kFusedTokens tokens (decode and MTP steps): one launch.  A
+// workgroup rotates whole vectors -- one K or V vector (token, kv head), or kQPW
+// query heads of a token -- with R streamed through LDS in blocks of QR rows (two
+// buffers: the loads of block b + 1 overlap the arithmetic on block b) and
+// the contraction split over KP parts of the rows (fp64 accumulation, parts added
+// in order: the fp32 result is the correctly rounded one); wave 0 then quantizes,
+// packs and scatters a K / V vector in place (quant_vector, winners by scanning)
+// and writes the read-path copies.
+constexpr int64_t kFusedTokens = 64;
+constexpr int kQPW = 2;  // query heads per fused workgroup
+
+template <int D, int XT>
+__global__ __launch_bounds__(kThreads) void store_small_kernel(StoreParams p) {
+  constexpr int NL = D / 4;             // lanes of a 4-column group
+  constexpr int KP = kThreads / NL;     // parts of the contraction
+  constexpr int QR = D > 128 ? D / 4 : D;    // rows of R per streamed block
+  constexpr int NQB = D / QR;                 // blocks
+  constexpr int NBUF = NQB > 1 ? 2 : 1;
+  const oscar_store_args_v1& a = p.a;
+  const int64_t hk = a.cache.num_kv_heads;
+  const int64_t t = blockIdx.x;
+  const int yb = blockIdx.y;
+  const int kind = yb < hk ? KIND_K : (yb < 2 * hk ? KIND_V : KIND_Q);
+  const int64_t h0 = kind == KIND_K ? yb : (kind == KIND_V ? yb - hk : (int64_t)(yb - 2 * hk) * kQPW);
+  const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
+  const int nv = kind == KIND_Q ? (heads - h0 < kQPW ? (int)(heads - h0) : kQPW) : 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = tid % NL, kp = tid / NL;
+  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
+  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
+                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
+  const float* R = (kind == KIND_V) ? a.rv : a.rk;
+  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
+
+  __shared__ __attribute__((aligned(16))) float s_r[NBUF][QR * D];
+  __shared__ float s_x[kQPW][D];
+  __shared__ double s_red[KP - 1][kQPW][4][NL];
+  __shared__ float s_row[D];
+  __shared__ float s_clip;
+  // the destination of a K / V vector: its loads go out first and overlap the rotation
+  Dest dest{};
+  if (kind != KIND_Q && wave == 0) dest = vector_dest<true>(p, kind, t, 0);
+  // the input vectors (fp32 in LDS; slots past nv are zero)
+  for (int e = tid; e < kQPW * D; e += kThreads)
+    if (e >= nv * D) s_x[e / D][e % D] = 0.f;
+  for (int e = tid; e < nv * (D / 8); e += kThreads) {
+    const int v = e / (D / 8), k8 = (e % (D / 8)) * 8;
+    float xv[8];
+    load8<XT>(src, t * src_stride + (h0 + v) * D + k8, xv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_x[v][k8 + j] = xv[j];
+  }
+  double acc[kQPW][4];
+#pragma unroll
+  for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[v][j] = 0.0;
+  if (R != nullptr) {
+    // block q = rows [q * QR, (q + 1) * QR) of R, moved through registers: thread tid
+    // holds the 16-byte chunks tid + kThreads * i of the block
+    constexpr int CH = QR * D / 4 / kThreads;  // 16-byte chunks per thread
+    f32x4 nxt[CH];
+    auto load = [&](int q) {
+      const f32x4* src4 = (const f32x4*)(R + (int64_t)q * QR * D);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) nxt[i] = src4[tid + kThreads * i];
+    };
+    auto stash = [&](int q) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) *(f32x4*)&s_r[q % NBUF][4 * (tid + kThreads * i)] = nxt[i];
+    };
+    load(0);
+    stash(0);
+    __syncthreads();  // block 0 and the input vectors are in LDS
+    for (int q = 0; q < NQB; ++q) {
+      if (q + 1 < NQB) load(q + 1);  // in flight during the arithmetic on block q
+      const float* rb = s_r[q % NBUF];
+      // rows kl = kp + KP * i of this block, all read before the FMAs
+      f32x4 r4[QR / KP];
+      float xs[QR / KP][kQPW];
+#pragma unroll
+      for (int i = 0; i < QR / KP; ++i) {
+        const int kl = kp + KP * i;
+        r4[i] = *(const f32x4*)&rb[kl * D + 4 * cg];
+#pragma unroll
+        for (int v = 0; v < kQPW; ++v) xs[i][v] = s_x[v][q * QR + kl];
+      }
+#pragma unroll
+      for (int i = 0; i < QR / KP; ++i)
+#pragma unroll
+        for (int v = 0; v < kQPW; ++v) {
+          const double x = xs[i][v];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[v][j] = fma(x, (double)r4[i][j], acc[v][j]);
+        }
+      if (q + 1 < NQB) stash(q + 1);  // block q - 1's buffer: free since the last barrier
+      __syncthreads();
+    }
+  } else {
+    __syncthreads();
+    if (kp == 0) {
+#pragma unroll
+      for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[v][j] = v < nv ? (double)s_x[v][4 * cg + j] : 0.0;
+    }
+  }
+  // parts 1..KP-1 to LDS, part 0 adds them in order
+  if (kp > 0) {
+#pragma unroll
+    for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_red[kp - 1][v][j][cg] = acc[v][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const bool active = lane < NL;  // kp == 0
+  float y[kQPW][4];
+#pragma unroll
+  for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      double sum = acc[v][j];
+      if (R != nullptr)
+        for (int w = 0; w < KP - 1; ++w) sum += s_red[w][v][j][active ? cg : 0];
+      y[v][j] = (float)sum;
+    }
+  if (active && rot_out != nullptr) {
+    const int64_t hq = kind == KIND_Q ? a.num_q_heads : hk;
+#pragma unroll
+    for (int v = 0; v < kQPW; ++v)
+      if (v < nv) store4<XT>(rot_out, (t * hq + h0 + v) * D + 4 * cg, y[v]);
+  }
+  if (kind == KIND_Q) return;
+  quant_vector<D>(p, kind, t, h0, dest, f32x4{y[0][0], y[0][1], y[0][2], y[0][3]}, s_row, &s_clip);
+}
+
 template <int D, int TV>
 void launch_rotate(const StoreParams& p, dim3 grid, hipStream_t s) {
   dim3 block(kThreads);
@@ -454,6 +630,16 @@ void launch_rotate(const StoreParams& p, dim3 grid, hipStream_t s) {
 
 template <int D>
 int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_t s) {
+  if (p.a.num_tokens <= kFusedTokens && p.scan) {
+    const int64_t hk = p.a.cache.num_kv_heads;
+    const int64_t qg = q_vec ? (p.a.num_q_heads + kQPW - 1) / kQPW : 0;
+    dim3 grid((unsigned)p.a.num_tokens, (unsigned)(2 * hk + qg));
+    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kThreads), 0, s, p);
+    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F32>), grid, dim3(kThreads), 0, s, p);
+    OSCAR_CHECK_LAUNCH("store_small_kernel");
+    return 0;
+  }
   const int kinds = q_vec ? 3 : 2;
   const int64_t max_vec = kv_vec > q_vec ? kv_vec : q_vec;
   if (max_vec >= 4096) {
