@@ -512,6 +512,30 @@ def pmc_summary(fetch_csv, write_csv, kernel="attn_main_kernel", copy_mib=1024):
     return out
 
 
+def rdreq_summary(rdreq_csv, kernel="attn_main_kernel"):
+    """Read bytes per launch from the TCC/EA read-request counters by size (32, 64 and
+    128 B), unscaled, with the same figure for the elementwise calibration copy: a
+    cross-check of the scaled FETCH_SIZE (whose formula counts 128-byte requests as
+    64 bytes on this part)."""
+    import csv
+
+    per = {}
+    with open(rdreq_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], row["Dispatch_Id"])
+            per.setdefault(key, {})[row["Counter_Name"]] = float(row["Counter_Value"])
+
+    def nbytes(v):
+        return (v.get("TCC_EA0_RDREQ_128B_sum", 0) * 128 + v.get("TCC_EA0_RDREQ_64B_sum", 0) * 64
+                + v.get("TCC_EA0_RDREQ_32B_sum", 0) * 32)
+
+    main = [nbytes(v) for (name, _), v in per.items() if kernel in name]
+    ew = [nbytes(v) for (name, _), v in per.items() if "MulFunctor" in name]
+    n128 = [v.get("TCC_EA0_RDREQ_128B_sum", 0) for (name, _), v in per.items() if kernel in name]
+    return {"read_bytes_per_dispatch": float(np.median(main)), "requests_128B_per_dispatch": float(np.median(n128)),
+            "calib_elementwise_read_bytes": max(ew), "dispatches": len(main)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -524,11 +548,14 @@ def main(argv=None):
     ap.add_argument("--profile-main", action="store_true",
                     help="only run attn_main over the layer caches plus a calibration copy "
                          "(the workload of the rocprofv3 --pmc passes)")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="turn the two counter-collection CSVs into " + str(TRAFFIC_FILE))
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="FETCH_CSV WRITE_CSV [RDREQ_CSV]: turn the counter-collection CSVs into "
+                         + str(TRAFFIC_FILE))
     args = ap.parse_args(argv)
     if args.pmc_summary:
-        res = pmc_summary(*args.pmc_summary)
+        if len(args.pmc_summary) not in (2, 3):
+            ap.error("--pmc-summary takes FETCH_CSV WRITE_CSV [RDREQ_CSV]")
+        res = pmc_summary(*args.pmc_summary[:2])
         lines = [f"# attn_main_kernel<256>, config 4a (8 x 24576 + 4 MTP), HBM bytes per launch",
                  "# from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE passes over",
                  "#   python bench.py --profile-main",
@@ -537,6 +564,11 @@ def main(argv=None):
             for k, v in res[counter].items():
                 lines.append(f"{counter}.{k} {v}")
         lines.append(f"traffic_bytes {res['traffic_bytes']}")
+        if len(args.pmc_summary) == 3:
+            lines += ["# cross-check: rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum",
+                      "#   TCC_EA0_RDREQ_64B_sum TCC_EA0_RDREQ_128B_sum (same workload), unscaled"]
+            for k, v in rdreq_summary(args.pmc_summary[2]).items():
+                lines.append(f"RDREQ.{k} {v}")
         TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
         print(TRAFFIC_FILE.read_text(), end="")
         return 0
