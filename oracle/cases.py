@@ -64,11 +64,13 @@ def empty_caches(num_blocks: int, bs: int, hk: int, d: int, legacy: bool = False
 
 
 def make_case(prefixes, lengths, *, hk=1, group=6, d=256, bs=128, window=True, fresh=True,
-              seed=117, sink=128, recent=256, legacy=False):
+              seed=117, sink=128, recent=256, legacy=False, key_ramp=0.0):
     """probe_streaming.py:31-81: packed history + optional staging + current chunk.
 
     Returns dict(q, k, v, k8, v8, bt, qsl, seqs, scale, stage).  All floats are
     float32 arrays on the bf16 grid; stage = (stage_k, stage_v, owner) or None.
+    key_ramp > 0 scales history key t by 1 + key_ramp * t / 1024 (a rising score
+    maximum along the history, for the attention kernels' rescale paths).
     """
     g = rng(seed)
     hq = hk * group
@@ -84,7 +86,13 @@ def make_case(prefixes, lengths, *, hk=1, group=6, d=256, bs=128, window=True, f
         slots.append(bt[req, pos // bs].astype(np.int64) * bs + pos % bs)
         qsl.append(qsl[-1] + n)
     total = sum(prefixes)
-    old_k = fmt.bf16_round(g.standard_normal((total, hk, d)).astype(np.float32))
+    old_k = g.standard_normal((total, hk, d)).astype(np.float32)
+    if key_ramp:
+        # history keys grow with their position (x (1 + key_ramp * pos / 1024)), so a
+        # row's score maximum keeps rising along the history
+        pos = np.concatenate([np.arange(p_) for p_ in prefixes]) if total else np.zeros(0)
+        old_k *= (1.0 + key_ramp * pos / 1024.0).astype(np.float32)[:, None, None]
+    old_k = fmt.bf16_round(old_k)
     old_v = fmt.bf16_round(g.standard_normal((total, hk, d)).astype(np.float32))
     store_ref(old_k, old_v, k8, v8, np.concatenate(slots) if slots else np.zeros(0, np.int64))
     q = fmt.bf16_round(g.standard_normal((qsl[-1], hq, d)).astype(np.float32))

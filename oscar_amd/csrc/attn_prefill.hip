@@ -250,7 +250,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       }
       // p = 2^(S c - m) (exp2 of -inf is 0); rows with no key yet keep m = -inf and p = 0
       const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
-      bf16x8 pb[2];
+      // P = hi + lo, both bf16 (the pair carries ~16 bits of p)
+      bf16x8 pb[2], pl[2];
       float lsum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
@@ -258,8 +259,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
         const float p1 = __builtin_amdgcn_exp2f(fmaf(S[r + 1], c, nm));
         lsum += p0 + p1;
         const bf16x2 h = __builtin_convertvector(f32x2{p0, p1}, bf16x2);
+        const f32x2 hf = __builtin_convertvector(h, f32x2);
+        const bf16x2 lo = __builtin_convertvector(f32x2{p0 - hf[0], p1 - hf[1]}, bf16x2);
         pb[r >> 3][r & 7] = h[0];
         pb[r >> 3][(r & 7) + 1] = h[1];
+        pl[r >> 3][r & 7] = lo[0];
+        pl[r >> 3][(r & 7) + 1] = lo[1];
       }
       l_run += lsum;
       // ---- O^T += V^T P^T; the V^T operands of two output blocks (8 transpose reads)
@@ -283,10 +288,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-          for (int s = 0; s < 2; ++s)
+          for (int s = 0; s < 2; ++s) {
             O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
+            O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
+          }
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
       }
       // the prefetched tile kt+1 goes to the other buffer (last read before the previous
       // barrier), then tile kt+2 is prefetched; one barrier per tile

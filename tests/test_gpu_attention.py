@@ -62,6 +62,9 @@ DECODE_CASES = [
     # chunk) at item-tile indices past 32 and 64
     ("few_long_items", [9000], [1], {"fresh": False, "target": 2}),
     ("few_long_items_mtp", [8000, 3001], [4, 2], {"target": 3}),
+    # keys growing along the history: each item's running max moves many times
+    # (the fast tiles' rescale of O, l and z)
+    ("rising_scores", [6000, 2500], [4, 1], {"key_ramp": 4.0, "target": 4}),
 ]
 
 
@@ -71,7 +74,8 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     hk = opts.get("hk", 1)
     group = opts.get("group", 6)
     c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group,
-                        fresh=opts.get("fresh", True), window=opts.get("window", True))
+                        fresh=opts.get("fresh", True), window=opts.get("window", True),
+                        key_ramp=opts.get("key_ramp", 0.0))
     out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256))
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
@@ -112,11 +116,12 @@ def test_prefill_fresh_only_matches_sdpa(cuda):
         assert err <= OUT_TOL
 
 
-@pytest.mark.parametrize("prefix,n", [(1025, 100), (8193, 257), (129, 1024)])
-def test_prefill_continuation_matches_oracle(cuda, prefix, n):
+@pytest.mark.parametrize("prefix,n,ramp", [(1025, 100, 0.0), (8193, 257, 0.0), (129, 1024, 0.0),
+                                           (3000, 300, 4.0)])
+def test_prefill_continuation_matches_oracle(cuda, prefix, n, ramp):
     from oscar_amd import ops
 
-    c = cases.make_case([prefix], [n])
+    c = cases.make_case([prefix], [n], key_ramp=ramp)
     kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
     vc = torch.from_numpy(c["v8"]).view(torch.int8).cuda()
     stage = tuple(torch.from_numpy(a).cuda() for a in c["stage"])
