@@ -42,8 +42,8 @@
 //    when a tile's max exceeds it by more than kLazy, so p <= 2^kLazy.
 //
 // Slow tiles run after the fast tiles, one at a time by the whole workgroup: the
-// staged FP32 rows go straight to LDS (global_load_lds; the first slow tile's while
-// the fast tiles run), all threads build the tile's K operands and V values in LDS
+// staged FP32 rows go straight to LDS (global_load_lds), all threads build the
+// tile's K operands and V values in LDS
 // (staged rows, codes or current chunk, rounded as the reference does), and one
 // wave adds the tile to its softmax state with P split into bf16 hi + lo parts.
 #include <vector>
@@ -247,17 +247,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   __shared__ uint64_t s_slowset[kMaxItemTokens / kTile / 64];  // slow-set bits of the item tiles
   __shared__ int16_t s_slow[kMaxItemTokens / kTile];             // the slow tiles, ascending
   __shared__ uint32_t s_tmask[kMaxItemTokens / kTile]; // staged-token mask of every item tile
-  // union of the phases: V codes of each wave's current fast tile
-  // [kWaves][kTile * NB], then the slow tiles' staged FP32 K / V rows
-  // [2][kTile / TPR][SROW] (loaded while the fast tiles run), K operands (bf16 pairs
-  // in MFMA order) [kTile][2][NCH][8] and V values (bf16, permuted columns)
-  // [kTile][VROW]; after them, the cross-wave merge rounds of two output blocks
-  // [kWaves][2][4][64] f32x4 from the start
+  // the slow tiles' staged FP32 K / V rows [2][kTile / TPR][SROW], moved by
+  // global_load_lds after the fast tiles.  (An LDS DMA still pending at the fast loop
+  // makes the compiler wait for every outstanding load before the loop's LDS accesses,
+  // which empties the two-tile prefetch, so none is issued before the loop.)
+  constexpr int kRowsBytes = 2 * (kTile / C::TPR) * C::SROW * 4;
+  __shared__ __attribute__((aligned(16))) float s_rows[kRowsBytes / 4];
+  // union of the phases: V codes of each wave's current fast tile [kWaves][kTile * NB];
+  // the slow tile's K operands (bf16 pairs in MFMA order) [kTile][2][NCH][8] and V
+  // values (bf16, permuted columns) [kTile][VROW]; the cross-wave merge rounds of two
+  // output blocks [kWaves][2][4][64] f32x4
   constexpr int kVcodeBytes = kWaves * kTile * C::NB;
-  constexpr int kRowsBytes = 2 * (kTile / C::TPR) * C::SROW * 4, kKopBytes = kTile * 2 * C::NCH * 8 * 4;
-  constexpr int kSlowBytes = kVcodeBytes + kRowsBytes + kKopBytes + kTile * C::VROW * 2;
+  constexpr int kKopBytes = kTile * 2 * C::NCH * 8 * 4;
+  constexpr int kSlowBytes = kKopBytes + kTile * C::VROW * 2;
   constexpr int kMergeBytes = kWaves * 2 * 4 * 64 * 16;
-  __shared__ __attribute__((aligned(16))) uint8_t s_u[kSlowBytes > kMergeBytes ? kSlowBytes : kMergeBytes];
+  constexpr int kU0 = kVcodeBytes > kSlowBytes ? kVcodeBytes : kSlowBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t s_u[kU0 > kMergeBytes ? kU0 : kMergeBytes];
   uint8_t (*s_vcode)[kTile * C::NB] = (uint8_t (*)[kTile * C::NB])s_u;
   const unsigned st_rows = (unsigned)P.st.rows;
 
@@ -415,8 +420,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // loaded in the prologue) or past the fast range (current chunk, causal
   // boundary, ragged end).  The fast tiles skip them; they run after the fast
   // tiles, one at a time by the whole workgroup: (1) the staged FP32 rows of the
-  // tile's staged tokens go straight to LDS (for the first slow tile while the fast
-  // tiles run), and every
+  // tile's staged tokens go straight to LDS, and every
   // thread loads the codes, constants or current-chunk values of its share (token
   // tid / 16); (2) the threads build the tile's K operands and V values into LDS
   // with the reference rounding; (3) one wave (round-robin) adds the tile to its
@@ -455,9 +459,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const int jl = (wave + kWaves * lane) & (kMaxItemTokens / kTile - 1);  // lanes >= my: any in-range index
   const uint32_t myslow = (uint32_t)__ballot(lane < my && ((s_slowset[jl >> 6] >> (jl & 63)) & 1ull));
   __syncthreads();
-  float* s_rows = (float*)(s_u + kVcodeBytes);                            // [2][kTile / TPR][SROW]
-  u32x4* s_kop = (u32x4*)(s_u + kVcodeBytes + kRowsBytes);                 // [kTile][2][NCH][2]
-  uint16_t* s_slowv = (uint16_t*)(s_u + kVcodeBytes + kRowsBytes + kKopBytes);  // [kTile][VROW]
+  u32x4* s_kop = (u32x4*)s_u;                                 // [kTile][2][NCH][2]
+  uint16_t* s_slowv = (uint16_t*)(s_u + kKopBytes);           // [kTile][VROW]
   // builder share: token bt of the tile, units uid = bpart + 16 u (u < NU) of the
   // 4 * NCH (K|V, half, 16-element chunk) units of the token
   constexpr int NU = C::NCH / 4;
@@ -643,7 +646,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       }
       __syncthreads();  // the LDS buffers are rewritten by the next tile
   };
-  if (nslow > 0) issue_rows(__builtin_amdgcn_readfirstlane(s_slow[0]));  // lands during the fast tiles
 
   // ---------------------------------------------------------------- fast tiles
   // Phase 1 (QK) of a fast tile (INT2 history only, no staged token, no mask): its
@@ -770,7 +772,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 #pragma unroll 1
   for (int k = 0; k < nslow; ++k) {
     const int j = __builtin_amdgcn_readfirstlane(s_slow[k]);
-    if (k > 0) issue_rows(j);
+    issue_rows(j);
     run_slow(j, k % kWaves);
   }
 
