@@ -149,7 +149,8 @@ class Setup:
         self.lse = torch.zeros(B * n, hq, dtype=torch.float32, device=dev)
         self.out = torch.empty(B * n, hq, d, dtype=torch.bfloat16, device=dev)
         self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=has_new, num_kv_heads=hk,
-                                    group=hq // hk, head_dim=d, device=dev)
+                                    group=hq // hk, head_dim=d, device=dev,
+                                    window=(self.sink_eff, c["recent_tokens"]))
 
     def step(self, layer, phases=0):
         from oscar_amd import ops

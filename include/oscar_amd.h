@@ -145,10 +145,16 @@ int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
  * OSCAR_WORK_INTS int32 each and returns the item count (or < 0); with
  * items == NULL or groups == NULL it only fills *plan (size query).
  *
- * Keys of a (request, kv head) group are cut into 32-token tiles.  Body tiles
- * (before min(history, seq - n_q + 1)) are dealt round-robin to k items; the
- * remaining tiles (current chunk, causal boundary, ragged end) form one tail
- * item.  Item record, int32[8]:
+ * Keys of a (request, kv head) group are cut into 32-token tiles.  sink_tokens
+ * and recent_tokens describe the FP32 staging window the store keeps (positions
+ * < sink_tokens and >= seq - recent_tokens; 0 = none): a hint for balance only,
+ * the decode finds staged tokens from the owner tags whatever the plan expects.
+ * The expected window tiles and the tiles at and past the first masked or
+ * current key cost more (FP32 rows, one tile at a time); they are dealt to items
+ * of their own, the history tiles between them to the others, each range
+ * round-robin (item i of k: tiles first + i, first + i + k, ...), or the whole
+ * group as one range where that takes fewer items, so that the most expensive
+ * item is as cheap as target_items allows.  Item record, int32[8]:
  *   [0] request  [1] kv_head | n_q << 16  [2] first tile  [3] tile stride
  *   [4] tile count  [5] partial slot  [6] first query token  [7] seq length
  * Group record, int32[OSCAR_GROUP_INTS]: request, kv head, first partial slot,
@@ -163,8 +169,9 @@ typedef struct oscar_plan_v1 {
 
 int oscar_attn_plan_v1(const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs,
                        int32_t has_new, int32_t num_kv_heads, int32_t group, int32_t head_dim,
-                       int32_t chunk_tokens, int32_t target_items, int32_t* items,
-                       int32_t max_items, int32_t* groups, int32_t max_groups, oscar_plan_v1* plan);
+                       int32_t chunk_tokens, int32_t target_items, int32_t sink_tokens,
+                       int32_t recent_tokens, int32_t* items, int32_t max_items, int32_t* groups,
+                       int32_t max_groups, oscar_plan_v1* plan);
 
 typedef struct oscar_attn_args_v1 {
   const void* q;                /* [n, Hq, D] rotated queries, OSCAR_BF16 */

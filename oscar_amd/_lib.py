@@ -86,7 +86,7 @@ SIGNATURES = {
     "oscar_store_v1": (C.c_int, [C.POINTER(StoreArgs), vp]),
     "oscar_rotate_v1": (C.c_int, [C.POINTER(RotateArgs), vp]),
     "oscar_attn_plan_v1": (C.c_int, [C.POINTER(i32), C.POINTER(i32), i32, i32, i32, i32, i32,
-                                     i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
+                                     i32, i32, i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
                                      C.POINTER(Plan)]),
     "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),

@@ -320,8 +320,9 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             req = torch.tensor([i for i, _, _ in sub_rows], device=table.device)
             kn = None if not has_new else k_rot[ids]
             vn = None if not has_new else v_rot[ids]
+            window = (self.sink_eff, self._oscar.recent_tokens) if stage is not None else (0, 0)
             plan = ops.plan_decode(sub_qsl, sub_seqs, has_new=has_new, num_kv_heads=hk,
-                                   group=group, head_dim=D, device=query.device)
+                                   group=group, head_dim=D, device=query.device, window=window)
             o, l = ops.attention_decode(q_rot[ids], kn, vn, self.key_cache, self.value_cache,
                                         table[req], plan, self.scale, stage, head_dim=D)
             out_rot[ids], lse[ids] = o, l

@@ -949,27 +949,100 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
 using namespace oscar;
 
 // ----------------------------------------------------------------- planning
+namespace {
+
+// Planning cost of a key tile in units of an INT2 history tile.  Tiles expected to
+// hold staged tokens (the FP32 sink / recent window) or to need the slow path for
+// another reason (current chunk, causal boundary, ragged end) move up to 64 KB of
+// FP32 rows and run one at a time through the whole workgroup, against the 8 KB of
+// code lines of a history tile that the eight waves stream concurrently.  16 is the
+// measured ratio on MI355X (8 x 24K MTP and 64 mixed-length cache-only decodes both
+// end fastest with 12-16).
+constexpr int64_t kSlowCost = 16;
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// The key tiles of a (request, kv head) group as three ranges: head [0, he) (the
+// expected sink window), body [he, ts) (INT2 history) and tail [ts, n) (the
+// expected recent window and the slow-path tiles at the end).
+struct PlanGroup {
+  int req, kvh, n, he, ts;
+  int first_slot;
+  int64_t kh, kb, kt;  // items of head, body, tail (split), or kb items over all tiles
+  bool split;
+};
+
+// items of a range of nr tiles of cost c each when no item may cost more than C
+int64_t range_items(int64_t nr, int64_t c, int64_t C, int64_t max_tiles) {
+  if (nr <= 0) return 0;
+  int64_t cap = C / c;
+  if (cap < 1) cap = 1;
+  if (cap > max_tiles) cap = max_tiles;
+  return ceil_div(nr, cap);
+}
+
+// items when the group's tiles are dealt round-robin as one range: item i of k
+// takes tiles i, i + k, ..., at most ceil(n / k) of them and at most
+// ceil(nh / k) + ceil(nt / k) expensive ones (the head and tail are contiguous)
+int64_t merged_items(const PlanGroup& G, int64_t C, int64_t max_tiles) {
+  const int64_t n = G.n, nh = G.he, nt = G.n - G.ts;
+  auto cost = [&](int64_t k) { return ceil_div(n, k) + (kSlowCost - 1) * (ceil_div(nh, k) + ceil_div(nt, k)); };
+  int64_t lo = ceil_div(n, max_tiles), hi = n;
+  if (lo < 1) lo = 1;
+  if (hi < lo) hi = lo;
+  if (cost(hi) > C) return hi;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) / 2;
+    if (cost(mid) <= C) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+
+// items of group G under the bound C: the cheaper of the split and merged layouts
+// (split on a tie, which keeps the expensive tiles out of the history items);
+// commit = record the choice in G
+int64_t group_items(PlanGroup& G, int64_t C, int64_t max_tiles, bool commit) {
+  if (G.n == 0) {
+    if (commit) { G.split = false; G.kb = 1; G.kh = G.kt = 0; }
+    return 1;
+  }
+  const int64_t kh = range_items(G.he, kSlowCost, C, max_tiles);
+  const int64_t kb = range_items(G.ts - G.he, 1, C, max_tiles);
+  const int64_t kt = range_items(G.n - G.ts, kSlowCost, C, max_tiles);
+  const int64_t merged = merged_items(G, C, max_tiles);
+  const bool split = kh + kb + kt <= merged;
+  if (commit) {
+    G.split = split;
+    if (split) { G.kh = kh; G.kb = kb; G.kt = kt; }
+    else { G.kh = G.kt = 0; G.kb = merged; }
+  }
+  return split ? kh + kb + kt : merged;
+}
+
+}  // namespace
+
 extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32_t num_reqs,
                                   int32_t has_new, int32_t num_kv_heads, int32_t group,
                                   int32_t head_dim, int32_t chunk_tokens, int32_t target_items,
-                                  int32_t* items, int32_t max_items, int32_t* groups,
-                                  int32_t max_groups, oscar_plan_v1* plan) {
-  if (!qsl || !seqs || !plan || num_reqs < 0 || num_kv_heads < 1 || num_kv_heads > 0xffff || group < 1)
+                                  int32_t sink_tokens, int32_t recent_tokens, int32_t* items,
+                                  int32_t max_items, int32_t* groups, int32_t max_groups,
+                                  oscar_plan_v1* plan) {
+  if (!qsl || !seqs || !plan || num_reqs < 0 || num_kv_heads < 1 || num_kv_heads > 0xffff || group < 1 ||
+      sink_tokens < 0 || recent_tokens < 0)
     return fail(-22, "oscar_attn_plan_v1: invalid arguments");
   if (head_dim != 128 && head_dim != 256)
     return fail(-22, "oscar_attn_plan_v1: head_dim %d unsupported (128/256)", head_dim);
   if (chunk_tokens < kTile) chunk_tokens = kTile;
   if (chunk_tokens > kMaxItemTokens) chunk_tokens = kMaxItemTokens;
   if (target_items < 1) target_items = 1;
-  // Per (request, kv head) group: the ceil(seq / 32) key tiles are dealt round-robin
-  // to k items (item j: tiles j, j + k, ...), so a contiguous run of expensive tiles
-  // (the FP32 staging window, the current chunk, the causal boundary) spreads over
-  // the group's items.  k is chosen per group so that no item holds more than T
-  // tiles, with T the smallest bound that keeps the total item count within
-  // target_items (one item per group at least; at most chunk_tokens keys per item).
-  struct Grp { int req, kvh, ntiles, k, first_slot; };
+  // Per group the tiles are cut into head / body / tail (PlanGroup) from the window
+  // hint, and each range is dealt round-robin to its own items (item i of k: tiles
+  // first + i, first + i + k, ...), or, where that takes fewer items, the whole group
+  // is dealt as one range.  The bound C on an item's cost (history tiles + kSlowCost
+  // per expected slow tile) is the smallest that keeps the item count within
+  // target_items (at least one item per group; at most chunk_tokens keys per item).
   int ngroups = 0;
-  int64_t tiles_total = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
@@ -979,77 +1052,104 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
     ngroups += num_kv_heads;
     if (ngroups > (1 << 24)) return fail(-22, "oscar_attn_plan_v1: too many request x kv-head groups");
   }
-  std::vector<Grp> gl((size_t)(ngroups > 0 ? ngroups : 1));
-  int gi = 0;
+  std::vector<PlanGroup> gl;
+  gl.reserve((size_t)ngroups);
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
-    const int ntiles = (seqs[r] + kTile - 1) / kTile;
-    for (int h = 0; h < num_kv_heads; ++h) {
-      gl[gi++] = {r, h, ntiles, 0, 0};
-      tiles_total += ntiles;
+    const int seq = seqs[r];
+    const int hist = has_new ? seq - nq : seq;
+    const int n = (int)ceil_div(seq, kTile);
+    // the slow path takes every tile that reaches the first masked or current key
+    int fe = hist < seq - nq + 1 ? hist : seq - nq + 1;
+    if (fe < 0) fe = 0;
+    int ts = fe / kTile;
+    if (recent_tokens > 0) {
+      const int w0 = seq - recent_tokens > 0 ? seq - recent_tokens : 0;
+      if (w0 / kTile < ts) ts = w0 / kTile;
     }
+    if (ts > n) ts = n;
+    int he = 0;
+    if (sink_tokens > 0) he = (int)ceil_div(sink_tokens < hist ? sink_tokens : hist, kTile);
+    if (he >= ts) he = ts = 0;  // the expected window covers the group
+    for (int h = 0; h < num_kv_heads; ++h) gl.push_back({r, h, n, he, ts, 0, 0, 0, 0, false});
   }
-  const int max_tiles = chunk_tokens / kTile;
-  auto items_for = [&](int64_t T) {
+  const int64_t max_tiles = chunk_tokens / kTile;
+  auto items_for = [&](int64_t C) {
     int64_t total = 0;
-    for (int q = 0; q < ngroups; ++q) total += gl[q].ntiles > 0 ? (gl[q].ntiles + T - 1) / T : 1;
+    for (PlanGroup& G : gl) total += group_items(G, C, max_tiles, false);
     return total;
   };
-  // smallest T in [ceil(total / target), max_tiles] with items_for(T) <= target
-  int64_t lo = (tiles_total + target_items - 1) / target_items, hi = max_tiles;
-  if (lo < 1) lo = 1;
-  if (lo > hi) lo = hi;
+  int64_t lo = 1, hi = kSlowCost * max_tiles;
   while (lo < hi) {
     const int64_t mid = (lo + hi) / 2;
     if (items_for(mid) <= target_items) hi = mid;
     else lo = mid + 1;
   }
-  const int64_t T = lo;
-  int nitems = 0, max_k = 0;
-  for (int q = 0; q < ngroups; ++q) {
-    Grp& G = gl[q];
-    G.k = G.ntiles > 0 ? (int)((G.ntiles + T - 1) / T) : 1;
-    G.first_slot = nitems;
-    nitems += G.k;
-    if (G.k > max_k) max_k = G.k;
+  for (PlanGroup& G : gl) group_items(G, lo, max_tiles, true);
+  int64_t nitems = 0, max_k = 0;
+  for (PlanGroup& G : gl) {
+    const int64_t k = G.split ? G.kh + G.kb + G.kt : G.kb;
+    G.first_slot = (int)nitems;
+    nitems += k;
+    if (k > max_k) max_k = k;
     if (nitems > (1 << 26)) return fail(-22, "oscar_attn_plan_v1: too many work items");
   }
-  plan->num_items = nitems;
+  plan->num_items = (int32_t)nitems;
   plan->num_groups = ngroups;
-  plan->partial_bytes = (int64_t)nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
-  if (items == nullptr || groups == nullptr) return nitems;  // size query
+  plan->partial_bytes = nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
+  if (items == nullptr || groups == nullptr) return (int)nitems;  // size query
   if (nitems > max_items || ngroups > max_groups) return fail(-28, "oscar_attn_plan_v1: buffers too small");
-  // Launch order: items interleaved over the groups (item j of every group, then
-  // j + 1, ...), so that all groups progress together when there are more items
+  // item p of a group: tail items, then head, then body (split), or item p of the
+  // round-robin over all tiles (merged); tiles first + stride * i, i < count
+  auto group_item = [&](const PlanGroup& G, int64_t p, int& first, int& stride, int& count) {
+    int64_t a = 0, b = G.n, k = G.kb;
+    if (G.split) {
+      if (p < G.kt) { a = G.ts; b = G.n; k = G.kt; }
+      else if ((p -= G.kt) < G.kh) { a = 0; b = G.he; k = G.kh; }
+      else { p -= G.kh; a = G.he; b = G.ts; k = G.kb; }
+    }
+    first = (int)(a + p);
+    stride = (int)k;
+    count = b - a > p ? (int)ceil_div(b - a - p, k) : 0;
+    if (count == 0) {
+      first = 0;
+      stride = 1;
+    }
+  };
+  // Launch order: items interleaved over the groups (item p of every group, then
+  // p + 1, ...), so that all groups progress together when there are more items
   // than compute units.  The partial slots of a group stay contiguous for the merge.
-  int idx = 0;
-  for (int pos = 0; pos < max_k; ++pos)
-    for (int q = 0; q < ngroups; ++q) {
-      const Grp& G = gl[q];
-      if (pos >= G.k) continue;
-      int32_t* it = items + (int64_t)idx++ * OSCAR_WORK_INTS;
+  int64_t idx = 0;
+  for (int64_t pos = 0; pos < max_k; ++pos)
+    for (const PlanGroup& G : gl) {
+      const int64_t k = G.split ? G.kh + G.kb + G.kt : G.kb;
+      if (pos >= k) continue;
+      int32_t* it = items + idx++ * OSCAR_WORK_INTS;
       const int nq = qsl[G.req + 1] - qsl[G.req];
+      int first, stride, count;
+      group_item(G, pos, first, stride, count);
       it[0] = G.req;
       it[1] = G.kvh | (nq << 16);
-      it[2] = pos;
-      it[3] = G.k;
-      it[4] = G.ntiles > pos ? (G.ntiles - pos + G.k - 1) / G.k : 0;
-      it[5] = G.first_slot + pos;
+      it[2] = first;
+      it[3] = stride;
+      it[4] = count;
+      it[5] = G.first_slot + (int)pos;
       it[6] = qsl[G.req];
       it[7] = seqs[G.req];
     }
   for (int q = 0; q < ngroups; ++q) {
+    const PlanGroup& G = gl[(size_t)q];
     int32_t* gr = groups + (int64_t)q * OSCAR_GROUP_INTS;
-    gr[0] = gl[q].req;
-    gr[1] = gl[q].kvh;
-    gr[2] = gl[q].first_slot;
-    gr[3] = gl[q].k;
-    gr[4] = qsl[gl[q].req];
-    gr[5] = qsl[gl[q].req + 1] - qsl[gl[q].req];
+    gr[0] = G.req;
+    gr[1] = G.kvh;
+    gr[2] = G.first_slot;
+    gr[3] = (int)(G.split ? G.kh + G.kb + G.kt : G.kb);
+    gr[4] = qsl[G.req];
+    gr[5] = qsl[G.req + 1] - qsl[G.req];
     gr[6] = gr[7] = 0;
   }
-  return nitems;
+  return (int)nitems;
 }
 
 extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream) {

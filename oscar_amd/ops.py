@@ -219,8 +219,12 @@ class DecodePlan:
 
 def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, group: int,
                 head_dim: int, device, target_items: int | None = None,
-                chunk_tokens: int = 8192) -> DecodePlan:
-    """Split-K plan (host): items of whole 32-token tiles, balanced over the CUs."""
+                chunk_tokens: int = 8192, window: tuple = (0, 0)) -> DecodePlan:
+    """Split-K plan (host): items of whole 32-token tiles, balanced over the CUs.
+
+    window = (sink_tokens, recent_tokens) of the FP32 staging window, a balance hint
+    (the expected window tiles go to items of their own); (0, 0) = no window.
+    """
     lib = _lib.load()
     nreq = len(seqs)
     qa = (C.c_int32 * (nreq + 1))(*qsl)
@@ -228,15 +232,17 @@ def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, grou
     if target_items is None:
         target_items = torch.cuda.get_device_properties(device).multi_processor_count
     plan = _lib.Plan()
+    sink, recent = (int(x) for x in window)
     n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
-                               chunk_tokens, target_items, None, 0, None, 0, C.byref(plan))
+                               chunk_tokens, target_items, sink, recent, None, 0, None, 0,
+                               C.byref(plan))
     if n < 0:
         _lib.check(n, "oscar_attn_plan_v1")
     items = (C.c_int32 * max(plan.num_items * WORK_INTS, 1))()
     groups = (C.c_int32 * max(plan.num_groups * GROUP_INTS, 1))()
     n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
-                               chunk_tokens, target_items, items, plan.num_items, groups,
-                               plan.num_groups, C.byref(plan))
+                               chunk_tokens, target_items, sink, recent, items, plan.num_items,
+                               groups, plan.num_groups, C.byref(plan))
     if n < 0:
         _lib.check(n, "oscar_attn_plan_v1")
     host_items = list(items)[: plan.num_items * WORK_INTS]

@@ -75,23 +75,27 @@ def test_ctypes_structs_match_c_layout(tmp_path):
 
 
 # ------------------------------------------------------------------ planner
-def plan(lib, qsl, seqs, has_new=True, hk=1, group=6, d=256, chunk=8192, target=256):
+def plan(lib, qsl, seqs, has_new=True, hk=1, group=6, d=256, chunk=8192, target=256, window=(0, 0)):
     n = len(seqs)
     qa = (C.c_int32 * (n + 1))(*qsl)
     sa = (C.c_int32 * max(n, 1))(*seqs)
     p = _lib.Plan()
-    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, None, 0, None, 0,
-                                 C.byref(p))
+    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, *window, None, 0,
+                                 None, 0, C.byref(p))
     if cnt < 0:
         return cnt, None, None, p
     items = (C.c_int32 * max(p.num_items * 8, 1))()
     groups = (C.c_int32 * max(p.num_groups * 8, 1))()
-    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, items, p.num_items,
-                                 groups, p.num_groups, C.byref(p))
+    cnt = lib.oscar_attn_plan_v1(qa, sa, n, int(has_new), hk, group, d, chunk, target, *window, items,
+                                 p.num_items, groups, p.num_groups, C.byref(p))
     assert cnt == p.num_items
     it = np.array(list(items)[:p.num_items * 8], np.int64).reshape(-1, 8)
     gr = np.array(list(groups)[:p.num_groups * 8], np.int64).reshape(-1, 8)
     return cnt, it, gr, p
+
+
+def item_tiles(it):
+    return it[2] + it[3] * np.arange(it[4])
 
 
 PLAN_CASES = [
@@ -100,12 +104,14 @@ PLAN_CASES = [
     ([0, 1, 1, 5, 10], [0, 257, 3, 263], False, 1, 6),        # cache-only, empty request
     ([0, 4, 6], [1025, 702], True, 2, 4),
     ([0] + list(range(1, 65)), [2048 + 37 * i for i in range(64)], False, 1, 6),
+    ([0] + list(range(1, 65)), [1024 + 487 * i for i in range(64)], False, 1, 6),
 ]
 
 
+@pytest.mark.parametrize("window", [(0, 0), (128, 256), (0, 4096)])
 @pytest.mark.parametrize("qsl,seqs,has_new,hk,group", PLAN_CASES)
-def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, has_new, hk, group):
-    cnt, items, groups, p = plan(lib, qsl, seqs, has_new, hk, group)
+def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, has_new, hk, group, window):
+    cnt, items, groups, p = plan(lib, qsl, seqs, has_new, hk, group, window=window)
     assert cnt > 0
     assert sorted(items[:, 5].tolist()) == list(range(cnt))          # partial slots: a permutation
     assert p.partial_bytes == cnt * 32 * (256 + 1) * 4
@@ -115,33 +121,84 @@ def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, 
         req, kvh, nq, first, stride, count, part, qa, seq = (it[0], it[1] & 0xFFFF, it[1] >> 16, *it[2:8])
         assert nq == qsl[req + 1] - qsl[req] and qa == qsl[req] and seq == seqs[req]
         assert 0 <= kvh < hk and nq * group <= 32
-        assert 0 <= first < stride or (first == 0 and stride == 1)
+        assert 0 <= first and stride >= 1 and (count > 0 or (first == 0 and stride == 1))
         assert count <= 8192 // TILE
         assert count == 0 or (first + stride * (count - 1)) * TILE < seq   # no tile past the end
-    # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous,
-    # item sizes within one tile of each other
+    # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous
     for req, kvh, first_slot, nslots, qa, nq, z0, z1 in groups:
         assert qa == qsl[req] and nq == qsl[req + 1] - qsl[req] and z0 == z1 == 0
         rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh)]
         assert sorted(rows[:, 5].tolist()) == list(range(first_slot, first_slot + nslots))
         cover = np.zeros((seqs[req] + TILE - 1) // TILE, np.int64)
         for it in rows:
-            np.add.at(cover, it[2] + it[3] * np.arange(it[4]), 1)
+            np.add.at(cover, item_tiles(it), 1)
         assert (cover == 1).all()
-        assert rows[:, 4].max() - rows[:, 4].min() <= 1
     assert len(groups) == ngroups
-    # balance across groups: the largest item is the smallest bound that fits the target
-    ntiles = [(seqs[r] + TILE - 1) // TILE for r in range(len(seqs)) if qsl[r + 1] > qsl[r] for _ in range(hk)]
-    T = items[:, 4].max()
-    if T > 1:
-        assert sum(-(-n // (T - 1)) for n in ntiles) > 256
+
+
+def test_plan_without_window_deals_history_evenly(lib):
+    # no window hint: the history tiles of a group go round-robin to items within one
+    # tile of each other; the one tile holding the current chunk goes to an item of its own
+    _, items, _, _ = plan(lib, [0] + [4 * i for i in range(1, 9)], [24580] * 8)
+    for r in range(8):
+        rows = items[items[:, 0] == r]
+        hist_rows = [it for it in rows if item_tiles(it).max() < 768]
+        cur_rows = [it for it in rows if 768 in item_tiles(it)]
+        assert len(cur_rows) == 1 and cur_rows[0][4] == 1
+        sizes = [it[4] for it in hist_rows]
+        assert len(hist_rows) + 1 == len(rows) and max(sizes) - min(sizes) <= 1
+    assert len(items) <= 256 and items[:, 4].max() <= 25
+
+
+def test_plan_puts_the_expected_window_in_items_of_its_own(lib):
+    # 8 x (24576 + 4 MTP), recent window 256: tiles >= (24580 - 256) // 32 = 760 are
+    # expected FP32 (or current) tiles; sink 128 -> tiles 0..3
+    _, items, _, _ = plan(lib, [0] + [4 * i for i in range(1, 9)], [24580] * 8, window=(128, 256))
+    assert len(items) <= 256
+    for it in items:
+        t = item_tiles(it)
+        kinds = {"sink" if x < 4 else ("tail" if x >= 760 else "body") for x in t}
+        assert len(kinds) == 1, (it, kinds)
+    window_items = [it for it in items if item_tiles(it).max() >= 760 or item_tiles(it).min() < 4]
+    assert max(it[4] for it in window_items) >= 2          # several window tiles per item
+    body = [it[4] for it in items if 4 <= item_tiles(it).min() and item_tiles(it).max() < 760]
+    assert max(body) - min(body) <= 1
+
+
+def test_plan_keeps_short_groups_whole(lib):
+    # 64 cache-only requests: a 1024-token request is one item even with the hint
+    # (its 9 window tiles are cheaper together than another item), long ones are split
+    seqs = [1024 + 487 * i for i in range(64)]
+    _, items, _, _ = plan(lib, list(range(65)), seqs, has_new=False, window=(0, 256))
+    assert len(items) <= 256
+    assert (items[:, 0] == 0).sum() == 1
+    for r in (40, 63):
+        rows = items[items[:, 0] == r]
+        w0 = (seqs[r] - 256) // TILE
+        tail = [it for it in rows if item_tiles(it).max() >= w0]
+        assert all(item_tiles(it).min() >= w0 for it in tail)
+
+
+@pytest.mark.parametrize("window", [(0, 0), (128, 256)])
+def test_plan_larger_target_never_makes_items_larger(lib, window):
+    seqs = [1024 + 487 * i for i in range(64)]
+    prev = None
+    for target in (64, 128, 256, 512, 1024):
+        _, items, _, _ = plan(lib, list(range(65)), seqs, has_new=False, target=target, window=window)
+        floor_items = sum(-(-s // (TILE * 256)) for s in seqs)   # at most 256 tiles per item
+        assert len(items) <= max(target, floor_items)
+        big = items[:, 4].max()
+        assert prev is None or big <= prev
+        prev = big
 
 
 def test_plan_launch_order_interleaves_groups(lib):
     _, items, _, _ = plan(lib, [0] + [4 * i for i in range(1, 9)], [24580] * 8)
-    # item j of every group before item j + 1 of any group
-    assert items[:8, 0].tolist() == list(range(8)) and (items[:8, 2] == 0).all()
-    assert (np.diff(items[:, 2]) >= 0).all()
+    # item p of every group before item p + 1 of any group
+    assert items[:8, 0].tolist() == list(range(8))
+    slot0 = {r: items[items[:, 0] == r][:, 5].min() for r in range(8)}
+    pos = np.array([it[5] - slot0[it[0]] for it in items])
+    assert (np.diff(pos) >= 0).all()
 
 
 def test_plan_splits_long_history_across_items(lib):
@@ -159,7 +216,9 @@ def test_plan_rejects_bad_requests(lib):
     qa, sa = (C.c_int32 * 2)(0, 1), (C.c_int32 * 1)(100)
     p = _lib.Plan()
     small = (C.c_int32 * 16)()
-    assert lib.oscar_attn_plan_v1(qa, sa, 1, 1, 1, 6, 256, 32, 64, small, 1, small, 2, C.byref(p)) == -28
+    assert lib.oscar_attn_plan_v1(qa, sa, 1, 1, 1, 6, 256, 32, 64, 0, 0, small, 1, small, 2, C.byref(p)) == -28
+    cnt, *_ = plan(lib, [0, 1], [10], window=(-1, 0))
+    assert cnt == -22
 
 
 def test_empty_plan(lib):

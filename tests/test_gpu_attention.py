@@ -24,14 +24,19 @@ def dev(x, dtype=torch.bfloat16):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
 
 
-def run_decode(c, d=256, hk=1, group=6, target=256):
+def run_decode(c, d=256, hk=1, group=6, target=256, hint=None):
+    """hint: the planner's window hint; default the window make_case stages (sink 128,
+    recent 256) when the case has one."""
     from oscar_amd import ops
 
     kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
     vc = torch.from_numpy(c["v8"]).view(torch.int8).cuda()
     stage = None if c["stage"] is None else tuple(torch.from_numpy(a).cuda() for a in c["stage"])
+    if hint is None:
+        hint = (128, 256) if c["stage"] is not None else (0, 0)
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=c["k"] is not None, num_kv_heads=hk,
-                           group=group, head_dim=d, device=torch.device("cuda"), target_items=target)
+                           group=group, head_dim=d, device=torch.device("cuda"), target_items=target,
+                           window=hint)
     out, lse = ops.attention_decode(dev(c["q"]), None if c["k"] is None else dev(c["k"]),
                                     None if c["v"] is None else dev(c["v"]),
                                     kc, vc, torch.from_numpy(c["bt"]).cuda(), plan, c["scale"],
@@ -65,6 +70,10 @@ DECODE_CASES = [
     # keys growing along the history: each item's running max moves many times
     # (the fast tiles' rescale of O, l and z)
     ("rising_scores", [6000, 2500], [4, 1], {"key_ramp": 4.0, "target": 4}),
+    # the planner's window hint is only a hint: none, and one far wider than the
+    # staged window (window items that hold plain history tiles)
+    ("hint_off", [1025, 2048, 5000], [4, 4, 1], {"hint": (0, 0), "target": 24}),
+    ("hint_wide", [3000, 5000], [4, 1], {"hint": (512, 2048), "target": 24}),
 ]
 
 
@@ -76,7 +85,7 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group,
                         fresh=opts.get("fresh", True), window=opts.get("window", True),
                         key_ramp=opts.get("key_ramp", 0.0))
-    out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256))
+    out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256), opts.get("hint"))
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
     check(out, lse, ref_out, ref_lse, name)
@@ -87,10 +96,10 @@ def test_decode_plan_covers_each_history_token_once(cuda):
     from oscar_amd import ops
 
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=1, group=6,
-                           head_dim=256, device=torch.device("cuda"), target_items=256)
+                           head_dim=256, device=torch.device("cuda"), target_items=256,
+                           window=(128, 256))
     items = np.array(plan.host_items).reshape(-1, 8)
-    # 769 tiles per group, at most 25 per item (24 would need 264 > 256 items)
-    assert plan.num_items == 248 and max(np.array(plan.host_items).reshape(-1, 8)[:, 4]) == 25
+    assert plan.num_items <= 256 and items[:, 4].max() <= 32
     for r, seq in enumerate(c["seqs"]):
         rows = items[items[:, 0] == r]
         cover = np.zeros((seq + 31) // 32, np.int32)
