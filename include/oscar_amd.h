@@ -118,6 +118,10 @@ typedef struct oscar_store_args_v1 {
    * >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
   void* workspace;
   int64_t workspace_bytes;
+  /* calls of <= 64 tokens: one arrival counter per K / V vector, uint32
+   * [2 * 64 * num_kv_heads], zero-initialised once and shared per device (every
+   * call leaves it zero; calls that overlap on one device race on it) */
+  uint32_t* arrivals;
 } oscar_store_args_v1;
 
 int64_t oscar_store_workspace_bytes_v1(int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim);

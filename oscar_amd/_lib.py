@@ -42,7 +42,7 @@ class StoreArgs(C.Structure):
         ("recent_tokens", i32), ("sink_tokens_eff", i32),
         ("query_rot", vp), ("key_rot", vp), ("value_rot", vp),
         ("slot_claims", vp), ("seat_claims", vp), ("epoch_counter", vp),
-        ("workspace", vp), ("workspace_bytes", i64),
+        ("workspace", vp), ("workspace_bytes", i64), ("arrivals", vp),
     ]
 
 

@@ -483,141 +483,143 @@ __global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
   quant_vector<D>(p, kind, vec / hk, vec % hk, d, x4, rows[wave], &clip_slot[wave]);
 }
 
-// Calls of at most kFusedTokens tokens (decode and MTP steps): one launch.  A
-// workgroup rotates whole vectors -- one K or V vector (token, kv head), or kQPW
-// query heads of a token -- with R streamed through LDS in blocks of QR rows (two
-// buffers: the loads of block b + 1 overlap the arithmetic on block b) and
-// the contraction split over KP parts of the rows (fp64 accumulation, parts added
-// in order: the fp32 result is the correctly rounded one); wave 0 then quantizes,
-// packs and scatters a K / V vector in place (quant_vector, winners by scanning)
-// and writes the read-path copies.
+// Calls of at most kFusedTokens tokens (decode and MTP steps): one launch of
+// workgroups (token, vectors, column slice).  A workgroup rotates its vectors -- one
+// K or V vector (token, kv head), or kQPW query heads of a token -- for one slice of
+// kSliceCols output columns, so that no compute unit streams more than D x kSliceCols
+// of R: each thread loads RPT rows x 4 columns of the slice straight into registers,
+// the products accumulate in fp64 and the KP parts of the contraction are added in
+// order (the fp32 result is the correctly rounded one).  Query slices go to
+// query_rot.  K / V slices go to the read-path copies and to the workspace; the last
+// slice workgroup of a vector to arrive (one counter per vector that atomicInc wraps
+// back to zero) reads the whole vector back and quantizes, packs and scatters it in
+// place (quant_vector, winners by scanning).  The slices pass through the workspace
+// with agent-scope stores and loads, which bypass the per-XCD L2, ordered by the
+// store wait, the barrier and the counter; an agent-scope fence would instead write
+// back and invalidate the whole L2 in every workgroup.
 constexpr int64_t kFusedTokens = 64;
-constexpr int kQPW = 2;  // query heads per fused workgroup
+constexpr int kQPW = 2;         // query heads per fused workgroup
+constexpr int kSliceCols = 128;  // output columns per fused workgroup
+constexpr int kSmallThreads = 512;
 
 template <int D, int XT>
-__global__ __launch_bounds__(kThreads) void store_small_kernel(StoreParams p) {
-  constexpr int NL = D / 4;             // lanes of a 4-column group
-  constexpr int KP = kThreads / NL;     // parts of the contraction
-  constexpr int QR = D > 128 ? D / 4 : D;    // rows of R per streamed block
-  constexpr int NQB = D / QR;                 // blocks
-  constexpr int NBUF = NQB > 1 ? 2 : 1;
+__global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams p) {
+  constexpr int SC = D < kSliceCols ? D : kSliceCols;
+  constexpr int NS = D / SC;            // column slices of a vector
+  constexpr int CG = SC / 4;            // 4-column groups of a slice
+  constexpr int KP = kSmallThreads / CG;     // parts of the contraction
+  constexpr int RPT = D / KP;           // rows of R per thread
+  static_assert(RPT >= 1 && D % KP == 0 && kQPW * 4 * CG <= kSmallThreads, "slice shape");
   const oscar_store_args_v1& a = p.a;
   const int64_t hk = a.cache.num_kv_heads;
   const int64_t t = blockIdx.x;
   const int yb = blockIdx.y;
+  const int c0 = blockIdx.z * SC;
   const int kind = yb < hk ? KIND_K : (yb < 2 * hk ? KIND_V : KIND_Q);
   const int64_t h0 = kind == KIND_K ? yb : (kind == KIND_V ? yb - hk : (int64_t)(yb - 2 * hk) * kQPW);
   const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
   const int nv = kind == KIND_Q ? (heads - h0 < kQPW ? (int)(heads - h0) : kQPW) : 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cg = tid % NL, kp = tid / NL;
+  const int cg = tid % CG, kp = tid / CG;
   const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
   const int64_t src_stride = kind == KIND_K ? a.key_stride_token
                            : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
   const float* R = (kind == KIND_V) ? a.rv : a.rk;
   void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
 
-  __shared__ __attribute__((aligned(16))) float s_r[NBUF][QR * D];
   __shared__ float s_x[kQPW][D];
-  __shared__ double s_red[KP - 1][kQPW][4][NL];
+  __shared__ double s_red[KP][kQPW * 4 * CG];
+  __shared__ float s_y[kQPW][SC];
   __shared__ float s_row[D];
   __shared__ float s_clip;
-  // the destination of a K / V vector: its loads go out first and overlap the rotation
+  __shared__ int s_last;
+  // this thread's rows kp + KP * i of the slice: issued first, used after the barrier
+  f32x4 r4[RPT];
+  if (R != nullptr) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) r4[i] = *(const f32x4*)(R + (int64_t)(kp + KP * i) * D + c0 + 4 * cg);
+  }
+  // the destination of a K / V vector: its loads overlap the rotation (only the last
+  // slice to arrive uses it)
   Dest dest{};
   if (kind != KIND_Q && wave == 0) dest = vector_dest<true>(p, kind, t, 0);
   // the input vectors (fp32 in LDS; slots past nv are zero)
-  for (int e = tid; e < kQPW * D; e += kThreads)
+  for (int e = tid; e < kQPW * D; e += kSmallThreads)
     if (e >= nv * D) s_x[e / D][e % D] = 0.f;
-  for (int e = tid; e < nv * (D / 8); e += kThreads) {
+  for (int e = tid; e < nv * (D / 8); e += kSmallThreads) {
     const int v = e / (D / 8), k8 = (e % (D / 8)) * 8;
     float xv[8];
     load8<XT>(src, t * src_stride + (h0 + v) * D + k8, xv);
 #pragma unroll
     for (int j = 0; j < 8; ++j) s_x[v][k8 + j] = xv[j];
   }
+  __syncthreads();
   double acc[kQPW][4];
-#pragma unroll
-  for (int v = 0; v < kQPW; ++v)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[v][j] = 0.0;
   if (R != nullptr) {
-    // block q = rows [q * QR, (q + 1) * QR) of R, moved through registers: thread tid
-    // holds the 16-byte chunks tid + kThreads * i of the block
-    constexpr int CH = QR * D / 4 / kThreads;  // 16-byte chunks per thread
-    f32x4 nxt[CH];
-    auto load = [&](int q) {
-      const f32x4* src4 = (const f32x4*)(R + (int64_t)q * QR * D);
-#pragma unroll
-      for (int i = 0; i < CH; ++i) nxt[i] = src4[tid + kThreads * i];
-    };
-    auto stash = [&](int q) {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) *(f32x4*)&s_r[q % NBUF][4 * (tid + kThreads * i)] = nxt[i];
-    };
-    load(0);
-    stash(0);
-    __syncthreads();  // block 0 and the input vectors are in LDS
-    for (int q = 0; q < NQB; ++q) {
-      if (q + 1 < NQB) load(q + 1);  // in flight during the arithmetic on block q
-      const float* rb = s_r[q % NBUF];
-      // rows kl = kp + KP * i of this block, all read before the FMAs
-      f32x4 r4[QR / KP];
-      float xs[QR / KP][kQPW];
-#pragma unroll
-      for (int i = 0; i < QR / KP; ++i) {
-        const int kl = kp + KP * i;
-        r4[i] = *(const f32x4*)&rb[kl * D + 4 * cg];
-#pragma unroll
-        for (int v = 0; v < kQPW; ++v) xs[i][v] = s_x[v][q * QR + kl];
-      }
-#pragma unroll
-      for (int i = 0; i < QR / KP; ++i)
-#pragma unroll
-        for (int v = 0; v < kQPW; ++v) {
-          const double x = xs[i][v];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[v][j] = fma(x, (double)r4[i][j], acc[v][j]);
-        }
-      if (q + 1 < NQB) stash(q + 1);  // block q - 1's buffer: free since the last barrier
-      __syncthreads();
-    }
-  } else {
-    __syncthreads();
-    if (kp == 0) {
-#pragma unroll
-      for (int v = 0; v < kQPW; ++v)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[v][j] = v < nv ? (double)s_x[v][4 * cg + j] : 0.0;
-    }
-  }
-  // parts 1..KP-1 to LDS, part 0 adds them in order
-  if (kp > 0) {
 #pragma unroll
     for (int v = 0; v < kQPW; ++v)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s_red[kp - 1][v][j][cg] = acc[v][j];
+      for (int j = 0; j < 4; ++j) acc[v][j] = 0.0;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int v = 0; v < kQPW; ++v) {
+        const double x = s_x[v][kp + KP * i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[v][j] = fma(x, (double)r4[i][j], acc[v][j]);
+      }
+  } else {
+#pragma unroll
+    for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[v][j] = kp == 0 ? (double)s_x[v][c0 + 4 * cg + j] : 0.0;
+  }
+  // the KP parts to LDS; thread e < kQPW * SC adds the parts of output e in order
+#pragma unroll
+  for (int v = 0; v < kQPW; ++v)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_red[kp][(v * 4 + j) * CG + cg] = acc[v][j];
+  __syncthreads();
+  if (tid < kQPW * 4 * CG) {
+    double sum = 0.0;
+#pragma unroll 8
+    for (int w = 0; w < KP; ++w) sum += s_red[w][tid];
+    const int v = tid / (4 * CG), j = (tid / CG) % 4, g4 = tid % CG;
+    s_y[v][4 * g4 + j] = (float)sum;
   }
   __syncthreads();
-  if (wave != 0) return;
-  const bool active = lane < NL;  // kp == 0
-  float y[kQPW][4];
+  if (tid < kQPW * CG) {
+    const int v = tid / CG, g4 = tid % CG;
+    if (v < nv) {
+      const f32x4 y4 = *(const f32x4*)&s_y[v][4 * g4];
+      float y[4] = {y4[0], y4[1], y4[2], y4[3]};
+      const int64_t hq = kind == KIND_Q ? a.num_q_heads : hk;
+      if (rot_out != nullptr) store4<XT>(rot_out, (t * hq + h0 + v) * D + c0 + 4 * g4, y);
+      if (kind != KIND_Q) {
+        // agent-coherent stores (past this XCD's L2), read back the same way below
+        float* yw = p.y + (((int64_t)kind * a.num_tokens + t) * hk + h0) * D + c0 + 4 * g4;
 #pragma unroll
-  for (int v = 0; v < kQPW; ++v)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      double sum = acc[v][j];
-      if (R != nullptr)
-        for (int w = 0; w < KP - 1; ++w) sum += s_red[w][v][j][active ? cg : 0];
-      y[v][j] = (float)sum;
+        for (int j = 0; j < 4; ++j) __hip_atomic_store(yw + j, y[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-  if (active && rot_out != nullptr) {
-    const int64_t hq = kind == KIND_Q ? a.num_q_heads : hk;
-#pragma unroll
-    for (int v = 0; v < kQPW; ++v)
-      if (v < nv) store4<XT>(rot_out, (t * hq + h0 + v) * D + 4 * cg, y[v]);
   }
   if (kind == KIND_Q) return;
-  quant_vector<D>(p, kind, t, h0, dest, f32x4{y[0][0], y[0][1], y[0][2], y[0][3]}, s_row, &s_clip);
+  // the slice is written (stores complete before the barrier): count it in; the last
+  // of the vector's slices to arrive goes on
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if constexpr (NS > 1) {
+    if (tid == 0)
+      s_last = atomicInc(&a.arrivals[((int64_t)kind * a.num_tokens + t) * hk + h0], NS - 1) == NS - 1;
+    __syncthreads();
+    if (!s_last) return;
+  }
+  if (wave != 0) return;
+  const float* yv = p.y + (((int64_t)kind * a.num_tokens + t) * hk + h0) * D + 4 * (lane < D / 4 ? lane : 0);
+  f32x4 x4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x4[j] = __hip_atomic_load(yv + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  quant_vector<D>(p, kind, t, h0, dest, x4, s_row, &s_clip);
 }
 
 template <int D, int TV>
@@ -633,10 +635,10 @@ int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_
   if (p.a.num_tokens <= kFusedTokens && p.scan) {
     const int64_t hk = p.a.cache.num_kv_heads;
     const int64_t qg = q_vec ? (p.a.num_q_heads + kQPW - 1) / kQPW : 0;
-    dim3 grid((unsigned)p.a.num_tokens, (unsigned)(2 * hk + qg));
-    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kThreads), 0, s, p);
-    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
-    else hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F32>), grid, dim3(kThreads), 0, s, p);
+    dim3 grid((unsigned)p.a.num_tokens, (unsigned)(2 * hk + qg), (unsigned)(D < kSliceCols ? 1 : D / kSliceCols));
+    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kSmallThreads), 0, s, p);
+    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kSmallThreads), 0, s, p);
+    else hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F32>), grid, dim3(kSmallThreads), 0, s, p);
     OSCAR_CHECK_LAUNCH("store_small_kernel");
     return 0;
   }
@@ -728,6 +730,8 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
   const int64_t need = oscar_store_workspace_bytes_v1(a.num_tokens, a.cache.num_kv_heads, D);
   if (a.workspace == nullptr || a.workspace_bytes < need || (((uintptr_t)a.workspace) & 15))
     return fail(-22, "oscar_store_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
+  if (a.num_tokens <= kFusedTokens && (a.arrivals == nullptr || (((uintptr_t)a.arrivals) & 3)))
+    return fail(-22, "oscar_store_v1: calls of <= %lld tokens need the arrivals counters", (long long)kFusedTokens);
   StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size,
                 a.num_tokens <= kScanTokens};
   const int64_t kv_vec = a.num_tokens * a.cache.num_kv_heads;

@@ -73,6 +73,7 @@ class DeviceScratch:
         self.slot_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.seat_claims = torch.zeros(0, dtype=torch.int64, device=device)
         self.store_ws = torch.empty(0, dtype=torch.uint8, device=device)
+        self.arrivals = torch.zeros(0, dtype=torch.int32, device=device)
         self.attn_ws = torch.empty(0, dtype=torch.uint8, device=device)
         self.prefill_ws = torch.empty(0, dtype=torch.uint8, device=device)
 
@@ -98,6 +99,14 @@ class DeviceScratch:
         if self.store_ws.numel() < nbytes:
             self.store_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self.store_ws
+
+    def store_arrivals(self, num_kv_heads: int) -> torch.Tensor:
+        """Arrival counters of the one-launch store (calls of <= 64 tokens): zeroed
+        once, and every call leaves them zero."""
+        need = 2 * 64 * num_kv_heads
+        if self.arrivals.numel() < need:
+            self.arrivals = torch.zeros(need, dtype=torch.int32, device=self.device)
+        return self.arrivals
 
     def prefill_workspace(self, nbytes: int) -> torch.Tensor:
         if self.prefill_ws.numel() < nbytes:
@@ -176,6 +185,7 @@ def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=N
     need = lib.oscar_store_workspace_bytes_v1(n, hk, head_dim)
     ws = scratch.store_workspace(need)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.arrivals = scratch.store_arrivals(hk).data_ptr()
     _lib.check(lib.oscar_store_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_store_v1")
 
 
