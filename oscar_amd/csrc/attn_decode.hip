@@ -10,9 +10,10 @@
 // the current (rotated, unquantized) chunk.
 //
 // Work decomposition: the host plan (oscar_attn_plan_v1) deals the 32-token key
-// tiles of every (request, kv-head) group round-robin to items of at most T tiles
-// (T the smallest bound that fits the target item count).  One 512-thread
-// workgroup (8 waves, two per SIMD) per item; wave w takes item tiles w, w + 8, ...
+// tiles of every (request, kv-head) group round-robin to items, the expected staging
+// window and slow tail in items of their own, under a bound on the item cost.  One
+// 512-thread workgroup (8 waves, two per SIMD) per item; wave w starts with item
+// tiles w and w + 8 and then takes the next fast tile from a shared counter.
 // Pages hold a multiple of 32 tokens, so a tile never straddles a page: its block
 // id, seat row and in-page offset are wave-uniform scalars.  The eight wave
 // partials are merged in LDS and the item partial (normalised O in MFMA register
@@ -245,6 +246,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   __shared__ __attribute__((aligned(16))) float s_ml[kWaves][2][32];
   __shared__ __attribute__((aligned(16))) u32x4 s_q[C::KSTEPS][64];        // Q^T operand
   __shared__ uint64_t s_slowset[kMaxItemTokens / kTile / 64];  // slow-set bits of the item tiles
+  __shared__ int s_next;                               // next item tile for the fast loop
   __shared__ int16_t s_slow[kMaxItemTokens / kTile];             // the slow tiles, ascending
   __shared__ uint32_t s_tmask[kMaxItemTokens / kTile]; // staged-token mask of every item tile
   // the slow tiles' staged FP32 K / V rows [2][kTile / TPR][SROW], moved by
@@ -266,7 +268,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   uint8_t (*s_vcode)[kTile * C::NB] = (uint8_t (*)[kTile * C::NB])s_u;
   const unsigned st_rows = (unsigned)P.st.rows;
 
-  // wave w takes item tiles j = w + kWaves * i, i < my (my <= 32)
+  // prologue share of wave w: item tiles j = w + kWaves * i, i < my (my <= 32), whose
+  // pages, owner tags and (the first two) data it loads
   const int my = count > wave ? (count - 1 - wave) / kWaves + 1 : 0;
   const uint8_t* kbase = A.cache.k + (int64_t)kvh * A.cache.k_stride[2];
   const uint8_t* vbase = A.cache.v + (int64_t)kvh * A.cache.v_stride[2];
@@ -446,8 +449,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (lane == 0) s_slowset[wave] = b;
   }
   __syncthreads();
-  // the slow list (ascending tile order), and bit i of myslow = slow tile i of
-  // this wave (tile wave + kWaves * i)
+  // the slow list (ascending tile order)
   int nslow = 0;
 #pragma unroll
   for (int w = 0; w < (kMaxItemTokens / kTile) / 64; ++w) {
@@ -456,8 +458,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     nslow += __popcll(word);
   }
   nslow = __builtin_amdgcn_readfirstlane(nslow);
-  const int jl = (wave + kWaves * lane) & (kMaxItemTokens / kTile - 1);  // lanes >= my: any in-range index
-  const uint32_t myslow = (uint32_t)__ballot(lane < my && ((s_slowset[jl >> 6] >> (jl & 63)) & 1ull));
+  if (tid == 0) s_next = 2 * kWaves;  // the tiles after every wave's first two
   __syncthreads();
   u32x4* s_kop = (u32x4*)s_u;                                 // [kTile][2][NCH][2]
   uint16_t* s_slowv = (uint16_t*)(s_u + kKopBytes);           // [kTile][VROW]
@@ -734,25 +735,55 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     __builtin_amdgcn_wave_barrier();  // the LDS slots are rewritten by the next tile
   };
 
-  // Two register slots hold the packed data of the wave's next tiles: slot A the
-  // even tiles, slot B the odd ones.  A slot is refilled (index clamped to the last
-  // tile, so every path issues the same loads) as soon as its tile's QK has consumed
-  // it, so the next two tiles are in flight while a tile is computed.
-  // Tiles of the slow set were run before the loop: their slots are refilled
-  // without compute.
-  auto is_slow = [&](int i) { return ((myslow >> i) & 1u) != 0; };
-  for (int i = 0; i < my; i += 2) {
+  // Two register slots hold the packed data of the wave's next two tiles.  The
+  // first two of a wave are its item tiles w and w + kWaves (loaded in the
+  // prologue); after that a wave takes the next fast tile from the shared counter
+  // s_next (slow tiles are passed over), so that the waves of the item finish
+  // together however their loads are served.  A slot is refilled as soon as its
+  // tile's QK has consumed it (with a placeholder load once the tiles run out, so
+  // every path issues the same loads), so the next two tiles are in flight while a
+  // tile is computed.  A slow tile among the first two is refilled without compute.
+  auto slow_bit = [&](int j) { return ((s_slowset[j >> 6] >> (j & 63)) & 1ull) != 0; };
+  auto take = [&]() {
+    int j;
+    do {
+      int v = 0;
+      if (lane == 0) v = atomicAdd(&s_next, 1);
+      j = __builtin_amdgcn_readfirstlane(v);
+    } while (j < count && slow_bit(j));
+    return j < count ? j : count;
+  };
+  // page of item tile j (j >= count: the placeholder, block 0 at offsets 0..31)
+  auto load_next = [&](int j, TileRegs<D>& r) {
+    const bool real = j < count;
+    const int off0 = real ? tile_t0(j) % bs : 0;
+    r.blk = real ? __builtin_amdgcn_readfirstlane(s_blk[j]) : 0;
+    const int off = off0 + m;
+    const uint8_t* ks = kbase + (int64_t)r.blk * ks0 + (int64_t)off * ks1;
+    const uint8_t* vs = vbase + (int64_t)r.blk * vs0 + (int64_t)off * vs1;
+#pragma unroll
+    for (int i = 0; i < C::NQ; ++i) {
+      r.k[i] = *(const u32x4*)(ks + 32 + g * (D / 8) + 16 * i);
+      r.v[i] = *(const u32x4*)(vs + g * (D / 8) + 16 * i);
+    }
+    r.meta = *(const u32x2*)ks;
+  };
+  int jA = my > 0 ? wave : count;
+  int jB = my > 1 ? wave + kWaves : count;
+  while (jA < count || jB < count) {
     {
-      const bool fast = !is_slow(i);
+      const bool fast = jA < count && !slow_bit(jA);
       f32x16 S;
       if (fast) qk_tile(RA, S);
-      load_tile(i + 2 < last ? i + 2 : last, RA);
+      jA = take();
+      load_next(jA, RA);
       if (fast) pv_tile(S);
     }
-    const bool fast = i + 1 < my && !is_slow(i + 1);
+    const bool fast = jB < count && !slow_bit(jB);
     f32x16 S;
     if (fast) qk_tile(RB, S);
-    load_tile(i + 3 < last ? i + 3 : last, RB);
+    jB = take();
+    load_next(jB, RB);
     if (fast) pv_tile(S);
   }
 
@@ -794,22 +825,27 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const float fw = (m_run == -INFINITY || !(L > 0.f)) ? 0.f : exp2f(m_run - M) / L;
   f32x4* buf = (f32x4*)s_u;  // [kWaves][2 blocks][4][64] f32x4
   f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
+  // only the item's rows move through LDS (lane l and thread t hold row l % 32 / t % 32)
+  const bool my_row = (lane & 31) < nrows;
 #pragma unroll
   for (int rb = 0; rb < C::MBLK / 2; ++rb) {
+    if (my_row) {
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb)
+      for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x16& Ob = O[2 * rb + bb];
-        buf[((wave * 2 + bb) * 4 + q) * 64 + lane] =
-            f32x4{Ob[4 * q] * fw, Ob[4 * q + 1] * fw, Ob[4 * q + 2] * fw, Ob[4 * q + 3] * fw};
-      }
+        for (int q = 0; q < 4; ++q) {
+          const f32x16& Ob = O[2 * rb + bb];
+          buf[((wave * 2 + bb) * 4 + q) * 64 + lane] =
+              f32x4{Ob[4 * q] * fw, Ob[4 * q + 1] * fw, Ob[4 * q + 2] * fw, Ob[4 * q + 3] * fw};
+        }
+    }
     __syncthreads();
-    f32x4 acc = buf[tid];
+    if (my_row) {
+      f32x4 acc = buf[tid];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) acc += buf[w * kThreads + tid];
-    const int e = rb * kThreads + tid;  // f32x4 index of the partial (row = e % 32)
-    if ((e & 31) < nrows) po[e] = acc;
+      for (int w = 1; w < kWaves; ++w) acc += buf[w * kThreads + tid];
+      po[rb * kThreads + tid] = acc;  // f32x4 index of the partial (row = index % 32)
+    }
     __syncthreads();
   }
   if (tid < 32) {
