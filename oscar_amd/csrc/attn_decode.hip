@@ -42,11 +42,12 @@
 //  * softmax against a lazy reference max per row: it moves (rescaling O, l, z) only
 //    when a tile's max exceeds it by more than kLazy, so p <= 2^kLazy.
 //
-// Slow tiles run after the fast tiles, one at a time by the whole workgroup: the
-// staged FP32 rows go straight to LDS (global_load_lds), all threads build the
-// tile's K operands and V values in LDS
-// (staged rows, codes or current chunk, rounded as the reference does), and one
-// wave adds the tile to its softmax state with P split into bf16 hi + lo parts.
+// Slow tiles run after the fast tiles, one at a time by the whole workgroup: every
+// thread loads its share of the tile (staged FP32 values, codes or current chunk)
+// into registers one tile ahead, all threads build the tile's K operands and V
+// values in LDS (rounded as the reference does), and one wave adds the tile to its
+// softmax state with P split into bf16 hi + lo parts while the next tile's loads
+// are in flight.
 #include <vector>
 
 #include "common.h"
@@ -76,8 +77,6 @@ struct Cfg {
   static constexpr int NB = D / 4;       // code bytes per token
   static constexpr int MBLK = D / 32;    // PV output blocks (32 d each)
   static constexpr int VROW = D + 8;     // bf16 per row of the slow-tile V buffer
-  static constexpr int TPR = 256 / D;     // tokens per 1-KB row of the slow-tile staged rows
-  static constexpr int SROW = 260;        // fp32 per such row (16-byte pad)
   static constexpr int NV = MBLK * 4 * 64;  // f32x4 of one item partial (register order)
 };
 
@@ -260,12 +259,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   __shared__ int s_next;                               // next item tile for the fast loop
   __shared__ int16_t s_slow[kMaxItemTokens / kTile];             // the slow tiles, ascending
   __shared__ uint32_t s_tmask[kMaxItemTokens / kTile]; // staged-token mask of every item tile
-  // the slow tiles' staged FP32 K / V rows [2][kTile / TPR][SROW], moved by
-  // global_load_lds after the fast tiles.  (An LDS DMA still pending at the fast loop
-  // makes the compiler wait for every outstanding load before the loop's LDS accesses,
-  // which empties the two-tile prefetch, so none is issued before the loop.)
-  constexpr int kRowsBytes = 2 * (kTile / C::TPR) * C::SROW * 4;
-  __shared__ __attribute__((aligned(16))) float s_rows[kRowsBytes / 4];
   // union of the phases: V codes of each wave's current fast tile [kWaves][kTile * NB];
   // the slow tile's K operands (bf16 pairs in MFMA order) [kTile][2][NCH][8] and V
   // values (bf16, permuted columns) [kTile][VROW]; the cross-wave merge rounds of two
@@ -433,12 +426,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // The slow set: tiles with a staged token (owner tag == block, from the tags
   // loaded in the prologue) or past the fast range (current chunk, causal
   // boundary, ragged end).  The fast tiles skip them; they run after the fast
-  // tiles, one at a time by the whole workgroup: (1) the staged FP32 rows of the
-  // tile's staged tokens go straight to LDS, and every
-  // thread loads the codes, constants or current-chunk values of its share (token
-  // tid / 16); (2) the threads build the tile's K operands and V values into LDS
-  // with the reference rounding; (3) one wave (round-robin) adds the tile to its
-  // softmax state (the wave states are merged at the end).
+  // tiles, one at a time by the whole workgroup: (1) every thread loads the staged
+  // FP32 values, codes and constants or current-chunk values of its share (token
+  // tid / 16) into registers, one tile ahead; (2) the threads build the tile's K
+  // operands and V values into LDS with the reference rounding; (3) one wave
+  // (round-robin) adds the tile to its softmax state (the wave states are merged at
+  // the end).
 #pragma unroll
   for (int ii = 0; ii < kTagRounds; ++ii) {
     if (2 * ii >= my) break;
@@ -477,132 +470,106 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // 4 * NCH (K|V, half, 16-element chunk) units of the token
   constexpr int NU = C::NCH / 4;
   const int bt = tid >> 4, bpart = tid & 15;
-  // staged rows of slow tile j straight to LDS (all threads): lane l moves the
-  // 16-byte chunk l % (D / 4) of the row of seat l / (D / 4) of the TPR seats
-  const char* lane_row = (const char*)P.st.stage_k + 16 * (lane % (D / 4)) + (int64_t)(lane / (D / 4)) * hk * D * 4;
-  const int64_t vdelta = (const char*)P.st.stage_v - (const char*)P.st.stage_k;
-  auto issue_rows = [&](int j) {
-    // an opaque copy of the lane base: the per-row sums stay in the loop (one
-    // 64-bit add each) instead of being hoisted into eight live register pairs
-    const char* lrow = lane_row;
-    asm volatile("" : "+v"(lrow));
-    const uint32_t smask = s_tmask[j];
+  // A slow tile's inputs, per thread (token bt, units u < NU): the staged FP32
+  // values (4 x 16 bytes per unit), or the codes (one word per unit, constants in
+  // meta), or the current chunk's bf16 values (lo / hi 16 bytes per unit in x[u][0..1])
+  // -- loaded into registers one tile ahead, so the next tile's loads are in flight
+  // while the runner wave computes the current one.
+  f32x4 sx[NU][4];
+  u32x2 smeta = {0u, 0u};
+  auto slow_flags = [&](int j, bool& b_staged, bool& b_codes, bool& b_cur) {
+    const int bp = tile_t0(j) + bt;
+    b_staged = (s_tmask[j] >> bt) & 1u;
+    b_codes = bp < hist && !b_staged;
+    b_cur = has_new && bp >= hist && bp < seq;
+  };
+  auto load_slow = [&](int j) {
     const int t0 = tile_t0(j);
     int blk, off0, seat0;
     tile_page(j, t0, blk, off0, seat0);
-    if (smask != 0) {
-      // row r = wave + kWaves * i: K (r < R) or V rows of tokens TPR * (r % R) + u,
-      // u < TPR; lane l moves the 16-byte chunk l of the row straight to LDS (tokens
-      // outside the mask are skipped)
-      constexpr int R = kTile / C::TPR, CPT = D / 4;
+    bool b_staged, b_codes, b_cur;
+    slow_flags(j, b_staged, b_codes, b_cur);
+    const int bp = t0 + bt;
+    const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)(off0 + bt) * ks1;
+    const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)(off0 + bt) * vs1;
+    const int64_t cur_off = (int64_t)(qa + (b_cur ? bp - hist : 0)) * A.kv_new_stride_token + (int64_t)kvh * D;
+    const int64_t seat_row = ((int64_t)seat0 + off0 + bt) * hk + kvh;  // staged row of the token
+    smeta = b_codes ? *(const u32x2*)ks : u32x2{0u, 0u};
 #pragma unroll
-      for (int i = 0; i < 2 * R / kWaves; ++i) {
-        const int r = wave + kWaves * i, kv = r / R;
-        const int tok = C::TPR * (r % R) + lane / CPT;
-        if ((smask >> tok) & 1u) {
-          // one per-lane base plus wave-uniform byte offsets (nothing kept per row)
-          const int64_t seat = (int64_t)seat0 + off0 + C::TPR * (r % R);
-          const int64_t uoff = (kv ? vdelta : 0) + ((seat * hk + kvh) * D) * 4;
-          __builtin_amdgcn_global_load_lds(lrow + uoff,
-                                           (__attribute__((address_space(3))) void*)(s_rows + r * C::SROW), 16, 0, 0);
+    for (int u = 0; u < NU; ++u) {
+      const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
+      if (b_staged) {
+        const f32x4* src = (const f32x4*)((kv ? P.st.stage_v : P.st.stage_k) + seat_row * D + hg * (D / 2) + 16 * c);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) sx[u][x] = src[x];
+      } else if (b_codes) {
+        sx[u][0][0] = __uint_as_float(*(const uint32_t*)((kv ? vs : ks + 32) + hg * (D / 8) + 4 * c));
+      } else if (b_cur) {
+        const uint16_t* src = (const uint16_t*)(kv ? A.v_new : A.k_new) + cur_off + hg * (D / 2) + 16 * c;
+        sx[u][0] = __builtin_bit_cast(f32x4, *(const u32x4*)src);
+        sx[u][1] = __builtin_bit_cast(f32x4, *(const u32x4*)(src + 8));
+      }
+    }
+  };
+  // slow tile j (its inputs loaded by load_slow): every thread builds its units' K
+  // operands and V values into LDS with the reference rounding
+  auto build_slow = [&](int j) {
+    bool b_staged, b_codes, b_cur;
+    slow_flags(j, b_staged, b_codes, b_cur);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
+      unsigned o[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      if (b_staged) {
+        const f32x4* f = sx[u];
+        if (kv == 0) {
+          // K operand pairs in the lookup's order (e, e+4) / (e+8, e+12)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            o[x] = hist_pair(f[0][x], f[1][x]);
+            o[4 + x] = hist_pair(f[2][x], f[3][x]);
+          }
+        } else {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) o[x] = hist_pair(f[x >> 2][x & 3], f[2 + (x >> 2)][x & 3]);
+        }
+      } else if (kv == 0) {
+        if (b_cur) {
+          kpairs16(__builtin_bit_cast(u32x4, sx[u][0]), __builtin_bit_cast(u32x4, sx[u][1]), o);
+        } else if (b_codes) {
+          unsigned t_lo, t_hi;
+          byte_tables(smeta[0], t_lo, t_hi);
+          lut16(__float_as_uint(sx[u][0][0]), t_lo, t_hi, o);
+        }
+      } else {
+        // V values as (e, e+8) pairs
+        if (b_cur) {
+          interleave8(__builtin_bit_cast(u32x4, sx[u][0]), __builtin_bit_cast(u32x4, sx[u][1]), o);
+        } else if (b_codes) {
+          unsigned vlo, vhi;
+          value_table(smeta[1], vlo, vhi);
+          table_pairs(__float_as_uint(sx[u][0][0]), vlo, vhi, o);
+        }
+      }
+      if (kv == 0) {
+        u32x4* dst = s_kop + ((bt * 2 + hg) * C::NCH + c) * 2;
+        dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+        dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+      } else {
+        // to the V buffer, columns permuted so that MFMA row i of output block b
+        // reads column 32 b + i (d = pv_d(b, i))
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x2 w = {__builtin_amdgcn_perm(o[q + 4], o[q], 0x05040100u),
+                           __builtin_amdgcn_perm(o[q + 4], o[q], 0x07060302u)};
+          *(u32x2*)&s_slowv[bt * C::VROW + vbuf_col<D>(hg, q, c)] = w;
         }
       }
     }
   };
-  // slow tile j (its rows already issued): loads, build, then wave `runner` adds it
-  auto run_slow = [&](int j, int runner) {
-      const uint32_t smask = s_tmask[j];
+  // wave `runner` adds slow tile j (built in LDS) to its softmax state
+  auto compute_slow = [&](int j, int runner) {
       const int t0 = tile_t0(j);
-      int blk, off0, seat0;
-      tile_page(j, t0, blk, off0, seat0);
-      const int bp = t0 + bt;
-      const bool b_staged = (smask >> bt) & 1u;
-      const bool b_codes = bp < hist && !b_staged;
-      const bool b_cur = has_new && bp >= hist && bp < seq;
-      const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)(off0 + bt) * ks1;
-      const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)(off0 + bt) * vs1;
-      const int64_t cur_off = (int64_t)(qa + (b_cur ? bp - hist : 0)) * A.kv_new_stride_token + (int64_t)kvh * D;
-      uint32_t cw[NU] = {};
-      u32x4 clo[NU] = {}, chi[NU] = {};
-      u32x2 meta = {0u, 0u};
-      if (b_codes) meta = *(const u32x2*)ks;
-#pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
-        if (b_codes) cw[u] = *(const uint32_t*)((kv ? vs : ks + 32) + hg * (D / 8) + 4 * c);
-        if (b_cur) {
-          const uint16_t* src = (const uint16_t*)(kv ? A.v_new : A.k_new) + cur_off + hg * (D / 2) + 16 * c;
-          clo[u] = *(const u32x4*)src;
-          chi[u] = *(const u32x4*)(src + 8);
-        }
-      }
-      // a unit's values: staged tokens from the LDS rows (after the barrier), the
-      // others from the codes / current chunk in registers (before it, while the row
-      // loads land)
-      auto build = [&](int u, bool staged_pass) {
-        const int uid = bpart + 16 * u, kv = uid / (2 * C::NCH), hg = (uid / C::NCH) & 1, c = uid % C::NCH;
-        unsigned o[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if (staged_pass) {
-          const float* row = s_rows + (kv * (kTile / C::TPR) + bt / C::TPR) * C::SROW + (bt % C::TPR) * D +
-                             hg * (D / 2) + 16 * c;
-          f32x4 f[4];
-#pragma unroll
-          for (int x = 0; x < 4; ++x) f[x] = *(const f32x4*)(row + 4 * x);
-          if (kv == 0) {
-            // K operand pairs in the lookup's order (e, e+4) / (e+8, e+12)
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-              o[x] = hist_pair(f[0][x], f[1][x]);
-              o[4 + x] = hist_pair(f[2][x], f[3][x]);
-            }
-          } else {
-#pragma unroll
-            for (int x = 0; x < 8; ++x) o[x] = hist_pair(f[x >> 2][x & 3], f[2 + (x >> 2)][x & 3]);
-          }
-        } else if (kv == 0) {
-          if (b_cur) {
-            kpairs16(clo[u], chi[u], o);
-          } else if (b_codes) {
-            unsigned t_lo, t_hi;
-            byte_tables(meta[0], t_lo, t_hi);
-            lut16(cw[u], t_lo, t_hi, o);
-          }
-        } else {
-          // V values as (e, e+8) pairs
-          if (b_cur) {
-            interleave8(clo[u], chi[u], o);
-          } else if (b_codes) {
-            unsigned vlo, vhi;
-            value_table(meta[1], vlo, vhi);
-            table_pairs(cw[u], vlo, vhi, o);
-          }
-        }
-        if (kv == 0) {
-          u32x4* dst = s_kop + ((bt * 2 + hg) * C::NCH + c) * 2;
-          dst[0] = u32x4{o[0], o[1], o[2], o[3]};
-          dst[1] = u32x4{o[4], o[5], o[6], o[7]};
-        } else {
-          // to the V buffer, columns permuted so that MFMA row i of output block b
-          // reads column 32 b + i (d = pv_d(b, i))
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const u32x2 w = {__builtin_amdgcn_perm(o[q + 4], o[q], 0x05040100u),
-                             __builtin_amdgcn_perm(o[q + 4], o[q], 0x07060302u)};
-            *(u32x2*)&s_slowv[bt * C::VROW + vbuf_col<D>(hg, q, c)] = w;
-          }
-        }
-      };
-      if (!b_staged) {
-#pragma unroll
-        for (int u = 0; u < NU; ++u) build(u, false);
-      }
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's loads (and its row loads into LDS) are in
-      __syncthreads();
-      if (b_staged) {
-#pragma unroll
-        for (int u = 0; u < NU; ++u) build(u, true);
-      }
-      __syncthreads();
       if (wave == runner) {
         f32x16 S = {};
 #pragma unroll
@@ -656,7 +623,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
           }
         }
       }
-      __syncthreads();  // the LDS buffers are rewritten by the next tile
   };
 
   // ---------------------------------------------------------------- fast tiles
@@ -810,12 +776,17 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     z_run = 0.f;
   }
 
-  // ---- slow tiles, in value units
+  // ---- slow tiles, in value units, one at a time by the whole workgroup: build
+  // (all threads), then the next tile's loads go out while one wave computes
+  if (nslow > 0) load_slow(__builtin_amdgcn_readfirstlane(s_slow[0]));
 #pragma unroll 1
   for (int k = 0; k < nslow; ++k) {
     const int j = __builtin_amdgcn_readfirstlane(s_slow[k]);
-    issue_rows(j);
-    run_slow(j, k % kWaves);
+    build_slow(j);
+    __syncthreads();  // the tile's K operands and V values are in LDS
+    if (k + 1 < nslow) load_slow(__builtin_amdgcn_readfirstlane(s_slow[k + 1]));
+    compute_slow(j, k % kWaves);
+    __syncthreads();  // the LDS buffers are rewritten by the next tile
   }
 
   // ---- cross-wave merge: common max M and total L per row, then the wave partials
@@ -1002,9 +973,10 @@ namespace {
 // hold staged tokens (the FP32 sink / recent window) or to need the slow path for
 // another reason (current chunk, causal boundary, ragged end) move up to 64 KB of
 // FP32 rows and run one at a time through the whole workgroup, against the 8 KB of
-// code lines of a history tile that the eight waves stream concurrently.  16 is the
-// measured ratio on MI355X (8 x 24K MTP and 64 mixed-length cache-only decodes both
-// end fastest with 12-16).
+// code lines of a history tile that the eight waves stream concurrently.  16 was
+// the measured ratio on MI355X when slow tiles moved their rows by LDS DMA one tile
+// at a time (8 x 24K MTP and 64 mixed-length cache-only decodes both ended fastest
+// with 12-16); with the rows loaded one tile ahead, 6-16 all measure the same.
 constexpr int64_t kSlowCost = 16;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
