@@ -46,8 +46,9 @@ def run_store(k, v, caches, slots, d, rk, rv, **kw):
     return kc.view(torch.uint8).cpu().numpy(), vc.view(torch.uint8).cpu().numpy()
 
 
-# 1500 tokens: last writers via claim tables; 300 tokens: via the slot scan of small calls
-@pytest.mark.parametrize("n", [1500, 300])
+# 1500 tokens: last writers via claim tables; 300 tokens: via the slot scan (two
+# launches); 64 and 23 tokens: the one-launch path (column slices, last slice quantizes)
+@pytest.mark.parametrize("n", [1500, 300, 64, 23])
 @pytest.mark.parametrize("d,hk,rot", [(256, 1, "hadamard"), (256, 1, "identity"),
                                       (128, 2, "qr"), (64, 4, "hadamard")])
 def test_store_bytes_bit_exact(cuda, d, hk, rot, n):
@@ -69,6 +70,28 @@ def test_store_bytes_bit_exact(cuda, d, hk, rot, n):
               ek, ev, slots)
     assert np.array_equal(got_k, ek), f"K cache bytes differ at {np.argwhere(got_k != ek)[:5]}"
     assert np.array_equal(got_v, ev)
+
+
+@pytest.mark.parametrize("d,hk", [(256, 1), (256, 2), (128, 1)])
+def test_store_small_call_rewrites_bit_exact(cuda, d, hk):
+    """One-launch calls (<= 64 tokens) with many rewrites of one slot and skipped
+    slots: the last writer's bytes land, the others' never do; two calls in a row
+    (the arrival counters are left at zero by the first)."""
+    bs, nb, n = 128, 4, 48
+    rk, rv = cases.qr_rotation(d, 13), cases.hadamard_rotation(d, 14)
+    g = cases.rng(15)
+    k8, v8 = (g.integers(0, 256, (nb, bs, hk, d), dtype=np.uint8) for _ in range(2))
+    ek, ev = k8.copy(), v8.copy()
+    for call in range(2):
+        k = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 20 + call)
+        v = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 30 + call)
+        slots = slot_mapping(n, nb * bs, 16 + call, neg=0.1, dup=0.3)
+        slots[[5, 17, 40]] = slots[3]  # one slot written four times
+        got_k, got_v = run_store(k, v, (k8, v8), slots, d, rk, rv)
+        store_ref(rotate(k, rk), rotate(v, rv), ek, ev, slots)
+        assert np.array_equal(got_k, ek), f"call {call}: K bytes differ at {np.argwhere(got_k != ek)[:5]}"
+        assert np.array_equal(got_v, ev), f"call {call}: V bytes differ"
+        k8, v8 = got_k, got_v
 
 
 def test_store_prerotated_reference_sgemm_bits(cuda):
@@ -107,7 +130,8 @@ def test_store_clip_bit_exact(cuda):
 # the last request of each case is empty; with 100 blocks over 64 staging rows,
 # blocks b and b + 64 share seats (collisions resolved by the last writer)
 @pytest.mark.parametrize("qsl,seqs,nb", [([0, 700, 705, 1200, 1200], [700, 2000, 496, 10], 32),
-                                         ([0, 300, 305, 600, 600], [300, 2000, 496, 10], 100)])
+                                         ([0, 300, 305, 600, 600], [300, 2000, 496, 10], 100),
+                                         ([0, 4, 8, 9, 9], [700, 2000, 496, 10], 100)])  # one launch
 def test_store_window_tags_values_and_rotated_outputs(cuda, qsl, seqs, nb):
     """Forward write: codes + owner tags + FP32 window + rotated q/k/v for the read."""
     from oscar_amd import ops
