@@ -114,8 +114,9 @@ typedef struct oscar_store_args_v1 {
   int64_t* slot_claims;         /* [num_blocks * block_size] */
   int64_t* seat_claims;         /* [rows * block_size] (stage mode 2) */
   int64_t* epoch_counter;       /* device int64[2], zero-initialised once, shared per device */
-  /* fp32 rotated K/V staging between the two launches, 16-byte aligned,
-   * >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
+  /* fp32 rotated K/V between rotation and quantization (between the two launches of
+   * a large call, between the column-slice workgroups of a call of <= 64 tokens),
+   * 16-byte aligned, >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
   void* workspace;
   int64_t workspace_bytes;
   /* calls of <= 64 tokens: one arrival counter per K / V vector, uint32

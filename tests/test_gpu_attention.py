@@ -73,6 +73,9 @@ DECODE_CASES = [
     # the planner's window hint is only a hint: none, and one far wider than the
     # staged window (window items that hold plain history tiles)
     ("hint_off", [1025, 2048, 5000], [4, 4, 1], {"hint": (0, 0), "target": 24}),
+    # pages of 32 and 64 tokens: every tile is a whole page, or half of one
+    ("pages_32", [1000, 77], [4, 1], {"bs": 32, "target": 16}),
+    ("pages_64", [3000, 129], [4, 2], {"bs": 64}),
     ("hint_wide", [3000, 5000], [4, 1], {"hint": (512, 2048), "target": 24}),
 ]
 
@@ -82,7 +85,7 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     d = opts.get("d", 256)
     hk = opts.get("hk", 1)
     group = opts.get("group", 6)
-    c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group,
+    c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group, bs=opts.get("bs", 128),
                         fresh=opts.get("fresh", True), window=opts.get("window", True),
                         key_ramp=opts.get("key_ramp", 0.0))
     out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256), opts.get("hint"))
