@@ -279,7 +279,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const uint8_t* vbase = A.cache.v + (int64_t)kvh * A.cache.v_stride[2];
   const int64_t ks0 = A.cache.k_stride[0], ks1 = A.cache.k_stride[1];
   const int64_t vs0 = A.cache.v_stride[0], vs1 = A.cache.v_stride[1];
-  const int64_t* owner = P.st.owner;
 
   // ---- prologue.  Three rounds of global loads, issued so that no wait queues
   // behind a later round: (1) lane i < my of each wave loads the page of the wave's
