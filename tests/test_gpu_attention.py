@@ -76,6 +76,10 @@ DECODE_CASES = [
     # pages of 32 and 64 tokens: every tile is a whole page, or half of one
     ("pages_32", [1000, 77], [4, 1], {"bs": 32, "target": 16}),
     ("pages_64", [3000, 129], [4, 2], {"bs": 64}),
+    # other profiles: 1536-token pages; the legacy bf16-width cache (512-byte slots)
+    # with two KV heads
+    ("pages_1536", [5000, 300], [4, 2], {"bs": 1536}),
+    ("legacy_hk2", [700, 2000], [4, 1], {"legacy": True, "hk": 2, "group": 3}),
     ("hint_wide", [3000, 5000], [4, 1], {"hint": (512, 2048), "target": 24}),
 ]
 
@@ -87,7 +91,7 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     group = opts.get("group", 6)
     c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group, bs=opts.get("bs", 128),
                         fresh=opts.get("fresh", True), window=opts.get("window", True),
-                        key_ramp=opts.get("key_ramp", 0.0))
+                        key_ramp=opts.get("key_ramp", 0.0), legacy=opts.get("legacy", False))
     out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256), opts.get("hint"))
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
