@@ -179,7 +179,7 @@ int oscar_attn_plan_v1(const int32_t* query_start_loc, const int32_t* seq_lens, 
                        int32_t max_groups, oscar_plan_v1* plan);
 
 typedef struct oscar_attn_args_v1 {
-  const void* q;                /* [n, Hq, D] rotated queries, OSCAR_BF16 */
+  const void* q;                /* [n, Hq, D] rotated queries in q_dtype */
   int64_t num_tokens;
   int64_t num_q_heads;
   int64_t q_stride_token;       /* elements */
@@ -203,6 +203,8 @@ typedef struct oscar_attn_args_v1 {
   float* lse;                   /* [n, Hq] natural-log LSE (required) */
   int32_t phases;               /* 0 = split-K pass then merge; 1 = split-K pass only;
                                    2 = merge only (the workspace holds the pass) */
+  int32_t q_dtype;              /* OSCAR_BF16 or OSCAR_F16: q, k_new, v_new; history values
+                                   are rounded q_dtype(fp16(x)) as the reference does */
 } oscar_attn_args_v1;
 
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);

@@ -64,7 +64,7 @@ class AttnArgs(C.Structure):
         ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
         ("staging", C.POINTER(Staging)), ("scale", f32),
         ("items", vp), ("num_items", i32), ("groups", vp), ("num_groups", i32),
-        ("workspace", vp), ("out_rot", vp), ("lse", vp), ("phases", i32),
+        ("workspace", vp), ("out_rot", vp), ("lse", vp), ("phases", i32), ("q_dtype", i32),
     ]
 
 

@@ -110,17 +110,45 @@ __device__ __forceinline__ float swap_halves(float x) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-// reference history rounding, fp16 then bf16 (streaming_attention.py:124), of a
-// pair (a -> low half, b -> high half) with the packed RNE conversions
-// v_cvt_pk_f16_f32 / v_cvt_f32_f16 / v_cvt_pk_bf16_f32
+// Query dtype QT (OSCAR_BF16 or OSCAR_F16): the dtype of the QK operands, of the
+// slow tiles' V values and of P in their PV.
+//
+// reference history rounding q_dtype(fp16(x)) (streaming_attention.py:124) of a pair
+// (a -> low half, b -> high half) with the packed RNE conversions v_cvt_pk_f16_f32
+// (/ v_cvt_f32_f16 / v_cvt_pk_bf16_f32 for bf16 queries)
+template <int QT>
 __device__ __forceinline__ unsigned hist_pair(float a, float b) {
   const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
-  const f32x2 w = __builtin_convertvector(h, f32x2);
-  return __builtin_bit_cast(unsigned, __builtin_convertvector(w, bf16x2));
+  if constexpr (QT == OSCAR_F16) {
+    return __builtin_bit_cast(unsigned, h);
+  } else {
+    const f32x2 w = __builtin_convertvector(h, f32x2);
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(w, bf16x2));
+  }
 }
-// bf16 pair (RNE) of two floats
-__device__ __forceinline__ unsigned bf16_pair(float a, float b) {
-  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, bf16x2));
+// pair (RNE) of two floats in the query dtype, and the value of its half k
+template <int QT>
+__device__ __forceinline__ unsigned q_pair(float a, float b) {
+  if constexpr (QT == OSCAR_F16) return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <int QT>
+__device__ __forceinline__ float q_half(unsigned pair, int k) {
+  const unsigned bits = k ? pair >> 16 : pair & 0xffffu;
+  if constexpr (QT == OSCAR_F16) return f16_bits_to_f32(bits);
+  else return __uint_as_float(bits << 16);
+}
+// 8 query-dtype elements (one MFMA operand per lane)
+template <int QT> struct QVec { typedef bf16x8 type; };
+template <> struct QVec<OSCAR_F16> { typedef f16x8 type; };
+// C += A B (32x32x16 MFMA) with operands in the query dtype, given as packed words
+template <int QT>
+__device__ __forceinline__ f32x16 mma16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (QT == OSCAR_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
 }
 
 // PV output block mb, MFMA row m -> d, and the code position of the block
@@ -152,14 +180,15 @@ __device__ __forceinline__ void interleave8(const u32x4& lo, const u32x4& hi, un
   }
 }
 
-// history value table of one token, bf16(fp16(c*scale + zero)) for c = 0..3
+// history value table of one token, q_dtype(fp16(c*scale + zero)) for c = 0..3
+template <int QT>
 __device__ __forceinline__ void value_table(unsigned scale_zero, unsigned& lo, unsigned& hi) {
   const float s = f16_bits_to_f32(scale_zero & 0xffff), z = f16_bits_to_f32(scale_zero >> 16);
   float v[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(__fmul_rn((float)c, s), z);  // mul, then add
-  lo = hist_pair(v[0], v[1]);
-  hi = hist_pair(v[2], v[3]);
+  lo = hist_pair<QT>(v[0], v[1]);
+  hi = hist_pair<QT>(v[2], v[3]);
 }
 
 // bf16 pairs (element k, element k+8) of the 16 codes of one code dword
@@ -184,11 +213,12 @@ __device__ __forceinline__ void kpairs16(const u32x4& lo, const u32x4& hi, unsig
   o[7] = __builtin_amdgcn_perm(hi[3], hi[1], 0x07060302u);
 }
 
-// the four history values of a token as byte tables: t_lo = low bytes of the bf16
+// the four history values of a token as byte tables: t_lo = low bytes of the 16-bit
 // values for codes 0..3, t_hi = their high bytes
+template <int QT>
 __device__ __forceinline__ void byte_tables(unsigned scale_zero, unsigned& t_lo, unsigned& t_hi) {
   unsigned lo, hi;
-  value_table(scale_zero, lo, hi);
+  value_table<QT>(scale_zero, lo, hi);
   t_lo = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
   t_hi = __builtin_amdgcn_perm(hi, lo, 0x07050301u);
 }
@@ -216,9 +246,10 @@ struct TileRegs {
   int blk;              // physical block of the tile (0 off the history)
 };
 
-template <int D>
+template <int D, int QT>
 __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   using C = Cfg<D>;
+  using QV = typename QVec<QT>::type;  // one MFMA operand in the query dtype
   const oscar_attn_args_v1& A = P.a;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -389,9 +420,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const float c_score = A.scale * kLog2e;  // scores in log2 units
   __syncthreads();
   // Q^T operands are read from LDS at each use (volatile: kept out of registers)
-  auto qop = [&](int j) {
-    return __builtin_bit_cast(bf16x8, *(const volatile u32x4*)&s_q[j][lane]);
-  };
+  auto qop = [&](int j) { return __builtin_bit_cast(QV, *(const volatile u32x4*)&s_q[j][lane]); };
 
   // ---- running state (per lane row n): reference max m_run (log2 units), sum l, z
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f;
@@ -525,19 +554,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
           // K operand pairs in the lookup's order (e, e+4) / (e+8, e+12)
 #pragma unroll
           for (int x = 0; x < 4; ++x) {
-            o[x] = hist_pair(f[0][x], f[1][x]);
-            o[4 + x] = hist_pair(f[2][x], f[3][x]);
+            o[x] = hist_pair<QT>(f[0][x], f[1][x]);
+            o[4 + x] = hist_pair<QT>(f[2][x], f[3][x]);
           }
         } else {
 #pragma unroll
-          for (int x = 0; x < 8; ++x) o[x] = hist_pair(f[x >> 2][x & 3], f[2 + (x >> 2)][x & 3]);
+          for (int x = 0; x < 8; ++x) o[x] = hist_pair<QT>(f[x >> 2][x & 3], f[2 + (x >> 2)][x & 3]);
         }
       } else if (kv == 0) {
         if (b_cur) {
           kpairs16(__builtin_bit_cast(u32x4, sx[u][0]), __builtin_bit_cast(u32x4, sx[u][1]), o);
         } else if (b_codes) {
           unsigned t_lo, t_hi;
-          byte_tables(smeta[0], t_lo, t_hi);
+          byte_tables<QT>(smeta[0], t_lo, t_hi);
           lut16(__float_as_uint(sx[u][0][0]), t_lo, t_hi, o);
         }
       } else {
@@ -546,7 +575,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
           interleave8(__builtin_bit_cast(u32x4, sx[u][0]), __builtin_bit_cast(u32x4, sx[u][1]), o);
         } else if (b_codes) {
           unsigned vlo, vhi;
-          value_table(smeta[1], vlo, vhi);
+          value_table<QT>(smeta[1], vlo, vhi);
           table_pairs(__float_as_uint(sx[u][0][0]), vlo, vhi, o);
         }
       }
@@ -574,8 +603,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 #pragma unroll
         for (int c = 0; c < C::NCH; ++c) {
           const u32x4* src = s_kop + ((m * 2 + g) * C::NCH + c) * 2;
-          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, src[0]), qop(2 * c), S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, src[1]), qop(2 * c + 1), S, 0, 0, 0);
+          if constexpr (QT == OSCAR_F16) {
+            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(QV, src[0]), qop(2 * c), S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(QV, src[1]), qop(2 * c + 1), S, 0, 0, 0);
+          } else {
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(QV, src[0]), qop(2 * c), S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(QV, src[1]), qop(2 * c + 1), S, 0, 0, 0);
+          }
         }
         // masked scores
         float xs[16];
@@ -590,7 +624,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
         }
         mx = fmaxf(mx, swap_halves(mx));
         update_max(mx);
-        // P = hi + lo, both bf16
+        // P = hi + lo, both in the query dtype
         u32x4 ph[2], pl[2];
         float lsum = 0.f;
 #pragma unroll
@@ -598,9 +632,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
           const float p0 = (xs[r] == -INFINITY) ? 0.f : exp2f(xs[r] - m_run);
           const float p1 = (xs[r + 1] == -INFINITY) ? 0.f : exp2f(xs[r + 1] - m_run);
           lsum += p0 + p1;
-          const unsigned hb = bf16_pair(p0, p1);
+          const unsigned hb = q_pair<QT>(p0, p1);
           ph[r >> 3][(r & 7) >> 1] = hb;
-          pl[r >> 3][(r & 7) >> 1] = bf16_pair(p0 - __uint_as_float(hb << 16), p1 - __uint_as_float(hb & 0xffff0000u));
+          pl[r >> 3][(r & 7) >> 1] = q_pair<QT>(p0 - q_half<QT>(hb, 0), p1 - q_half<QT>(hb, 1));
         }
         l_run += lsum;
         const int G16 = lane >> 4, i16 = lane & 15;
@@ -608,17 +642,18 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
         for (int b = 0; b < C::MBLK; ++b) {
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
-            bf16x8 va;
+            u32x4 va;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
               const int key = 16 * s + 4 * (G16 >> 1) + 8 * h + (i16 >> 2);
               const uint16_t* addr = &s_slowv[key * C::VROW + 32 * b + 16 * (G16 & 1) + 4 * (i16 & 3)];
-              auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
-#pragma unroll
-              for (int e = 0; e < 4; ++e) va[4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
+              const u32x2 t = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr)));
+              va[2 * h] = t[0];
+              va[2 * h + 1] = t[1];
             }
-            O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, ph[s]), O[b], 0, 0, 0);
-            O[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, __builtin_bit_cast(bf16x8, pl[s]), O[b], 0, 0, 0);
+            O[b] = mma16<QT>(va, ph[s], O[b]);
+            O[b] = mma16<QT>(va, pl[s], O[b]);
           }
         }
       }
@@ -634,17 +669,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
     s_cst[wave][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
     unsigned t_lo, t_hi;
-    byte_tables(r.meta[0], t_lo, t_hi);
+    byte_tables<QT>(r.meta[0], t_lo, t_hi);
 #pragma unroll
     for (int r2 = 0; r2 < 16; ++r2) S[r2] = 0.f;
 #pragma unroll
     for (int i = 0; i < C::NCH; ++i) {
       unsigned o[8];
       lut16(r.k[i >> 2][i & 3], t_lo, t_hi, o);
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]}),
-                                                  qop(2 * i), S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]}),
-                                                  qop(2 * i + 1), S, 0, 0, 0);
+      if constexpr (QT == OSCAR_F16) {
+        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(QV, u32x4{o[0], o[1], o[2], o[3]}), qop(2 * i), S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(QV, u32x4{o[4], o[5], o[6], o[7]}), qop(2 * i + 1), S, 0, 0, 0);
+      } else {
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(QV, u32x4{o[0], o[1], o[2], o[3]}), qop(2 * i), S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(QV, u32x4{o[4], o[5], o[6], o[7]}), qop(2 * i + 1), S, 0, 0,
+                                                    0);
+      }
     }
   };
 
@@ -945,7 +984,10 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
 template <int D>
 int launch_decode(const AttnParams& p, hipStream_t s) {
   if (p.a.phases != 2) {
-    hipLaunchKernelGGL(attn_main_kernel<D>, dim3(p.a.num_items), dim3(kThreads), 0, s, p);
+    if (p.a.q_dtype == OSCAR_F16)
+      hipLaunchKernelGGL((attn_main_kernel<D, OSCAR_F16>), dim3(p.a.num_items), dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((attn_main_kernel<D, OSCAR_BF16>), dim3(p.a.num_items), dim3(kThreads), 0, s, p);
     OSCAR_CHECK_LAUNCH("attn_main_kernel");
   }
   if (p.a.phases != 1) {
@@ -1182,6 +1224,8 @@ extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream
   if ((a.k_new == nullptr) != (a.v_new == nullptr))
     return fail(-22, "oscar_attn_decode_v1: both new K and V must be supplied together");
   if (a.phases < 0 || a.phases > 2) return fail(-22, "oscar_attn_decode_v1: phases must be 0, 1 or 2");
+  if (a.q_dtype != OSCAR_BF16 && a.q_dtype != OSCAR_F16)
+    return fail(-22, "oscar_attn_decode_v1: q_dtype must be OSCAR_BF16 or OSCAR_F16");
   if (a.cache.num_kv_heads < 1 || a.num_q_heads % a.cache.num_kv_heads)
     return fail(-22, "oscar_attn_decode_v1: Hq must be a multiple of Hk");
   if ((a.cache.k_stride[2] & 15) || (a.cache.v_stride[2] & 15) || (a.cache.k_stride[1] & 15) ||

@@ -277,10 +277,12 @@ def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None
 
 def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: DecodePlan, scale,
                      stage=None, *, head_dim, out_rot=None, lse=None, phases=0):
-    """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32)."""
+    """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32).
+
+    q (and k_new / v_new) are bf16 or fp16; history values are rounded q_dtype(fp16(x))."""
     _require_cuda(q, k_cache, v_cache, block_table)
-    if q.dtype != torch.bfloat16:
-        raise ValueError("OSCAR HIP attention requires bf16 queries")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("OSCAR HIP attention requires bf16 or fp16 queries")
     n, hq, _ = q.shape
     dev = q.device
     if out_rot is None:
@@ -321,6 +323,7 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     a.workspace = ws.data_ptr()
     a.out_rot, a.lse = out_rot.data_ptr(), lse.data_ptr()
     a.phases = int(phases)
+    a.q_dtype = _DTYPES[q.dtype]
     lib = _lib.load()
     _lib.check(lib.oscar_attn_decode_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_attn_decode_v1")
     return out_rot, lse

@@ -24,9 +24,9 @@ def dev(x, dtype=torch.bfloat16):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
 
 
-def run_decode(c, d=256, hk=1, group=6, target=256, hint=None):
+def run_decode(c, d=256, hk=1, group=6, target=256, hint=None, qdt=torch.bfloat16):
     """hint: the planner's window hint; default the window make_case stages (sink 128,
-    recent 256) when the case has one."""
+    recent 256) when the case has one.  qdt: the query (and current K/V) dtype."""
     from oscar_amd import ops
 
     kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
@@ -37,8 +37,8 @@ def run_decode(c, d=256, hk=1, group=6, target=256, hint=None):
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=c["k"] is not None, num_kv_heads=hk,
                            group=group, head_dim=d, device=torch.device("cuda"), target_items=target,
                            window=hint)
-    out, lse = ops.attention_decode(dev(c["q"]), None if c["k"] is None else dev(c["k"]),
-                                    None if c["v"] is None else dev(c["v"]),
+    out, lse = ops.attention_decode(dev(c["q"], qdt), None if c["k"] is None else dev(c["k"], qdt),
+                                    None if c["v"] is None else dev(c["v"], qdt),
                                     kc, vc, torch.from_numpy(c["bt"]).cuda(), plan, c["scale"],
                                     stage, head_dim=d)
     torch.cuda.synchronize()
@@ -96,6 +96,24 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
     check(out, lse, ref_out, ref_lse, name)
+
+
+@pytest.mark.parametrize("name,prefixes,lengths,opts", [
+    ("mtp_mixed_window", [129, 1025, 3, 300], [4, 3, 1, 2], {}),
+    ("cache_only", [0, 257, 3, 263], [1, 1, 4, 5], {"fresh": False}),
+    ("d128_hk2", [129, 700], [4, 2], {"d": 128, "hk": 2, "group": 4}),
+    ("long_items", [9000, 2100], [4, 1], {"target": 6}),
+], ids=lambda v: v if isinstance(v, str) else None)
+def test_decode_fp16_queries_match_oracle(cuda, name, prefixes, lengths, opts):
+    """fp16 queries (probe_streaming.py:100-107 profiles): history values rounded
+    fp16(x), fp16 MFMA operands; the oracle evaluates the reference math with q_dtype
+    fp16.  The case values sit on the bf16 grid, which fp16 holds exactly."""
+    d, hk, group = opts.get("d", 256), opts.get("hk", 1), opts.get("group", 6)
+    c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group, fresh=opts.get("fresh", True))
+    out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256), qdt=torch.float16)
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"], d=d, q_dtype="f16")
+    check(out, lse, ref_out, ref_lse, f"fp16 {name}")
 
 
 def test_decode_plan_covers_each_history_token_once(cuda):
