@@ -210,9 +210,9 @@ typedef struct oscar_attn_args_v1 {
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
 
 typedef struct oscar_prefill_args_v1 {
-  const void* q;                /* [n, Hq, D] bf16 */
+  const void* q;                /* [n, Hq, D] in q_dtype */
   int64_t q_stride_token;
-  const void* k;                /* [n, Hk, D] bf16 current chunk */
+  const void* k;                /* [n, Hk, D] current chunk in q_dtype */
   const void* v;
   int64_t kv_stride_token;
   int64_t num_tokens;
@@ -224,13 +224,15 @@ typedef struct oscar_prefill_args_v1 {
   const int32_t* block_table_row; /* [max_blocks] of this request */
   const oscar_staging_v1* staging;
   float scale;
-  void* out;                    /* [n, Hq, D]: bf16 when history == 0, else fp32 rotated */
+  void* out;                    /* [n, Hq, D]: q_dtype when history == 0, else fp32 rotated */
   int64_t out_stride_token;
   float* lse;                   /* [n, Hq] or NULL */
-  /* history > 0: 16-byte aligned scratch for the history's bf16 K/V values,
+  /* history > 0: 16-byte aligned scratch for the history's K/V values in q_dtype,
    * >= oscar_prefill_workspace_bytes_v1(history, num_kv_heads, head_dim) */
   void* workspace;
   int64_t workspace_bytes;
+  int32_t q_dtype;              /* OSCAR_BF16 or OSCAR_F16: q, k, v (history values are
+                                   rounded q_dtype(fp16(x)) as the reference does) */
 } oscar_prefill_args_v1;
 
 int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim);

@@ -75,6 +75,7 @@ class PrefillArgs(C.Structure):
         ("history", i64), ("cache", Cache), ("block_table_row", vp),
         ("staging", C.POINTER(Staging)), ("scale", f32), ("out", vp),
         ("out_stride_token", i64), ("lse", vp), ("workspace", vp), ("workspace_bytes", i64),
+        ("q_dtype", i32),
     ]
 
 

@@ -265,8 +265,8 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         requests attend in the rotated domain, then out_rot @ R_v^T."""
         if (key is None) != (value is None):
             raise ValueError("Both new K and V must be supplied together")
-        if query.dtype != torch.bfloat16:
-            raise ValueError("OSCAR MI355X attention requires bf16 queries; "
+        if query.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("OSCAR MI355X attention requires bf16 or fp16 queries; "
                              f"got dtype={query.dtype}")
         D, hq, hk = self.head_size, self.num_heads, self.num_kv_heads
         group = hq // hk

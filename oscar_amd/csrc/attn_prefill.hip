@@ -38,12 +38,24 @@ constexpr float kLazy = 8.f;  // max drift (log2 units) before O is rescaled
 constexpr int kQK = 4;        // QK K-steps whose LDS operands are read together
 typedef short __attribute__((ext_vector_type(4))) i16x4;
 typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
+typedef _Float16 __attribute__((ext_vector_type(2))) f16x2;
 typedef float __attribute__((ext_vector_type(2))) f32x2;
 
-__device__ __forceinline__ float round_hist_bf16(float x) {
-  float h = __half2float(__float2half_rn(x));
-  return bf16_bits_to_f32(f32_to_bf16_bits(h));
+// the reference history value q_dtype(fp16(x)) (prepare_kv.py:77) as 16-bit bits
+template <int QT>
+__device__ __forceinline__ unsigned hist_bits(float x) {
+  const __half h = __float2half_rn(x);
+  if constexpr (QT == OSCAR_F16) return __half_as_ushort(h);
+  else return f32_to_bf16_bits(__half2float(h));
 }
+// 16-bit bits of x in the query dtype (RNE)
+template <int QT>
+__device__ __forceinline__ unsigned q_bits(float x) {
+  if constexpr (QT == OSCAR_F16) return f32_to_f16_bits(x);
+  else return f32_to_bf16_bits(x);
+}
+template <int QT> struct QVec { typedef bf16x8 type; typedef bf16x2 pair; typedef __bf16 elem; };
+template <> struct QVec<OSCAR_F16> { typedef f16x8 type; typedef f16x2 pair; typedef _Float16 elem; };
 
 struct PrefillParams {
   oscar_prefill_args_v1 a;
@@ -56,7 +68,7 @@ struct PrefillParams {
 };
 
 // one wave per (history token, kv head): lane l holds elements E*l .. E*l+E-1
-template <int D>
+template <int D, int QT>
 __global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
   constexpr int E = D / 64;
   const oscar_prefill_args_v1& A = P.a;
@@ -99,10 +111,8 @@ __global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
   unsigned kw[E / 2], vw[E / 2];
 #pragma unroll
   for (int i = 0; i < E / 2; ++i) {
-    kw[i] = (unsigned)f32_to_bf16_bits(round_hist_bf16(kv[2 * i])) |
-            ((unsigned)f32_to_bf16_bits(round_hist_bf16(kv[2 * i + 1])) << 16);
-    vw[i] = (unsigned)f32_to_bf16_bits(round_hist_bf16(vv[2 * i])) |
-            ((unsigned)f32_to_bf16_bits(round_hist_bf16(vv[2 * i + 1])) << 16);
+    kw[i] = hist_bits<QT>(kv[2 * i]) | (hist_bits<QT>(kv[2 * i + 1]) << 16);
+    vw[i] = hist_bits<QT>(vv[2 * i]) | (hist_bits<QT>(vv[2 * i + 1]) << 16);
   }
   uint16_t* dk = P.hist_k + vec * D + E * lane;
   uint16_t* dv = P.hist_v + vec * D + E * lane;
@@ -115,8 +125,11 @@ __global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
   }
 }
 
-template <int D>
+template <int D, int QT>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
+  using QV = typename QVec<QT>::type;    // one MFMA operand in the query dtype
+  using QP = typename QVec<QT>::pair;
+  using QE = typename QVec<QT>::elem;
   const oscar_prefill_args_v1& A = P.a;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = lane & 31, g = lane >> 5;
@@ -212,14 +225,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       f32x16 S = {};
 #pragma unroll
       for (int j0 = 0; j0 < D / 16; j0 += kQK) {
-        bf16x8 ka[kQK], qa[kQK];
+        QV ka[kQK], qa[kQK];
 #pragma unroll
         for (int j = 0; j < kQK; ++j) {
-          ka[j] = *(const bf16x8*)&s_k[buf][m][16 * (j0 + j) + 8 * g];
-          qa[j] = __builtin_bit_cast(bf16x8, s_q[wave][j0 + j][lane]);
+          ka[j] = *(const QV*)&s_k[buf][m][16 * (j0 + j) + 8 * g];
+          qa[j] = __builtin_bit_cast(QV, s_q[wave][j0 + j][lane]);
         }
 #pragma unroll
-        for (int j = 0; j < kQK; ++j) S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], S, 0, 0, 0);
+        for (int j = 0; j < kQK; ++j) {
+          if constexpr (QT == OSCAR_F16) S = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[j], qa[j], S, 0, 0, 0);
+          else S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], S, 0, 0, 0);
+        }
         // keep the group's LDS reads ahead of its MFMAs (one latency per group)
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQK, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, kQK, 0);
@@ -250,17 +266,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       }
       // p = 2^(S c - m) (exp2 of -inf is 0); rows with no key yet keep m = -inf and p = 0
       const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
-      // P = hi + lo, both bf16 (the pair carries ~16 bits of p)
-      bf16x8 pb[2], pl[2];
+      // P = hi + lo, both in the query dtype (the pair carries ~16 bits of p or more)
+      QV pb[2], pl[2];
       float lsum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(S[r], c, nm));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(S[r + 1], c, nm));
         lsum += p0 + p1;
-        const bf16x2 h = __builtin_convertvector(f32x2{p0, p1}, bf16x2);
+        const QP h = __builtin_convertvector(f32x2{p0, p1}, QP);
         const f32x2 hf = __builtin_convertvector(h, f32x2);
-        const bf16x2 lo = __builtin_convertvector(f32x2{p0 - hf[0], p1 - hf[1]}, bf16x2);
+        const QP lo = __builtin_convertvector(f32x2{p0 - hf[0], p1 - hf[1]}, QP);
         pb[r >> 3][r & 7] = h[0];
         pb[r >> 3][(r & 7) + 1] = h[1];
         pl[r >> 3][r & 7] = lo[0];
@@ -272,7 +288,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       const int G16 = lane >> 4, i16 = lane & 15;
 #pragma unroll
       for (int b0 = 0; b0 < D / 32; b0 += 2) {
-        bf16x8 va[2][2];
+        QV va[2][2];
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
@@ -283,14 +299,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
               const uint16_t* addr = &s_v[buf][key][32 * (b0 + bb) + 16 * (G16 & 1) + 4 * (i16 & 3)];
               auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
 #pragma unroll
-              for (int e = 0; e < 4; ++e) va[bb][s][4 * h + e] = __builtin_bit_cast(__bf16, (unsigned short)t[e]);
+              for (int e = 0; e < 4; ++e) va[bb][s][4 * h + e] = __builtin_bit_cast(QE, (unsigned short)t[e]);
             }
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
-            O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
-            O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
+            if constexpr (QT == OSCAR_F16) {
+              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
+              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
+            } else {
+              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
+              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
+            }
           }
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
         __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
@@ -329,7 +350,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
     for (int r = 0; r < 16; ++r) {
       const int d = 32 * b + 8 * (r >> 2) + 4 * g + (r & 3);
       const float v = O[b][r] * inv;
-      if (hist == 0) ((uint16_t*)A.out)[obase + d] = f32_to_bf16_bits(v);
+      if (hist == 0) ((uint16_t*)A.out)[obase + d] = (uint16_t)q_bits<QT>(v);
       else ((float*)A.out)[obase + d] = v;
     }
   if (A.lse != nullptr && g == 0)
@@ -356,6 +377,8 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
   if (!a.q || !a.k || !a.v || !a.out || a.num_tokens < 0 || a.num_kv_heads < 1 ||
       a.num_q_heads % a.num_kv_heads)
     return fail(-22, "oscar_attn_prefill_v1: invalid arguments");
+  if (a.q_dtype != OSCAR_BF16 && a.q_dtype != OSCAR_F16)
+    return fail(-22, "oscar_attn_prefill_v1: q_dtype must be OSCAR_BF16 or OSCAR_F16");
   const int G = (int)(a.num_q_heads / a.num_kv_heads);
   if (G > kRows) return fail(-22, "oscar_attn_prefill_v1: more than %d query heads per KV head", kRows);
   if (a.history < 0) return fail(-22, "oscar_attn_prefill_v1: negative history");
@@ -386,14 +409,24 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
   hipStream_t s = (hipStream_t)stream;
   if (a.history > 0) {
     const unsigned hb = (unsigned)((a.history * a.num_kv_heads + 3) / 4);
-    if (D == 256) hipLaunchKernelGGL(history_bf16_kernel<256>, dim3(hb), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(history_bf16_kernel<128>, dim3(hb), dim3(256), 0, s, p);
+    if (a.q_dtype == OSCAR_F16) {
+      if (D == 256) hipLaunchKernelGGL((history_bf16_kernel<256, OSCAR_F16>), dim3(hb), dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((history_bf16_kernel<128, OSCAR_F16>), dim3(hb), dim3(256), 0, s, p);
+    } else {
+      if (D == 256) hipLaunchKernelGGL((history_bf16_kernel<256, OSCAR_BF16>), dim3(hb), dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((history_bf16_kernel<128, OSCAR_BF16>), dim3(hb), dim3(256), 0, s, p);
+    }
     OSCAR_CHECK_LAUNCH("history_bf16_kernel");
   }
   const int ntq = (int)((a.num_tokens + p.qtok - 1) / p.qtok);
   dim3 grid(ntq, (unsigned)a.num_kv_heads);
-  if (D == 256) hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(kThreads), 0, s, p);
-  else hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, s, p);
+  if (a.q_dtype == OSCAR_F16) {
+    if (D == 256) hipLaunchKernelGGL((prefill_kernel<256, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL((prefill_kernel<128, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
+  } else {
+    if (D == 256) hipLaunchKernelGGL((prefill_kernel<256, OSCAR_BF16>), grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL((prefill_kernel<128, OSCAR_BF16>), grid, dim3(kThreads), 0, s, p);
+  }
   OSCAR_CHECK_LAUNCH("prefill_kernel");
   return 0;
 }

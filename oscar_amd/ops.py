@@ -334,18 +334,19 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
                       block_table_row=None, stage=None, out=None, lse=None):
     """Causal GQA prefill of one request.
 
-    history == 0: original-domain fresh-only prefill, returns bf16 [n, Hq, D].
+    q/k/v are bf16 or fp16 (history values rounded q_dtype(fp16(x))).
+    history == 0: original-domain fresh-only prefill, returns [n, Hq, D] in q's dtype.
     history > 0: rotated continuation over the packed history, returns fp32 out_rot
     (and fills lse [n, Hq] when given).
     """
     _require_cuda(q, k, v)
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("OSCAR HIP prefill requires bf16 q/k/v")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("OSCAR HIP prefill requires bf16 or fp16 q/k/v of one dtype")
     n, hq, _ = q.shape
     hk = k.shape[1]
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if out is None:
-        out = torch.empty(n, hq, head_dim, dtype=torch.bfloat16 if history == 0 else torch.float32,
+        out = torch.empty(n, hq, head_dim, dtype=q.dtype if history == 0 else torch.float32,
                           device=q.device)
     a = _lib.PrefillArgs()
     a.q, a.q_stride_token, a.k, a.v, a.kv_stride_token = q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k.stride(0)
@@ -365,6 +366,7 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
             a.staging = C.pointer(st)
     a.scale = float(scale)
     a.out, a.out_stride_token = out.data_ptr(), out.stride(0)
+    a.q_dtype = _DTYPES[q.dtype]
     if lse is not None:
         a.lse = lse.data_ptr()
     lib = _lib.load()

@@ -170,6 +170,37 @@ def test_prefill_continuation_matches_oracle(cuda, prefix, n, ramp):
     check(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, f"continuation {prefix}+{n}")
 
 
+def test_prefill_fp16_queries(cuda):
+    """fp16 q/k/v: the fresh-only prefill returns fp16 (original domain); the
+    continuation rounds the history fp16(x) (oracle with q_dtype f16)."""
+    from oscar_amd import ops
+
+    q = cases.bf16_normal((300, 6, 256), 81)
+    k = cases.bf16_normal((300, 1, 256), 82)
+    v = cases.bf16_normal((300, 1, 256), 83)
+    out = ops.attention_prefill(dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16), 1 / 16,
+                                head_dim=256)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    err = np.abs(out.float().cpu().numpy() - causal_prefill_ref(q, k, v, 1 / 16)).max()
+    print(f"fp16 fresh prefill: max|dO|={err:.3e}", flush=True)
+    assert err <= OUT_TOL
+    prefix, n = 3000, 300
+    c = cases.make_case([prefix], [n], key_ramp=4.0)
+    kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
+    vc = torch.from_numpy(c["v8"]).view(torch.int8).cuda()
+    stage = tuple(torch.from_numpy(a).cuda() for a in c["stage"])
+    lse = torch.empty(n, 6, dtype=torch.float32, device="cuda")
+    out = ops.attention_prefill(dev(c["q"], torch.float16), dev(c["k"], torch.float16),
+                                dev(c["v"], torch.float16), c["scale"], head_dim=256, history=prefix,
+                                k_cache=kc, v_cache=vc, block_table_row=torch.from_numpy(c["bt"][0]).cuda(),
+                                stage=stage, lse=lse)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"], q_dtype="f16")
+    check(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, "fp16 continuation 3000+300")
+
+
 def test_rotate_matches_fp32_reference(cuda):
     from oscar_amd import ops
 
