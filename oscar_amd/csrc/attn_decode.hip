@@ -292,12 +292,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   __shared__ uint32_t s_tmask[kMaxItemTokens / kTile]; // staged-token mask of every item tile
   // union of the phases: V codes of each wave's current fast tile [kWaves][kTile * NB];
   // the slow tile's K operands (bf16 pairs in MFMA order) [kTile][2][NCH][8] and V
-  // values (bf16, permuted columns) [kTile][VROW]; the cross-wave merge rounds of two
-  // output blocks [kWaves][2][4][64] f32x4
+  // values (bf16, permuted columns) [kTile][VROW]; the cross-wave merge rounds of four
+  // output blocks [kWaves][4][4][64] f32x4
   constexpr int kVcodeBytes = kWaves * kTile * C::NB;
   constexpr int kKopBytes = kTile * 2 * C::NCH * 8 * 4;
   constexpr int kSlowBytes = kKopBytes + kTile * C::VROW * 2;
-  constexpr int kMergeBytes = kWaves * 2 * 4 * 64 * 16;
+  constexpr int kMergeBytes = kWaves * 4 * 4 * 64 * 16;
   constexpr int kU0 = kVcodeBytes > kSlowBytes ? kVcodeBytes : kSlowBytes;
   __shared__ __attribute__((aligned(16))) uint8_t s_u[kU0 > kMergeBytes ? kU0 : kMergeBytes];
   uint8_t (*s_vcode)[kTile * C::NB] = (uint8_t (*)[kTile * C::NB])s_u;
@@ -828,7 +828,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   }
 
   // ---- cross-wave merge: common max M and total L per row, then the wave partials
-  // are summed in LDS in MFMA register order, two output blocks per round
+  // are summed in LDS in MFMA register order, four output blocks per round
   const float l_row = l_run + swap_halves(l_run);
   __syncthreads();  // every wave is past its fast tiles (s_u is free)
   if (g == 0) { s_ml[wave][0][m] = m_run; s_ml[wave][1][m] = l_row; }
@@ -843,28 +843,33 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (mw != -INFINITY) L += s_ml[w][1][n] * exp2f(mw - M);
   }
   const float fw = (m_run == -INFINITY || !(L > 0.f)) ? 0.f : exp2f(m_run - M) / L;
-  f32x4* buf = (f32x4*)s_u;  // [kWaves][2 blocks][4][64] f32x4
+  f32x4* buf = (f32x4*)s_u;  // [kWaves][4 blocks][4][64] f32x4
   f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
   // only the item's rows move through LDS (lane l and thread t hold row l % 32 / t % 32)
   const bool my_row = (lane & 31) < nrows;
 #pragma unroll
-  for (int rb = 0; rb < C::MBLK / 2; ++rb) {
+  for (int rb = 0; rb < C::MBLK / 4; ++rb) {
     if (my_row) {
 #pragma unroll
-      for (int bb = 0; bb < 2; ++bb)
+      for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f32x16& Ob = O[2 * rb + bb];
-          buf[((wave * 2 + bb) * 4 + q) * 64 + lane] =
+          const f32x16& Ob = O[4 * rb + bb];
+          buf[((wave * 4 + bb) * 4 + q) * 64 + lane] =
               f32x4{Ob[4 * q] * fw, Ob[4 * q + 1] * fw, Ob[4 * q + 2] * fw, Ob[4 * q + 3] * fw};
         }
     }
     __syncthreads();
     if (my_row) {
-      f32x4 acc = buf[tid];
+      // f32x4 index e of the round is index 2 rb * kThreads + e of the partial
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) acc += buf[w * kThreads + tid];
-      store_through(po, rb * kThreads + tid, acc);  // f32x4 index of the partial (row = index % 32)
+      for (int h = 0; h < 2; ++h) {
+        const int e = h * kThreads + tid;
+        f32x4 acc = buf[e];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) acc += buf[w * 2 * kThreads + e];
+        store_through(po, 2 * rb * kThreads + e, acc);
+      }
     }
     __syncthreads();
   }
