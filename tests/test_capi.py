@@ -111,12 +111,20 @@ PLAN_CASES = [
 @pytest.mark.parametrize("window", [(0, 0), (128, 256), (0, 4096)])
 @pytest.mark.parametrize("qsl,seqs,has_new,hk,group", PLAN_CASES)
 def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, has_new, hk, group, window):
-    cnt, items, groups, p = plan(lib, qsl, seqs, has_new, hk, group, window=window)
+    check_plan(lib, qsl, seqs, has_new, hk, group, window, 256, 256)
+
+
+def check_plan(lib, qsl, seqs, has_new, hk, group, window, target, d):
+    """The plan's contract with the decode kernel: every key tile of every group in
+    exactly one item, partial slots a permutation, item limits, group records."""
+    cnt, items, groups, p = plan(lib, qsl, seqs, has_new, hk, group, d=d, target=target, window=window)
     assert cnt > 0
     assert sorted(items[:, 5].tolist()) == list(range(cnt))          # partial slots: a permutation
-    assert p.partial_bytes == cnt * 32 * (256 + 1) * 4
+    assert p.partial_bytes == cnt * 32 * (d + 1) * 4
     ngroups = hk * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
-    assert cnt <= max(256, ngroups)                                  # within the target
+    # within the target, unless the groups need more: an item holds at most 256 tiles
+    floor = hk * sum(max(1, -(-(-(-s // TILE)) // 256)) for a, b, s in zip(qsl, qsl[1:], seqs) if b > a)
+    assert cnt <= max(target, floor)
     for it in items:
         req, kvh, nq, first, stride, count, part, qa, seq = (it[0], it[1] & 0xFFFF, it[1] >> 16, *it[2:8])
         assert nq == qsl[req + 1] - qsl[req] and qa == qsl[req] and seq == seqs[req]
@@ -134,6 +142,32 @@ def test_plan_covers_every_tile_once_and_respects_kernel_limits(lib, qsl, seqs, 
             np.add.at(cover, item_tiles(it), 1)
         assert (cover == 1).all()
     assert len(groups) == ngroups
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_plan_random_requests_cover_every_tile_once(lib, seed):
+    """Seeded random batches: request counts, query lengths (MTP, decode, cache-only,
+    empty), history lengths from 0 to 40K, window hints, targets, Hk and head dims."""
+    rng = np.random.default_rng(9000 + seed)
+    for _ in range(25):
+        hk = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 3, 4, 6, 8]))
+        has_new = bool(rng.integers(2))
+        nreq = int(rng.integers(1, 40))
+        lens = rng.integers(0 if not has_new else 1, 32 // group + 1, nreq)
+        lens[rng.random(nreq) < 0.1] = 0                            # empty requests
+        if lens.sum() == 0:
+            lens[0] = 1
+        qsl = [0] + np.cumsum(lens).tolist()
+        hist = rng.integers(0, 40000, nreq) * (rng.random(nreq) < 0.9)
+        seqs = (hist + (lens if has_new else 0)).tolist()
+        if not has_new:
+            seqs = [max(s, 1) for s in seqs]
+        window = tuple(int(v) for v in rng.choice([0, 128, 512], 1).tolist() +
+                       rng.choice([0, 256, 2048], 1).tolist())
+        target = int(rng.choice([1, 16, 100, 256, 1024]))
+        d = int(rng.choice([128, 256]))
+        check_plan(lib, qsl, seqs, has_new, hk, group, window, target, d)
 
 
 def test_plan_without_window_deals_history_evenly(lib):
