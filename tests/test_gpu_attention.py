@@ -116,6 +116,33 @@ def test_decode_fp16_queries_match_oracle(cuda, name, prefixes, lengths, opts):
     check(out, lse, ref_out, ref_lse, f"fp16 {name}")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_random_batches_match_oracle(cuda, seed):
+    """Seeded random batches: request count, history lengths (0 to 6000), query
+    lengths, fresh or cache-only, window or none, Hk, group, head dim, page size and
+    the planner's target, each against the oracle."""
+    rng = np.random.default_rng(4100 + seed)
+    d = int(rng.choice([128, 256]))
+    hk = int(rng.choice([1, 2]))
+    group = int(rng.choice([2, 3, 4, 6]))
+    fresh = bool(rng.integers(2))
+    nreq = int(rng.integers(1, 7))
+    prefixes = rng.integers(0 if not fresh else 1, 6000, nreq).tolist()
+    lengths = rng.integers(1, 32 // group + 1, nreq).tolist()
+    bs = int(rng.choice([32, 64, 128, 256]))
+    window = bool(rng.integers(2))
+    target = int(rng.choice([8, 64, 256]))
+    label = f"seed {seed}: d={d} hk={hk} group={group} fresh={fresh} bs={bs} window={window} " \
+            f"target={target} prefixes={prefixes} lengths={lengths}"
+    print(label, flush=True)
+    c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group, bs=bs, fresh=fresh,
+                        window=window, seed=200 + seed)
+    out, lse, _ = run_decode(c, d, hk, group, target)
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"], d=d)
+    check(out, lse, ref_out, ref_lse, label)
+
+
 def test_decode_plan_covers_each_history_token_once(cuda):
     c = cases.make_case([24579] * 8, [4] * 8)
     from oscar_amd import ops
