@@ -205,33 +205,48 @@ class Setup:
         return b_main, b_main + b_out
 
 
-def time_graph(setup, steps, warmup):
-    """Whole-step time: a HIP graph of LAYERS layer steps replayed steps/LAYERS times."""
-    nl = len(setup.layers)
-    for i in range(max(warmup, nl)):
-        setup.step(i % nl)
-    torch.cuda.synchronize()
+def capture(fn_steps, stream=None):
+    """A HIP graph of fn_steps() (captured on a side stream, torch's rule for capture)."""
     graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
+    stream = stream or torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
-            for layer in range(nl):
-                setup.step(layer)
+            fn_steps()
     torch.cuda.current_stream().wait_stream(stream)
-    graph.replay()
+    return graph
+
+
+def time_graph(setup, steps, warmup):
+    """Whole-step time: exactly `steps` layer steps (cycling the layer caches) captured in
+    one HIP graph; `warmup` untimed steps (graph replays), then one timed replay of the
+    `steps` steps between synchronizations.  Returns (ms per step, steps timed, the
+    per-step ms of 5 further replays)."""
+    nl = len(setup.layers)
+    for i in range(nl):  # eager first use of every layer (lazy state, plans)
+        setup.step(i)
     torch.cuda.synchronize()
-    reps = max(1, steps // nl)
+    graph = capture(lambda: [setup.step(i % nl) for i in range(steps)])
+    for _ in range(max(1, math.ceil(warmup / steps))):
+        graph.replay()
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
-    for _ in range(reps):
-        graph.replay()
+    graph.replay()
     t1.record()
     torch.cuda.synchronize()
-    wall = t0.elapsed_time(t1)
-    return wall / (reps * nl), reps * nl
+    ms = t0.elapsed_time(t1) / steps
+    extra = []
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        e1.synchronize()
+        extra.append(e0.elapsed_time(e1) / steps)
+    return ms, steps, extra
 
 
 def time_main_kernel(setup, reps=10):
@@ -242,14 +257,7 @@ def time_main_kernel(setup, reps=10):
     for layer in range(nl):
         setup.attention(layer, phases=1)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            for layer in range(nl):
-                setup.attention(layer, phases=1)
-    torch.cuda.current_stream().wait_stream(stream)
+    graph = capture(lambda: [setup.attention(layer, phases=1) for layer in range(nl)])
     graph.replay()
     torch.cuda.synchronize()
     per = []
@@ -286,7 +294,7 @@ def config_decode(dev, name, histories, q_len, has_new, layers, steps, warmup):
     setup = Setup(dev, histories, q_len, has_new, layers)
     staged = setup.staged_counts()
     b_main, _ = setup.algorithmic_bytes(staged)
-    ms_step, nsteps = time_graph(setup, steps, warmup)
+    ms_step, nsteps, _ = time_graph(setup, steps, warmup)
     med_ms, _ = time_main_kernel(setup)
     achieved = b_main / (med_ms * 1e-3) / 1e9
     kv_tokens = sum(setup.seqs)
@@ -606,8 +614,9 @@ def main(argv=None):
     staged = setup.staged_counts()
     b_main, b_op = setup.algorithmic_bytes(staged)
     log(f"staged history tokens per request: {staged}; B_main={b_main} B_op={b_op}")
-    ms_step, steps = time_graph(setup, args.steps, args.warmup)
-    log(f"step {ms_step * 1e3:.2f} us ({steps} steps)")
+    ms_step, steps, extra = time_graph(setup, args.steps, args.warmup)
+    log(f"step {ms_step * 1e3:.2f} us ({steps} steps); 5 more replays: "
+        + " ".join(f"{x * 1e3:.2f}" for x in extra) + " us")
     med_ms, mean_ms = time_main_kernel(setup)
     log(f"attn_main median {med_ms * 1e3:.2f} us mean {mean_ms * 1e3:.2f} us")
     achieved = b_main / (med_ms * 1e-3) / 1e9

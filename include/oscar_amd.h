@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define OSCAR_ABI_VERSION 1
+#define OSCAR_ABI_VERSION 2
 
 /* element types of dense inputs/outputs */
 enum oscar_dtype { OSCAR_F32 = 0, OSCAR_F16 = 1, OSCAR_BF16 = 2 };
@@ -170,6 +170,8 @@ typedef struct oscar_plan_v1 {
   int32_t num_items;
   int32_t num_groups;           /* request x kv-head groups with queries */
   int64_t partial_bytes;        /* workspace bytes needed by oscar_attn_decode_v1 */
+  int32_t max_group_items;      /* largest item count of any group (sizes the merge) */
+  int32_t reserved;
 } oscar_plan_v1;
 
 int oscar_attn_plan_v1(const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs,
@@ -198,7 +200,9 @@ typedef struct oscar_attn_args_v1 {
   int32_t num_items;
   const int32_t* groups;
   int32_t num_groups;
-  void* workspace;              /* >= plan.partial_bytes */
+  void* workspace;              /* item partials, >= plan.partial_bytes */
+  int64_t workspace_bytes;      /* checked: >= num_items * 32 * (D + 1) * 4 */
+  int32_t max_group_items;      /* plan.max_group_items (0: num_items) */
   float* out_rot;               /* [n, Hq, D] fp32 rotated output (required) */
   float* lse;                   /* [n, Hq] natural-log LSE (required) */
   int32_t phases;               /* 0 = split-K pass then merge; 1 = split-K pass only;

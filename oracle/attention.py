@@ -42,12 +42,14 @@ def read_history(k8, v8, bt_row, start: int, end: int, hk: int, d: int, stage, q
 
 
 def attention_ref(q, k_new, v_new, k8, v8, bt, qsl, seqs, scale, stage=None, *,
-                  d=None, q_dtype="bf16"):
+                  d=None, q_dtype="bf16", rows=None):
     """streaming_attention.py:134-196 (exact softmax, float64 evaluation).
 
     q: [n, Hq, D] (values on the q_dtype grid), k_new/v_new: [n, Hk, D] or None.
     Query i of a request with ``n_q`` queries and length ``seq`` sees keys
     ``[0, seq - n_q + i + 1)``; rows that see nothing get out 0 and LSE -inf.
+    ``rows`` (optional): the query token indices to evaluate; the others are left
+    at out 0 / LSE -inf (a sampled check of long chunks).
     Returns (out_rot [n, Hq, D] f32, lse [n, Hq] f32).
     """
     q = np.asarray(q, np.float32)
@@ -57,8 +59,11 @@ def attention_ref(q, k_new, v_new, k8, v8, bt, qsl, seqs, scale, stage=None, *,
     group = hq // hk
     out = np.zeros((n, hq, d), np.float32)
     lse = np.full((n, hq), -np.inf, np.float32)
+    wanted = None if rows is None else set(int(t) for t in rows)
     for r, (a, b, seq) in enumerate(zip(qsl[:-1], qsl[1:], seqs)):
         if b <= a:
+            continue
+        if wanted is not None and not any(a <= t < b for t in wanted):
             continue
         n_q = b - a
         prefix = seq - n_q if k_new is not None else seq
@@ -71,7 +76,7 @@ def attention_ref(q, k_new, v_new, k8, v8, bt, qsl, seqs, scale, stage=None, *,
         keys64, vals64 = keys.astype(np.float64), vals.astype(np.float64)
         for i in range(n_q):
             visible = seq - n_q + i + 1
-            if visible <= 0:
+            if visible <= 0 or (wanted is not None and a + i not in wanted):
                 continue
             for h in range(hq):
                 kv = h // group

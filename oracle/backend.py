@@ -73,10 +73,13 @@ def staging_write(layer: OracleLayer, key, value, slot_mapping, qsl, seqs) -> No
 
 
 def forward(layer: OracleLayer, query, key, value, slot_mapping, qsl, seqs, block_tables,
-            num_actual_tokens=None, q_dtype="bf16"):
+            num_actual_tokens=None, q_dtype="bf16", rows=None):
     """backend.py:249-282 + :334-393 in streaming mode.
 
     query [N, Hq, D], key/value [N, Hk, D] or None; all on the q_dtype grid.
+    ``rows`` (optional): token indices whose rotated-domain attention is evaluated
+    (a sampled check of long chunks); the other cached rows stay 0.  Writes and
+    fresh-only prefills are always evaluated in full.
     Returns the output [N, Hq, D] on the q_dtype grid (float32 array).
     """
     def rnd(x):
@@ -110,11 +113,22 @@ def forward(layer: OracleLayer, query, key, value, slot_mapping, qsl, seqs, bloc
         sub_qsl = np.concatenate([[0], np.cumsum(lengths)]).tolist()
         sub_seqs = [seqs[i] for i in cached]
         table = np.asarray(block_tables)[cached]
-        q_rot = rnd(rotate(query[ids], layer.rk))
+        sub_rows = None
+        if rows is not None:
+            wanted = set(int(t) for t in rows)
+            sub_rows = [j for j, t in enumerate(ids) if int(t) in wanted]
+        if sub_rows is None:
+            q_rot = rnd(rotate(query[ids], layer.rk))
+        else:
+            q_rot = np.zeros((len(ids),) + query.shape[1:], np.float32)
+            q_rot[sub_rows] = rnd(rotate(query[ids[sub_rows]], layer.rk))
         k_rot = None if key is None else rnd(rotate(np.asarray(key, np.float32)[ids], layer.rk))
         v_rot = None if value is None else rnd(rotate(np.asarray(value, np.float32)[ids], layer.rv))
         stage = layer.staging.arrays() if (layer.window_enabled and layer.staging) else None
         rotated, _ = attention_ref(q_rot, k_rot, v_rot, layer.k8, layer.v8, table, sub_qsl,
-                                   sub_seqs, layer.scale, stage, d=layer.d, q_dtype=q_dtype)
-        output[ids] = rnd(rotate(rotated, np.ascontiguousarray(layer.rv.T)))
+                                   sub_seqs, layer.scale, stage, d=layer.d, q_dtype=q_dtype,
+                                   rows=sub_rows)
+        keep = ids if sub_rows is None else ids[sub_rows]
+        src = rotated if sub_rows is None else rotated[sub_rows]
+        output[keep] = rnd(rotate(src, np.ascontiguousarray(layer.rv.T)))
     return output

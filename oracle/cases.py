@@ -64,13 +64,15 @@ def empty_caches(num_blocks: int, bs: int, hk: int, d: int, legacy: bool = False
 
 
 def make_case(prefixes, lengths, *, hk=1, group=6, d=256, bs=128, window=True, fresh=True,
-              seed=117, sink=128, recent=256, legacy=False, key_ramp=0.0):
+              seed=117, sink=128, recent=256, legacy=False, key_ramp=0.0, v_gain=1.0):
     """probe_streaming.py:31-81: packed history + optional staging + current chunk.
 
     Returns dict(q, k, v, k8, v8, bt, qsl, seqs, scale, stage).  All floats are
     float32 arrays on the bf16 grid; stage = (stage_k, stage_v, owner) or None.
     key_ramp > 0 scales history key t by 1 + key_ramp * t / 1024 (a rising score
     maximum along the history, for the attention kernels' rescale paths).
+    v_gain scales every value vector (history and current chunk), e.g. 1e3 for V
+    scales far above the unit range.
     """
     g = rng(seed)
     hq = hk * group
@@ -93,13 +95,13 @@ def make_case(prefixes, lengths, *, hk=1, group=6, d=256, bs=128, window=True, f
         pos = np.concatenate([np.arange(p_) for p_ in prefixes]) if total else np.zeros(0)
         old_k *= (1.0 + key_ramp * pos / 1024.0).astype(np.float32)[:, None, None]
     old_k = fmt.bf16_round(old_k)
-    old_v = fmt.bf16_round(g.standard_normal((total, hk, d)).astype(np.float32))
+    old_v = fmt.bf16_round(g.standard_normal((total, hk, d)).astype(np.float32) * np.float32(v_gain))
     store_ref(old_k, old_v, k8, v8, np.concatenate(slots) if slots else np.zeros(0, np.int64))
     q = fmt.bf16_round(g.standard_normal((qsl[-1], hq, d)).astype(np.float32))
     k = v = None
     if fresh:
         k = fmt.bf16_round(g.standard_normal((qsl[-1], hk, d)).astype(np.float32))
-        v = fmt.bf16_round(g.standard_normal((qsl[-1], hk, d)).astype(np.float32))
+        v = fmt.bf16_round(g.standard_normal((qsl[-1], hk, d)).astype(np.float32) * np.float32(v_gain))
     stage = None
     if window:
         rows = max(math.ceil(8192 / bs), 4)

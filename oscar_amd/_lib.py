@@ -15,6 +15,7 @@ OSCAR_F32, OSCAR_F16, OSCAR_BF16 = 0, 1, 2
 STAGE_NONE, STAGE_INVALIDATE, STAGE_WRITE = 0, 1, 2
 WORK_INTS = 8
 GROUP_INTS = 8
+ABI_VERSION = 2
 
 vp = C.c_void_p
 i32, i64, f32 = C.c_int32, C.c_int64, C.c_float
@@ -53,7 +54,8 @@ class RotateArgs(C.Structure):
 
 
 class Plan(C.Structure):
-    _fields_ = [("num_items", i32), ("num_groups", i32), ("partial_bytes", i64)]
+    _fields_ = [("num_items", i32), ("num_groups", i32), ("partial_bytes", i64),
+                ("max_group_items", i32), ("reserved", i32)]
 
 
 class AttnArgs(C.Structure):
@@ -64,7 +66,8 @@ class AttnArgs(C.Structure):
         ("query_start_loc", vp), ("seq_lens", vp), ("num_reqs", i32),
         ("staging", C.POINTER(Staging)), ("scale", f32),
         ("items", vp), ("num_items", i32), ("groups", vp), ("num_groups", i32),
-        ("workspace", vp), ("out_rot", vp), ("lse", vp), ("phases", i32), ("q_dtype", i32),
+        ("workspace", vp), ("workspace_bytes", i64), ("max_group_items", i32),
+        ("out_rot", vp), ("lse", vp), ("phases", i32), ("q_dtype", i32),
     ]
 
 
@@ -115,7 +118,7 @@ def load() -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.oscar_abi_version() != 1:
+    if lib.oscar_abi_version() != ABI_VERSION:
         raise OscarLibraryError("liboscar_amd.so ABI version mismatch")
     _LIB = lib
     return lib

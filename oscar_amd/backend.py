@@ -1,25 +1,29 @@
 """OSCAR INT2 FULL-attention impl for MI355X (drop-in for oscar_ascend/backend.py).
 
 The plugin swaps ``impl.__class__`` of FULL decoder layers to
-``OscarAttentionBackendImpl``; only ``forward`` and ``do_kv_cache_update`` (and
-their helpers) are replaced, with the reference's signatures and metadata
-accessors.  The arithmetic runs in liboscar_amd.so:
+``OscarAttentionBackendImpl``; ``forward`` and ``do_kv_cache_update`` keep the
+reference's signatures (backend.py:151-158, :249-260) and metadata accessors.  The
+arithmetic runs in liboscar_amd.so:
 
-* write   ``ops.store``: rotate (fp64-accumulated, correctly rounded), sort-clip,
-          INT2 quantize/pack/scatter with last-writer-wins, staging owner tags and
-          FP32 window, plus the bf16 rotated q/k/v the read path needs;
-* read    ``ops.attention_decode`` (requests with <= 32 rows per KV head) and
-          ``ops.attention_prefill`` (long continuation chunks and history-free
-          prefill in the original domain), then the inverse rotation
-          ``ops.rotate(out_rot, R_v^T)``.
+* write  ``ops.store``: rotate (correctly rounded), sort-clip, INT2 quantize / pack /
+         scatter with last-writer-wins, owner tags and FP32 window, plus the rotated
+         q/k/v the read path needs;
+* read   ``ops.attention_decode`` (requests of <= 32 rows per KV head),
+         ``ops.attention_prefill`` (long continuation chunks; history-free requests in
+         the original domain), then the inverse rotation ``ops.rotate(out_rot, R_v^T)``.
 
-There is no dense-history or CPU fallback: failures raise.
+Host work per call is bounded: the batch is classified on the host from the
+metadata's host lists, every integer array the kernels need goes to the device in one
+non-blocking copy from pinned memory, and a batch of decode-shaped requests (the
+serving steady state) runs with no gathers or scatters.  There is no dense-history or
+CPU fallback: failures raise.
 """
 from __future__ import annotations
 
+from dataclasses import dataclass, field
 from importlib import import_module, util
-from itertools import pairwise
 
+import numpy as np
 import torch
 
 from . import ops
@@ -28,34 +32,38 @@ from .config import OscarConfig
 from .format import K_IDX_OFF, VALUES_PER_BYTE, check_d
 from .rotation import get_layer_rotation
 
-MAX_DECODE_ROWS = 32
+MAX_DECODE_ROWS = 32  # rows (query tokens x heads per KV head) of one decode MFMA tile
+
+
+# ---------------------------------------------------------------- metadata
+def _host_list(value) -> list:
+    return value.tolist() if hasattr(value, "tolist") else list(value)
+
+
+# (attribute, how it becomes query_start_loc) in the order the reference consults them
+# (backend.py:26-56): a host tensor first, then vLLM-Ascend's cumulative ends, then the
+# device tensor.  Presence is tested with `is not None`: a multi-element tensor has no
+# truth value.
+_QUERY_STARTS = (("query_start_loc_cpu", lambda v: v),
+                 ("actual_seq_lengths_q", lambda ends: [0] + ends),
+                 ("query_start_loc", lambda v: v))
+_SEQ_LENS = ("seq_lens_list", "seq_lens_cpu", "_seq_lens_cpu", "seq_lens")
 
 
 def metadata_batch_lists(attn_metadata) -> tuple[list, list]:
-    """backend.py:26-56: host (query_start_loc, seq_lens) lists; never a Tensor as bool."""
-
-    def _as_list(x, name: str) -> list:
-        if x is None:
-            raise RuntimeError(f"attn_metadata.{name} is missing")
-        if hasattr(x, "tolist"):
-            return x.tolist()
-        return list(x)
-
-    q_sl_cpu = getattr(attn_metadata, "query_start_loc_cpu", None)
-    ends = getattr(attn_metadata, "actual_seq_lengths_q", None)
-    if q_sl_cpu is not None:
-        qsl = _as_list(q_sl_cpu, "query_start_loc_cpu")
-    elif ends is not None:
-        qsl = [0] + _as_list(ends, "actual_seq_lengths_q")
+    """Host (query_start_loc, seq_lens) lists of a batch."""
+    for attr, shape in _QUERY_STARTS:
+        value = getattr(attn_metadata, attr, None)
+        if value is not None:
+            qsl = shape(_host_list(value))
+            break
     else:
-        qsl = _as_list(attn_metadata.query_start_loc, "query_start_loc")
-    seq_cpu = getattr(attn_metadata, "seq_lens_cpu", None)
-    if seq_cpu is None:
-        seq_cpu = getattr(attn_metadata, "_seq_lens_cpu", None)
-    seq_list = getattr(attn_metadata, "seq_lens_list", None)
-    seqs = _as_list(seq_list if seq_list is not None else (
-        seq_cpu if seq_cpu is not None else attn_metadata.seq_lens), "seq_lens")
-    return qsl, seqs
+        raise RuntimeError("attn_metadata carries no query start locations")
+    for attr in _SEQ_LENS:
+        value = getattr(attn_metadata, attr, None)
+        if value is not None:
+            return qsl, _host_list(value)
+    raise RuntimeError("attn_metadata carries no sequence lengths")
 
 
 def _block_tables(md):
@@ -63,23 +71,59 @@ def _block_tables(md):
     return bt if bt is not None else md.block_table
 
 
-def _load_base_impl():
-    """Base class: vLLM's ROCm attention impl when vLLM is installed, else object.
-
-    Mirrors backend.py:68-85: an installed but broken vendor stack must fail
-    loudly instead of silently degrading to a placeholder.
-    """
+def _native_base():
+    """vLLM's ROCm attention impl when vLLM is installed, else ``object``.  An installed
+    but unimportable stack raises (the reference's rule, backend.py:68-85): the plugin
+    must not silently degrade to a placeholder."""
     if util.find_spec("vllm") is None:
         return object
     try:
         _ = import_module("vllm.platforms").current_platform
-        native = import_module("vllm.v1.attention.backends.rocm_attn")
-        return native.RocmAttentionImpl
+        return import_module("vllm.v1.attention.backends.rocm_attn").RocmAttentionImpl
     except Exception as exc:
         raise RuntimeError("OSCAR could not import the installed ROCm attention backend") from exc
 
 
-BaseAttentionImpl = _load_base_impl()
+BaseAttentionImpl = _native_base()
+
+
+# ---------------------------------------------------------------- batch classification
+@dataclass
+class _Batch:
+    """Host view of one read: which requests go where (backend.py:334-393 routing)."""
+    qsl: list                  # query starts clipped to the actual token count
+    seqs: list
+    actual: int
+    fresh: list = field(default_factory=list)   # no history: original-domain prefill
+    short: list = field(default_factory=list)   # cached, <= 32 rows per KV head: decode
+    long: list = field(default_factory=list)    # cached, more rows: prefill / split
+
+    @classmethod
+    def classify(cls, qsl, seqs, actual, has_new, group):
+        b = cls([min(s, actual) for s in qsl], list(seqs), actual)
+        for i in range(len(b.qsl) - 1):
+            n = b.qsl[i + 1] - b.qsl[i]
+            if n <= 0:
+                continue
+            if has_new and b.seqs[i] == n:
+                b.fresh.append(i)
+            elif n * group <= MAX_DECODE_ROWS:
+                b.short.append(i)
+            else:
+                b.long.append(i)
+        if has_new and any(b.seqs[i] < b.qsl[i + 1] - b.qsl[i] for i in b.short + b.long):
+            raise ValueError("Sequence length must cover its query chunk")
+        return b
+
+    @property
+    def decode_only(self) -> bool:
+        """Every active request decode-shaped: the plan runs over the batch as it is."""
+        return not self.fresh and not self.long
+
+    @property
+    def covers_all(self) -> bool:
+        """The requests' query ranges tile [0, actual) (no padding rows to zero)."""
+        return self.qsl[0] == 0 and self.qsl[-1] == self.actual
 
 
 class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-type]
@@ -87,7 +131,7 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
 
     # ------------------------------------------------------------------ setup
     def _oscar_setup(self) -> None:
-        """backend.py:100-123."""
+        """Idempotent per impl: configuration from the environment, shape checks."""
         if getattr(self, "_oscar_cfg", None) is not None:
             return
         cfg = OscarConfig.from_env(head_dim=self.head_size)
@@ -109,64 +153,67 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
 
     # ------------------------------------------------------------------ geometry
     def _set_caches(self, kv_cache) -> None:
-        """backend.py:200-236: accept a (K, V) pair or a stacked tensor; check slot fit."""
+        """Take the (K, V) pair or a stacked [2, ...] tensor; check the slot geometry
+        once: the slot width must be D (packed int8) or 2D (legacy bf16) bytes, and the
+        96-byte K / 64-byte V payload must fit (backend.py:200-236 contract)."""
+        pair = None
         if isinstance(kv_cache, (tuple, list)) and len(kv_cache) >= 2:
-            self.key_cache, self.value_cache = kv_cache[0], kv_cache[1]
+            pair = (kv_cache[0], kv_cache[1])
         elif isinstance(kv_cache, torch.Tensor) and kv_cache.dim() > 0:
-            self.key_cache, self.value_cache = kv_cache[0], kv_cache[1]
+            pair = (kv_cache[0], kv_cache[1])
+        if pair is not None:
+            self.key_cache, self.value_cache = pair
         if getattr(self, "key_cache", None) is None or getattr(self, "value_cache", None) is None:
             raise ValueError("OSCAR requires K and V caches")
-        if not getattr(self, "_oscar_geo_ok", False):
-            k8 = self.key_cache.view(torch.uint8)
-            v8 = self.value_cache.view(torch.uint8)
-            if k8.ndim != 4 or v8.ndim != 4 or not k8.is_contiguous() or not v8.is_contiguous():
-                raise ValueError("OSCAR requires contiguous [blocks, tokens, heads, bytes] caches")
-            slot_k, slot_v = int(k8.stride(2)), int(v8.stride(2))
-            need_k = K_IDX_OFF + self.head_size // VALUES_PER_BYTE
-            need_v = self.head_size // VALUES_PER_BYTE
-            if slot_k not in (self.head_size, 2 * self.head_size):
-                raise AssertionError(f"[oscar-amd] K slot width {slot_k}B, expected "
-                                     f"{self.head_size} (packed) or {2 * self.head_size} (legacy)")
-            if need_k > slot_k or need_v > slot_v:
-                raise AssertionError(f"[oscar-amd] slot too small: K needs {need_k}B / V {need_v}B")
-            self._oscar_geo_ok = True
+        if getattr(self, "_oscar_geo_ok", False):
+            return
+        k8, v8 = self.key_cache.view(torch.uint8), self.value_cache.view(torch.uint8)
+        if k8.ndim != 4 or v8.ndim != 4 or not k8.is_contiguous() or not v8.is_contiguous():
+            raise ValueError("OSCAR requires contiguous [blocks, tokens, heads, bytes] caches")
+        d = self.head_size
+        k_slot, v_slot = int(k8.stride(2)), int(v8.stride(2))
+        if k_slot not in (d, 2 * d):
+            raise AssertionError(f"[oscar-amd] K slot width {k_slot}B, expected {d} (packed) "
+                                 f"or {2 * d} (legacy)")
+        k_need, v_need = K_IDX_OFF + d // VALUES_PER_BYTE, d // VALUES_PER_BYTE
+        if k_need > k_slot or v_need > v_slot:
+            raise AssertionError(f"[oscar-amd] slot too small: K needs {k_need}B / V {v_need}B")
+        self._oscar_geo_ok = True
 
     def _layer_rots(self, layer, device):
-        """backend.py:238-246: strict per-layer R_k, R_v cached on the layer."""
-        if not getattr(layer, "_oscar_rots", None):
+        """(R_k, R_v) of the layer, loaded strictly once and kept on the layer as fp32."""
+        rots = getattr(layer, "_oscar_rots", None)
+        if not rots:
             cfg = self._oscar
-            rk = get_layer_rotation(cfg.k_rotation_path, layer.layer_name, self.head_size, device,
-                                    mode="k", strict=True)
-            rv = get_layer_rotation(cfg.v_rotation_path, layer.layer_name, self.head_size, device,
-                                    mode="v", strict=True)
-            layer._oscar_rots = (rk, rv)
-        rk, rv = layer._oscar_rots
-        if rk.device != device or rk.dtype != torch.float32:
-            rk = rk.to(device=device, dtype=torch.float32).contiguous()
-            rv = rv.to(device=device, dtype=torch.float32).contiguous()
-            layer._oscar_rots = (rk, rv)
-        return layer._oscar_rots
+            rots = tuple(get_layer_rotation(path, layer.layer_name, self.head_size, device,
+                                            mode=mode, strict=True)
+                         for path, mode in ((cfg.k_rotation_path, "k"), (cfg.v_rotation_path, "v")))
+        if rots[0].device != device or rots[0].dtype != torch.float32:
+            rots = tuple(r.to(device=device, dtype=torch.float32).contiguous() for r in rots)
+        layer._oscar_rots = rots
+        return rots
 
     # ------------------------------------------------------------------ staging arena
     def _ensure_staging(self, layer, kv_cache) -> None:
-        """backend.py:492-511: per-layer FP32 window arena and owner tags."""
+        """Allocate the layer's FP32 window arena once (backend.py:492-511 sizing): seats
+        for ceil(staging / bs) pages, and never fewer than the sink pages, the recent
+        pages (+1 for a page boundary) and 2 spare rows."""
         if getattr(layer, "_oscar_stage_ready", False):
             return
-        bs = kv_cache[0].shape[1]
         cfg = self._oscar
+        bs = kv_cache[0].shape[1]
         self.stage_block = bs
-        self.sink_eff = (cfg.sink_tokens // bs) * bs
+        self.sink_eff = cfg.sink_tokens - cfg.sink_tokens % bs   # whole sink pages only
         self.sink_pages = self.sink_eff // bs
-        self.tail_pages = (cfg.recent_tokens + bs - 1) // bs + 1
-        rows = max((cfg.staging_tokens + bs - 1) // bs, self.sink_pages + self.tail_pages + 2)
+        self.tail_pages = -(-cfg.recent_tokens // bs) + 1
+        rows = max(-(-cfg.staging_tokens // bs), self.sink_pages + self.tail_pages + 2)
         dev = kv_cache[0].device
-        layer._oscar_stage_k = torch.zeros(rows, bs, self.num_kv_heads, self.head_size,
-                                           dtype=torch.float32, device=dev)
-        layer._oscar_stage_v = torch.zeros_like(layer._oscar_stage_k)
-        layer._oscar_slot_owner = torch.full((rows, bs), -1, dtype=torch.int64, device=dev)
+        shape = (rows, bs, self.num_kv_heads, self.head_size)
+        layer._oscar_stage_k = torch.zeros(shape, dtype=torch.float32, device=dev)
+        layer._oscar_stage_v = torch.zeros(shape, dtype=torch.float32, device=dev)
+        layer._oscar_slot_owner = torch.full(shape[:2], -1, dtype=torch.int64, device=dev)
         layer._oscar_stage_rows = rows
-        layer._oscar_stage_ready = True
-        self._oscar_stage_ready = True
+        layer._oscar_stage_ready = self._oscar_stage_ready = True
 
     def _stage(self, layer):
         if self._oscar.window_enabled and getattr(layer, "_oscar_stage_ready", False):
@@ -174,34 +221,31 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         return None
 
     # ------------------------------------------------------------------ write path
-    def _store(self, layer, key, value, slot_mapping, *, mode, qsl=None, seqs=None, query=None,
-               outputs=None):
+    def _store(self, layer, key, value, slot_mapping, *, mode, qsl_dev=None, seqs_dev=None,
+               num_reqs=0, query=None, outputs=False):
+        """One fused store call; returns the rotated (q, k, v) for the read when asked."""
         n = slot_mapping.shape[0]
-        D, hk = self.head_size, self.num_kv_heads
+        d, hk = self.head_size, self.num_kv_heads
         rk, rv = self._layer_rots(layer, key.device)
         stage = None
         if getattr(layer, "_oscar_stage_ready", False):
             stage = (layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner)
-        extra = {}
+        window = {}
         if mode == STAGE_WRITE:
-            n_req = len(seqs)
-            qsl_t = torch.tensor(qsl[: n_req + 1], dtype=torch.int32).to(key.device)
-            seq_t = torch.tensor(seqs[:n_req] or [0], dtype=torch.int32).to(key.device)
-            extra = dict(qsl_dev=qsl_t, seqs_dev=seq_t, num_reqs=n_req,
-                         recent_tokens=self._oscar.recent_tokens,
-                         sink_tokens_eff=self.sink_eff)
+            window = dict(qsl_dev=qsl_dev, seqs_dev=seqs_dev, num_reqs=num_reqs,
+                          recent_tokens=self._oscar.recent_tokens, sink_tokens_eff=self.sink_eff)
         q_rot = k_rot = v_rot = None
         if outputs:
-            k_rot = torch.empty(n, hk, D, dtype=key.dtype, device=key.device)
+            k_rot = torch.empty(n, hk, d, dtype=key.dtype, device=key.device)
             v_rot = torch.empty_like(k_rot)
             if query is not None:
-                q_rot = torch.empty(n, query.shape[1], D, dtype=query.dtype, device=key.device)
+                q_rot = torch.empty(n, query.shape[1], d, dtype=query.dtype, device=key.device)
         ops.store(key[:n], value[:n], self.key_cache, self.value_cache, slot_mapping,
-                  head_dim=D, rk=rk, rv=rv, k_clip=self._oscar.k_clip_ratio,
+                  head_dim=d, rk=rk, rv=rv, k_clip=self._oscar.k_clip_ratio,
                   v_clip=self._oscar.v_clip_ratio, stage=stage,
                   stage_mode=mode if stage is not None else STAGE_NONE,
                   query=None if query is None else query[:n], query_rot=q_rot,
-                  key_rot=k_rot, value_rot=v_rot, **extra)
+                  key_rot=k_rot, value_rot=v_rot, **window)
         self._oscar_stats["writes"] += 1
         self._oscar_stats["kv_bytes_written"] += n * hk * 160
         return q_rot, k_rot, v_rot
@@ -216,20 +260,10 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         self._set_caches(kv_cache)
         self._store(layer, key, value, slot_mapping, mode=STAGE_INVALIDATE)
 
-    def _staging_write(self, layer, key, value, attn_metadata) -> None:
-        """backend.py:513-555: window values and owner tags (the INT2 bytes are rewritten
-        with identical contents by the same fused call)."""
-        n = attn_metadata.num_actual_tokens
-        if n == 0:
-            return
-        qsl, seqs = metadata_batch_lists(attn_metadata)
-        slots = attn_metadata.slot_mapping[:n].to(device=key.device, dtype=torch.int64)
-        self._store(layer, key, value, slots, mode=STAGE_WRITE, qsl=qsl, seqs=seqs)
-
     # ------------------------------------------------------------------ forward
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
                 output_scale=None, output_block_scale=None):
-        """backend.py:249-282 (streaming mode)."""
+        """backend.py:249-282 (streaming mode): write + window, then the read."""
         assert output is not None, "Output tensor must be provided."
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("OSCAR fused output quantization is unsupported")
@@ -238,106 +272,143 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         self._set_caches(kv_cache)
         if (key is None) != (value is None):
             raise ValueError("Both new K and V must be supplied together")
-        rotated = None
-        if key is not None:
-            n = attn_metadata.num_actual_tokens
-            slots = attn_metadata.slot_mapping[:n].to(device=key.device, dtype=torch.int64)
-            mode = STAGE_NONE
-            qsl = seqs = None
-            if self._oscar.window_enabled:
-                self._ensure_staging(layer, kv_cache)
-                mode = STAGE_WRITE
-                qsl, seqs = metadata_batch_lists(attn_metadata)
-            elif getattr(layer, "_oscar_stage_ready", False):
-                mode = STAGE_INVALIDATE
-            if n > 0:
-                rotated = self._store(layer, key.view(-1, self.num_kv_heads, self.head_size),
-                                      value.view(-1, self.num_kv_heads, self.head_size), slots,
-                                      mode=mode, qsl=qsl, seqs=seqs,
-                                      query=query.view(-1, self.num_heads, self.head_size),
-                                      outputs=True)
-        return self._streaming_attention(layer, query, key, value, kv_cache, attn_metadata,
-                                         output, rotated)
+        return self._run(layer, query, key, value, kv_cache, attn_metadata, output, write=True)
 
-    def _streaming_attention(self, layer, query, key, value, kv_cache, metadata, output,
-                             rotated=None):
-        """backend.py:334-393: fresh-only requests prefill in the original domain; cached
-        requests attend in the rotated domain, then out_rot @ R_v^T."""
+    def _streaming_attention(self, layer, query, key, value, kv_cache, metadata, output):
+        """backend.py:334-393: the read alone (the history and window are the state)."""
+        return self._run(layer, query, key, value, kv_cache, metadata, output, write=False)
+
+    def _run(self, layer, query, key, value, kv_cache, md, output, *, write):
         if (key is None) != (value is None):
             raise ValueError("Both new K and V must be supplied together")
         if query.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("OSCAR MI355X attention requires bf16 or fp16 queries; "
                              f"got dtype={query.dtype}")
-        D, hq, hk = self.head_size, self.num_heads, self.num_kv_heads
+        d, hq, hk = self.head_size, self.num_heads, self.num_kv_heads
         group = hq // hk
-        q3 = query.view(-1, hq, D)
-        actual = min(q3.shape[0], metadata.num_actual_tokens)
-        output.zero_()
+        dev = query.device
+        q3 = query.view(-1, hq, d)
+        k3 = None if key is None else key.view(-1, hk, d)
+        v3 = None if value is None else value.view(-1, hk, d)
+        n_md = md.num_actual_tokens
+        actual = min(q3.shape[0], n_md)
+        has_new = key is not None
+        if write and has_new and (q3.shape[0] < n_md or k3.shape[0] < n_md or v3.shape[0] < n_md):
+            raise ValueError("query/key/value hold fewer rows than num_actual_tokens")
+        qsl, seqs = metadata_batch_lists(md)
+        batch = _Batch.classify(qsl, seqs, actual, has_new, group)
+        stage_mode = STAGE_NONE
+        if write and has_new:
+            if self._oscar.window_enabled:
+                self._ensure_staging(layer, kv_cache)
+                stage_mode = STAGE_WRITE
+            elif getattr(layer, "_oscar_stage_ready", False):
+                stage_mode = STAGE_INVALIDATE
+        write_now = write and has_new and n_md > 0
+        window = (self.sink_eff, self._oscar.recent_tokens) if self._stage(layer) is not None else (0, 0)
+
+        # ---- host planning, then every integer array in one upload
+        parts = []
+        if write_now and stage_mode == STAGE_WRITE:
+            store_qsl = [min(s, n_md) for s in qsl]
+            parts += [np.asarray(store_qsl, np.int32), np.asarray(seqs[:len(qsl) - 1] or [0], np.int32)]
+        plan, route = None, None
+        if batch.short or (batch.long and not has_new):
+            route = self._decode_route(batch, has_new, group)
+            plan = ops.plan_decode(route["qsl"], route["seqs"], has_new=has_new, num_kv_heads=hk,
+                                   group=group, head_dim=d, device=dev, window=window,
+                                   upload_now=False)
+            parts += plan.host_parts() + route["index_parts"]
+        cached_rows = None
+        if not batch.decode_only and (batch.short or batch.long):
+            cached_rows = np.concatenate([np.arange(batch.qsl[i], batch.qsl[i + 1])
+                                          for i in batch.short + batch.long]).astype(np.int64)
+            parts.append(cached_rows)
+        dev_parts = ops.upload(parts, dev) if parts else []
+        if write_now and stage_mode == STAGE_WRITE:
+            store_qsl_dev, store_seqs_dev, dev_parts = dev_parts[0], dev_parts[1], dev_parts[2:]
+        if plan is not None:
+            plan.adopt(dev_parts[:4])
+            route["index_dev"] = dev_parts[4:4 + len(route["index_parts"])]
+            dev_parts = dev_parts[4 + len(route["index_parts"]):]
+        cached_rows_dev = dev_parts[0] if cached_rows is not None else None
+
+        # ---- write
+        rotated = None
+        if write_now:
+            slots = md.slot_mapping[:n_md].to(device=dev, dtype=torch.int64)
+            extra = {}
+            if stage_mode == STAGE_WRITE:
+                extra = dict(qsl_dev=store_qsl_dev, seqs_dev=store_seqs_dev, num_reqs=len(qsl) - 1)
+            rotated = self._store(layer, k3, v3, slots, mode=stage_mode, query=q3, outputs=True, **extra)
+
+        # ---- read
+        if actual < q3.shape[0] or actual == 0 or not (batch.decode_only and batch.covers_all):
+            output.zero_()
         if actual == 0:
             return output
-        out3 = output.view(-1, hq, D)
-        starts, seqs = metadata_batch_lists(metadata)
-        starts = [min(s, actual) for s in starts]
-        active = [i for i, (a, b) in enumerate(pairwise(starts)) if b > a]
-        fresh = [i for i in active if key is not None and seqs[i] == starts[i + 1] - starts[i]]
-        cached = [i for i in active if i not in fresh]
-        k3 = None if key is None else key.view(-1, hk, D)
-        v3 = None if value is None else value.view(-1, hk, D)
-        for i in fresh:
-            a, b = starts[i], starts[i + 1]
-            out3[a:b] = ops.attention_prefill(q3[a:b], k3[a:b], v3[a:b], self.scale, head_dim=D)
-        if not cached:
+        out3 = output.view(-1, hq, d)
+        for i in batch.fresh:
+            a, b = batch.qsl[i], batch.qsl[i + 1]
+            ops.attention_prefill(q3[a:b], k3[a:b], v3[a:b], self.scale, head_dim=d, out=out3[a:b])
+        if not (batch.short or batch.long):
             return output
-        rk, rv = self._layer_rots(layer, query.device)
-        if rotated is not None:
-            q_rot, k_rot, v_rot = rotated
+        rk, rv = self._layer_rots(layer, dev)
+        if rotated is not None and rotated[0] is not None:
+            q_rot, k_rot, v_rot = (t[:actual] for t in rotated)
         else:
             q_rot = ops.rotate(q3[:actual], rk)
             k_rot = None if k3 is None else ops.rotate(k3[:actual], rk)
             v_rot = None if v3 is None else ops.rotate(v3[:actual], rv)
         stage = self._stage(layer)
-        table = _block_tables(metadata)
-        out_rot = torch.zeros(actual, hq, D, dtype=torch.float32, device=query.device)
-        lse = torch.full((actual, hq), float("-inf"), dtype=torch.float32, device=query.device)
-        has_new = key is not None
-        short = [i for i in cached if (starts[i + 1] - starts[i]) * group <= MAX_DECODE_ROWS]
-        long = [i for i in cached if i not in short]
-        # cache-only long chunks: split into sub-requests of at most 32 rows (right-aligned
-        # causality is preserved: sub-request j sees the keys up to its own last query)
-        sub_qsl, sub_seqs, sub_rows = [0], [], []
-        step = max(1, MAX_DECODE_ROWS // group)
-        for i in short + ([] if has_new else long):
-            a, b, seq = starts[i], starts[i + 1], seqs[i]
-            for s in range(a, b, step):
-                e = min(b, s + step)
-                sub_rows.append((i, s, e))
-                sub_qsl.append(sub_qsl[-1] + e - s)
-                sub_seqs.append(seq - (b - e))
-        if has_new and any(seqs[i] < starts[i + 1] - starts[i] for i in cached):
-            raise ValueError("Sequence length must cover its query chunk")
-        if sub_rows:
-            ids = torch.cat([torch.arange(s, e) for _, s, e in sub_rows]).to(query.device)
-            req = torch.tensor([i for i, _, _ in sub_rows], device=table.device)
-            kn = None if not has_new else k_rot[ids]
-            vn = None if not has_new else v_rot[ids]
-            window = (self.sink_eff, self._oscar.recent_tokens) if stage is not None else (0, 0)
-            plan = ops.plan_decode(sub_qsl, sub_seqs, has_new=has_new, num_kv_heads=hk,
-                                   group=group, head_dim=D, device=query.device, window=window)
-            o, l = ops.attention_decode(q_rot[ids], kn, vn, self.key_cache, self.value_cache,
-                                        table[req], plan, self.scale, stage, head_dim=D)
-            out_rot[ids], lse[ids] = o, l
+        table = _block_tables(md)
+        out_rot = torch.empty(actual, hq, d, dtype=torch.float32, device=dev)
+        lse = torch.empty(actual, hq, dtype=torch.float32, device=dev)
+        if plan is not None:
+            if route["identity"]:
+                ops.attention_decode(q_rot, k_rot, v_rot, self.key_cache, self.value_cache, table,
+                                     plan, self.scale, stage, head_dim=d, out_rot=out_rot, lse=lse)
+            else:
+                ids, req = route["index_dev"]
+                pick = (lambda t: None if t is None else torch.index_select(t, 0, ids))
+                o, l_ = ops.attention_decode(pick(q_rot), pick(k_rot), pick(v_rot), self.key_cache,
+                                             self.value_cache, torch.index_select(table, 0, req),
+                                             plan, self.scale, stage, head_dim=d)
+                out_rot.index_copy_(0, ids, o)
+                lse.index_copy_(0, ids, l_)
         if has_new:
-            for i in long:
-                a, b, seq = starts[i], starts[i + 1], seqs[i]
-                lse_i = torch.empty(b - a, hq, dtype=torch.float32, device=query.device)
-                out_rot[a:b] = ops.attention_prefill(
-                    q_rot[a:b], k_rot[a:b], v_rot[a:b], self.scale, head_dim=D,
-                    history=seq - (b - a), k_cache=self.key_cache, v_cache=self.value_cache,
-                    block_table_row=table[i], stage=stage, lse=lse_i)
-                lse[a:b] = lse_i
-        idx = torch.tensor([t for i in cached for t in range(starts[i], starts[i + 1])],
-                           device=query.device)
-        out3[idx] = ops.rotate(out_rot[idx], rv, transpose=True, out_dtype=query.dtype)
+            for i in batch.long:
+                a, b = batch.qsl[i], batch.qsl[i + 1]
+                ops.attention_prefill(q_rot[a:b], k_rot[a:b], v_rot[a:b], self.scale, head_dim=d,
+                                      history=batch.seqs[i] - (b - a), k_cache=self.key_cache,
+                                      v_cache=self.value_cache, block_table_row=table[i],
+                                      stage=stage, out=out_rot[a:b], lse=lse[a:b])
+        if batch.decode_only:
+            ops.rotate(out_rot, rv, transpose=True, out_dtype=query.dtype, out=out3[:actual])
+        else:
+            rows = torch.index_select(out_rot, 0, cached_rows_dev)
+            out3.index_copy_(0, cached_rows_dev, ops.rotate(rows, rv, transpose=True, out_dtype=query.dtype))
         self._oscar_stats["reads"] += 1
         self._last_lse = lse
         return output
+
+    def _decode_route(self, batch: _Batch, has_new: bool, group: int) -> dict:
+        """Requests for the split-K decode.  A decode-only batch is planned as it is (the
+        plan's request r is metadata request r: no gathers).  Otherwise the decode-shaped
+        requests, and (cache-only) the long ones cut into sub-requests of <= 32 rows,
+        form a compact batch: sub-request j of request i keeps right-aligned causality by
+        seeing the keys up to its own last query."""
+        if batch.decode_only:
+            return dict(identity=True, qsl=batch.qsl, seqs=batch.seqs, index_parts=[])
+        step = max(1, MAX_DECODE_ROWS // group)
+        sub_qsl, sub_seqs, ids, req = [0], [], [], []
+        for i in batch.short + ([] if has_new else batch.long):
+            a, b, seq = batch.qsl[i], batch.qsl[i + 1], batch.seqs[i]
+            for s in range(a, b, step):
+                e = min(b, s + step)
+                ids.extend(range(s, e))
+                req.append(i)
+                sub_qsl.append(sub_qsl[-1] + e - s)
+                sub_seqs.append(seq - (b - e))
+        return dict(identity=False, qsl=sub_qsl, seqs=sub_seqs,
+                    index_parts=[np.asarray(ids, np.int64), np.asarray(req, np.int64)])

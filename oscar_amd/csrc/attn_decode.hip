@@ -64,6 +64,9 @@ constexpr int kMaxPages = kMaxItemTokens / kTile + 2;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.f;         // max drift (log2 units) before O is rescaled
+// largest V scale (after the wave's power-of-two factor) in the fast PV operand:
+// P' = p * s_V with p <= 2^kLazy stays below the fp16 maximum 65504
+constexpr float kVScaleMax = 255.f;
 typedef short __attribute__((ext_vector_type(4))) i16x4;
 typedef _Float16 __attribute__((ext_vector_type(2))) f16x2;
 typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
@@ -424,6 +427,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
 
   // ---- running state (per lane row n): reference max m_run (log2 units), sum l, z
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f;
+  // Power-of-two factor applied to the V scales of the fast PV operand P' = p * s_V * v_fac
+  // (wave-uniform).  p <= 2^kLazy, so P' stays finite in fp16 while s_V * v_fac <=
+  // kVScaleMax; a tile whose V scale exceeds that lowers v_fac (and rescales O by the
+  // same factor) before its PV.  v_fac = 1 unless some V range exceeds ~765.
+  float v_fac = 1.f;
   f32x16 O[C::MBLK];
 #pragma unroll
   for (int b = 0; b < C::MBLK; ++b)
@@ -666,7 +674,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   auto qk_tile = [&](const TileRegs<D>& r, f32x16& S) {
 #pragma unroll
     for (int i = 0; i < C::NQ; ++i) *(u32x4*)&s_vcode[wave][m * C::NB + g * (D / 8) + 16 * i] = r.v[i];
-    s_cst[wave][0][m] = f16_bits_to_f32(r.meta[1] & 0xffff);  // both halves write the same
+    const float sv_raw = f16_bits_to_f32(r.meta[1] & 0xffff);
+    if (__any(sv_raw * v_fac > kVScaleMax)) {
+      // lower v_fac to the largest power of two that keeps every V scale of the tile
+      // within kVScaleMax (frexp: mx / kVScaleMax = f * 2^e, f in [0.5, 1))
+      int e;
+      frexpf(wave_max(sv_raw) / kVScaleMax, &e);
+      const float nf = ldexpf(1.f, -e);
+      const float f = nf / v_fac;
+#pragma unroll
+      for (int b = 0; b < C::MBLK; ++b)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; ++r2) O[b][r2] *= f;
+      v_fac = nf;
+    }
+    s_cst[wave][0][m] = sv_raw * v_fac;  // both halves write the same
     s_cst[wave][1][m] = f16_bits_to_f32(r.meta[1] >> 16);
     unsigned t_lo, t_hi;
     byte_tables<QT>(r.meta[0], t_lo, t_hi);
@@ -802,12 +824,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     if (fast) pv_tile(S);
   }
 
-  // ---- fast-tile accumulators to value units: O = O * 2^(24-2k) + z
+  // ---- fast-tile accumulators to value units: O = O * 2^(24-2k) / v_fac + z
   {
     const float z_row = z_run + swap_halves(z_run);
 #pragma unroll
     for (int b = 0; b < C::MBLK; ++b) {
-      const float f = ldexpf(1.f, 24 - pv_pos(b));
+      const float f = ldexpf(1.f, 24 - pv_pos(b)) / v_fac;
 #pragma unroll
       for (int r = 0; r < 16; ++r) O[b][r] = fmaf(O[b][r], f, z_row);
     }
@@ -902,7 +924,22 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
   const int n = lane & 31, gg = lane >> 5;
   const int bq = blockIdx.y, b = bq >> 2, q = bq & 3;
   const int e = bq * 64 + lane;  // f32x4 index in the partial
+  // a record that breaks oscar_attn_plan_v1's rules: rows outside the call are not
+  // written at all; a bad item range turns the group's rows into NaN
+  if (a < 0 || nq < 1 || nq * G > 32 || (int64_t)a + nq > A.num_tokens || kvh < 0 ||
+      kvh >= A.cache.num_kv_heads)
+    return;
+  const bool bad = i0 < 0 || ni < 0 || (int64_t)i0 + ni > A.num_items;
   const bool row_ok = n < nq * G;
+  if (bad) {
+    if (wave > 0 || !row_ok) return;
+    const int tok = a + n / G, head = kvh * G + n % G;
+    float* orow = A.out_rot + ((int64_t)tok * A.num_q_heads + head) * D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) orow[pv_d<D>(b, out_tok(4 * q + j, gg))] = NAN;
+    if (bq == 0 && gg == 0) A.lse[(int64_t)tok * A.num_q_heads + head] = NAN;
+    return;
+  }
   const f32x4* po = (const f32x4*)P.part_o + (int64_t)i0 * C::NV + e;
   const float* pl = P.part_lse + (int64_t)i0 * 32 + n;
   float M = -INFINITY, L = 0.f;
@@ -997,9 +1034,9 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
   }
   if (p.a.phases != 1) {
     // waves per merge workgroup: a power of two giving each wave one load round of
-    // up to kBatch items (8 x 24K MTP, 32 items per group: 2 waves measured 0.2-0.3 us
-    // faster per step than 4, and 8 or 1 slower)
-    const int per_group = (p.a.num_items + p.a.num_groups - 1) / p.a.num_groups;
+    // up to kBatch items of the largest group (8 x 24K MTP, 32 items per group: 2 waves
+    // measured 0.2-0.3 us faster per step than 4, and 8 or 1 slower)
+    const int per_group = p.a.max_group_items > 0 ? p.a.max_group_items : p.a.num_items;
     int waves = 1;
     while (waves < kMergeWaves && waves * kBatch < per_group) waves *= 2;
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / 64), dim3(waves * 64), 0, s, p);
@@ -1165,6 +1202,8 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
   plan->num_items = (int32_t)nitems;
   plan->num_groups = ngroups;
   plan->partial_bytes = nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
+  plan->max_group_items = (int32_t)max_k;
+  plan->reserved = 0;
   if (items == nullptr || groups == nullptr) return (int)nitems;  // size query
   if (nitems > max_items || ngroups > max_groups) return fail(-28, "oscar_attn_plan_v1: buffers too small");
   // item p of a group: tail items, then head, then body (split), or item p of the
@@ -1249,6 +1288,11 @@ extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream
   if (a.staging && (a.staging->rows < 1 || a.staging->rows * a.cache.block_size >= (1ll << 31) ||
                     (((uintptr_t)a.staging->stage_k) & 15) || (((uintptr_t)a.staging->stage_v) & 15)))
     return fail(-22, "oscar_attn_decode_v1: staging arena rows out of range or unaligned");
+  if (a.workspace_bytes < (int64_t)a.num_items * 32 * (D + 1) * (int64_t)sizeof(float))
+    return fail(-22, "oscar_attn_decode_v1: workspace of %lld bytes < %lld for %d items",
+                (long long)a.workspace_bytes, (long long)a.num_items * 32 * (D + 1) * 4, a.num_items);
+  if (a.max_group_items < 0 || a.max_group_items > a.num_items)
+    return fail(-22, "oscar_attn_decode_v1: max_group_items out of range");
   AttnParams p{};
   p.a = a;
   p.has_stage = a.staging != nullptr;

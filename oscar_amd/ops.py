@@ -10,6 +10,7 @@ import ctypes as C
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -48,17 +49,50 @@ def cache_struct(k_cache: torch.Tensor, v_cache: torch.Tensor, head_dim: int) ->
     return c
 
 
-def staging_struct(stage) -> _lib.Staging | None:
+def staging_struct(stage, k_cache: torch.Tensor | None = None, head_dim: int | None = None) -> _lib.Staging | None:
+    """The FP32 window arena (stage_k, stage_v, owner) as a C struct.  With the cache
+    given, its geometry is checked against it (streaming_attention.py:55-65): owner
+    [rows, block_size], values [rows, block_size, Hk, D], rows >= 1, all contiguous."""
     if stage is None:
         return None
     sk, sv, owner = stage
-    if sk.dtype != torch.float32 or owner.dtype != torch.int64:
+    if sk.dtype != torch.float32 or sv.dtype != torch.float32 or owner.dtype != torch.int64:
         raise ValueError("staging arena must be fp32 values and int64 owner tags")
     if not (sk.is_contiguous() and sv.is_contiguous() and owner.is_contiguous()):
         raise ValueError("Streaming staging tensors must be contiguous")
+    if k_cache is not None:
+        rows = owner.shape[0] if owner.ndim == 2 else 0
+        want = (rows, k_cache.shape[1], k_cache.shape[2], head_dim)
+        if rows < 1 or tuple(owner.shape) != want[:2] or tuple(sk.shape) != want or tuple(sv.shape) != want:
+            raise ValueError("Invalid streaming staging geometry")
     s = _lib.Staging()
     s.stage_k, s.stage_v, s.owner, s.rows = sk.data_ptr(), sv.data_ptr(), owner.data_ptr(), owner.shape[0]
     return s
+
+
+def upload(parts, device) -> list:
+    """Host integer arrays (int32 / int64) to the device in ONE non-blocking copy.
+
+    The arrays are packed at 8-byte aligned offsets into one pinned host buffer (torch's
+    caching host allocator keeps the block until the copy has run, so the host never
+    waits for the stream); the returned device tensors are views of one device buffer."""
+    arrays = [np.ascontiguousarray(p) for p in parts]
+    offsets, total = [], 0
+    for a in arrays:
+        if a.dtype not in (np.int32, np.int64):
+            raise TypeError("upload() takes int32 or int64 arrays")
+        offsets.append(total)
+        total += (a.nbytes + 7) & ~7
+    host = torch.empty(max(total, 8), dtype=torch.uint8, pin_memory=True)
+    view = host.numpy()
+    for a, o in zip(arrays, offsets):
+        view[o:o + a.nbytes] = a.view(np.uint8)
+    dev = host.to(device, non_blocking=True)
+    out = []
+    for a, o in zip(arrays, offsets):
+        dt = torch.int32 if a.dtype == np.int32 else torch.int64
+        out.append(dev[o:o + a.nbytes].view(dt) if a.size else torch.empty(0, dtype=dt, device=device))
+    return out
 
 
 class DeviceScratch:
@@ -146,7 +180,7 @@ def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=N
     slot_mapping = slot_mapping.to(device=dev, dtype=torch.int64).contiguous()
     scratch = DeviceScratch.get(dev)
     cache = cache_struct(k_cache, v_cache, head_dim)
-    st = staging_struct(stage)
+    st = staging_struct(stage, k_cache, head_dim)
     seats = 0 if st is None else st.rows * cache.block_size
     slot_claims, seat_claims = scratch.claims(cache.num_blocks * cache.block_size, seats)
     a = _lib.StoreArgs()
@@ -214,55 +248,84 @@ def rotate(x: torch.Tensor, r: torch.Tensor, *, transpose=False, out_dtype=None,
 # ------------------------------------------------------------------------ decode attention
 @dataclass
 class DecodePlan:
-    items: torch.Tensor      # device int32 [num_items, WORK_INTS]
-    groups: torch.Tensor     # device int32 [num_groups, 4]
-    qsl: torch.Tensor        # device int32 [B + 1]
-    seqs: torch.Tensor       # device int32 [B]
-    num_items: int
-    num_groups: int
-    partial_bytes: int
-    host_items: list
+    """A split-K plan: host records (items, groups) and, once uploaded, their device copies."""
+    host_items: np.ndarray   # int32 [num_items * WORK_INTS]
+    host_groups: np.ndarray  # int32 [num_groups * GROUP_INTS]
     host_qsl: list
     host_seqs: list
     has_new: bool
+    num_items: int
+    num_groups: int
+    partial_bytes: int
+    max_group_items: int
+    items: torch.Tensor | None = None   # device int32 copies
+    groups: torch.Tensor | None = None
+    qsl: torch.Tensor | None = None
+    seqs: torch.Tensor | None = None
+
+    def host_parts(self) -> list:
+        """The arrays the kernels read, in upload() order (items, groups, qsl, seqs)."""
+        return [self.host_items, self.host_groups, np.asarray(self.host_qsl, np.int32),
+                np.asarray(self.host_seqs or [0], np.int32)]
+
+    def adopt(self, device_parts: list) -> "DecodePlan":
+        self.items, self.groups, self.qsl, self.seqs = device_parts
+        return self
 
 
 def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, group: int,
                 head_dim: int, device, target_items: int | None = None,
-                chunk_tokens: int = 8192, window: tuple = (0, 0)) -> DecodePlan:
+                chunk_tokens: int = 8192, window: tuple = (0, 0), upload_now: bool = True) -> DecodePlan:
     """Split-K plan (host): items of whole 32-token tiles, balanced over the CUs.
 
     window = (sink_tokens, recent_tokens) of the FP32 staging window, a balance hint
     (the expected window tiles go to items of their own); (0, 0) = no window.
+    upload_now=False leaves the device copies to the caller (one combined upload()).
     """
     lib = _lib.load()
     nreq = len(seqs)
     qa = (C.c_int32 * (nreq + 1))(*qsl)
     sa = (C.c_int32 * max(nreq, 1))(*seqs)
     if target_items is None:
-        target_items = torch.cuda.get_device_properties(device).multi_processor_count
+        target_items = cu_count(device)
     plan = _lib.Plan()
     sink, recent = (int(x) for x in window)
+    # one call with room for any plan the target allows (at most 3 ranges per group,
+    # at most 256 tiles per item); a second, exact call only if that was too small
+    ngroups = num_kv_heads * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+    guess = max(target_items, 1) + 3 * ngroups + sum(-(-s // 8192) for s in seqs) * num_kv_heads
+    items = np.zeros(max(guess, 1) * WORK_INTS, np.int32)
+    groups = np.zeros(max(ngroups, 1) * GROUP_INTS, np.int32)
+    i_ptr = items.ctypes.data_as(C.POINTER(C.c_int32))
+    g_ptr = groups.ctypes.data_as(C.POINTER(C.c_int32))
     n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
-                               chunk_tokens, target_items, sink, recent, None, 0, None, 0,
-                               C.byref(plan))
+                               chunk_tokens, target_items, sink, recent, i_ptr, guess,
+                               g_ptr, max(ngroups, 1), C.byref(plan))
+    if n == -28:
+        items = np.zeros(max(plan.num_items, 1) * WORK_INTS, np.int32)
+        i_ptr = items.ctypes.data_as(C.POINTER(C.c_int32))
+        n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
+                                   chunk_tokens, target_items, sink, recent, i_ptr, plan.num_items,
+                                   g_ptr, max(ngroups, 1), C.byref(plan))
     if n < 0:
         _lib.check(n, "oscar_attn_plan_v1")
-    items = (C.c_int32 * max(plan.num_items * WORK_INTS, 1))()
-    groups = (C.c_int32 * max(plan.num_groups * GROUP_INTS, 1))()
-    n = lib.oscar_attn_plan_v1(qa, sa, nreq, int(has_new), num_kv_heads, group, head_dim,
-                               chunk_tokens, target_items, sink, recent, items, plan.num_items,
-                               groups, plan.num_groups, C.byref(plan))
-    if n < 0:
-        _lib.check(n, "oscar_attn_plan_v1")
-    host_items = list(items)[: plan.num_items * WORK_INTS]
-    it = torch.tensor(host_items or [0], dtype=torch.int32).view(-1)
-    gr = torch.tensor(list(groups)[: plan.num_groups * GROUP_INTS] or [0], dtype=torch.int32)
-    return DecodePlan(it.to(device), gr.to(device),
-                      torch.tensor(qsl, dtype=torch.int32).to(device),
-                      torch.tensor(seqs or [0], dtype=torch.int32).to(device),
-                      plan.num_items, plan.num_groups, plan.partial_bytes, host_items,
-                      list(qsl), list(seqs), bool(has_new))
+    p = DecodePlan(items[: plan.num_items * WORK_INTS], groups[: plan.num_groups * GROUP_INTS],
+                   list(qsl), list(seqs), bool(has_new), plan.num_items, plan.num_groups,
+                   plan.partial_bytes, plan.max_group_items)
+    if upload_now:
+        p.adopt(upload(p.host_parts(), device))
+    return p
+
+
+_CU_COUNT: dict = {}
+
+
+def cu_count(device) -> int:
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _CU_COUNT:
+        _CU_COUNT[key] = torch.cuda.get_device_properties(key).multi_processor_count
+    return _CU_COUNT[key]
 
 
 def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None:
@@ -304,10 +367,12 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
         table = table.contiguous()
     if plan.has_new != (k_new is not None):
         raise ValueError("plan and call disagree on the presence of current K/V")
+    if plan.items is None:
+        raise ValueError("the decode plan has not been uploaded")
     _check_table(table, plan, k_cache.shape[1])
     scratch = DeviceScratch.get(dev)
     ws = scratch.attn_workspace(plan.partial_bytes)
-    st = staging_struct(stage)
+    st = staging_struct(stage, k_cache, head_dim)
     a = _lib.AttnArgs()
     a.q, a.num_tokens, a.num_q_heads, a.q_stride_token = q.data_ptr(), n, hq, q.stride(0)
     if k_new is not None:
@@ -320,7 +385,8 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     a.scale = float(scale)
     a.items, a.num_items = plan.items.data_ptr(), plan.num_items
     a.groups, a.num_groups = plan.groups.data_ptr(), plan.num_groups
-    a.workspace = ws.data_ptr()
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.max_group_items = plan.max_group_items
     a.out_rot, a.lse = out_rot.data_ptr(), lse.data_ptr()
     a.phases = int(phases)
     a.q_dtype = _DTYPES[q.dtype]
@@ -360,7 +426,7 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
             raise ValueError("Block table cannot cover the history")
         keep.append(row)
         a.block_table_row = row.data_ptr()
-        st = staging_struct(stage)
+        st = staging_struct(stage, k_cache, head_dim)
         if st is not None:
             keep.append(st)
             a.staging = C.pointer(st)

@@ -21,60 +21,67 @@ _SKIP_REASONS_LOGGED: set = set()
 
 
 def install_impl(impl, target_class):
-    """plugin.py:60-70: commit class surgery only if setup succeeds; restore otherwise."""
-    old_class, old_state = impl.__class__, impl.__dict__.copy()
+    """Move ``impl`` onto ``target_class`` and run its setup as one transaction: if setup
+    raises, the object gets its original class and attribute dict back and the error
+    propagates (the reference's rollback contract, plugin.py:60-70)."""
+    original_class, original_state = type(impl), dict(vars(impl))
+    impl.__class__ = target_class
     try:
-        impl.__class__ = target_class
         impl._oscar_setup()
-    except Exception:
-        impl.__class__ = old_class
-        impl.__dict__.clear()
-        impl.__dict__.update(old_state)
+    except BaseException:
+        impl.__class__ = original_class
+        vars(impl).clear()
+        vars(impl).update(original_state)
         raise
 
 
-def _is_hybrid_config(model_config) -> bool:
-    """plugin.py:202-214: registry flag, or any non-attention entry in layer_types."""
+def hybrid_model(model_config) -> bool:
+    """True for models that mix attention with other layer kinds: the registry's
+    ``is_hybrid`` flag, or a ``layer_types`` list naming anything but "attention"."""
     if getattr(model_config, "is_hybrid", False):
         return True
-    hf = getattr(model_config, "hf_text_config", None) or getattr(model_config, "hf_config", None)
-    layer_types = getattr(hf, "layer_types", None) or []
-    return any(lt != "attention" for lt in layer_types)
+    text_cfg = getattr(model_config, "hf_text_config", None) or getattr(model_config, "hf_config", None)
+    kinds = set(getattr(text_cfg, "layer_types", None) or ())
+    return bool(kinds - {"attention"})
+
+
+def _is_mtp_draft(layer_name: str) -> bool:
+    return layer_name.startswith("mtp.") or ".mtp." in layer_name
+
+
+def skip_reasons(layer, impl, model_config) -> list[str]:
+    """Why a layer keeps the native impl (empty list: OSCAR takes it).  OSCAR takes only
+    FULL decoder self-attention of hybrid models (plugin.py:220-253); MTP draft layers
+    keep bf16 KV, and are turned down before the model config is consulted."""
+    if _is_mtp_draft(getattr(layer, "layer_name", "") or ""):
+        return ["mtp-draft"]
+    reasons = [] if hybrid_model(model_config) else ["not-hybrid"]
+    kind = getattr(impl, "attn_type", "decoder")
+    if str(getattr(kind, "value", kind)) != "decoder":  # AttentionType is a str enum
+        reasons.append(f"attn_type={kind!r}")
+    for attr, label in (("sliding_window", "sliding-window"), ("sinks", "sinks")):
+        if getattr(impl, attr, None) is not None:
+            reasons.append(label)
+    return reasons
 
 
 def _should_oscar(layer, impl, model_config=None) -> bool:
-    """plugin.py:220-253: FULL decoder attention of a hybrid model, never an MTP draft."""
-    layer_name = getattr(layer, "layer_name", "") or ""
-    if ".mtp." in layer_name or layer_name.startswith("mtp."):
-        if "mtp-draft" not in _SKIP_REASONS_LOGGED:
-            _SKIP_REASONS_LOGGED.add("mtp-draft")
-            print(f"[oscar-amd][SKIP] {layer_name}: mtp-draft (draft KV stays bf16)")
-        return False
+    """skip_reasons() with the live vLLM model config; each distinct reason is logged once."""
+    name = getattr(layer, "layer_name", "") or ""
     try:
-        if model_config is None:
+        if model_config is None and not _is_mtp_draft(name):
             from vllm.config import get_current_vllm_config
 
             model_config = get_current_vllm_config().model_config
-        reasons = []
-        if not _is_hybrid_config(model_config):
-            reasons.append("not-hybrid")
-        at = getattr(impl, "attn_type", "decoder")
-        if str(getattr(at, "value", at)) != "decoder":
-            reasons.append(f"attn_type={at!r}")
-        if getattr(impl, "sliding_window", None) is not None:
-            reasons.append("sliding-window")
-        if getattr(impl, "sinks", None) is not None:
-            reasons.append("sinks")
-        if reasons:
-            key = ",".join(reasons)
-            if key not in _SKIP_REASONS_LOGGED:
-                _SKIP_REASONS_LOGGED.add(key)
-                print(f"[oscar-amd][SKIP] {layer_name}: {key}")
-            return False
-        return True
-    except Exception as e:  # pragma: no cover - reported, layer stays native
-        print(f"[oscar-amd][SKIP] _should_oscar failed: {e}")
-        return False
+        reasons = skip_reasons(layer, impl, model_config)
+    except Exception as e:  # pragma: no cover - reported, the layer stays native
+        reasons = [f"routing check failed: {e}"]
+    if reasons:
+        key = ",".join(reasons)
+        if key not in _SKIP_REASONS_LOGGED:
+            _SKIP_REASONS_LOGGED.add(key)
+            print(f"[oscar-amd][SKIP] {name or '?'}: {key}")
+    return not reasons
 
 
 def _patch_attention_class(attention_cls, target_class=None) -> None:

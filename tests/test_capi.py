@@ -142,6 +142,7 @@ def check_plan(lib, qsl, seqs, has_new, hk, group, window, target, d):
             np.add.at(cover, item_tiles(it), 1)
         assert (cover == 1).all()
     assert len(groups) == ngroups
+    assert p.max_group_items == groups[:, 3].max()
 
 
 @pytest.mark.parametrize("seed", range(8))
@@ -277,3 +278,31 @@ def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(
     s = _lib.StoreArgs(num_tokens=0)
     assert lib.oscar_store_v1(C.byref(s), None) == 0
     assert lib.oscar_store_workspace_bytes_v1(10, 2, 256) == 2 * 10 * 2 * 256 * 4
+
+
+def decode_args(**kw):
+    """Decode arguments that pass every host check before the launch (placeholder
+    device addresses; the calls below are rejected before anything is launched)."""
+    a = _lib.AttnArgs(q=0x10000, num_tokens=4, num_q_heads=6, q_stride_token=1536,
+                      block_table=0x20000, block_table_stride=16, query_start_loc=0x30000,
+                      seq_lens=0x40000, num_reqs=1, scale=0.0625, items=0x50000, num_items=4,
+                      groups=0x60000, num_groups=1, workspace=0x70000, out_rot=0x80000,
+                      lse=0x90000, q_dtype=_lib.OSCAR_BF16)
+    a.cache.k, a.cache.v = 0x100000, 0x200000
+    a.cache.num_blocks, a.cache.block_size, a.cache.num_kv_heads, a.cache.head_dim = 8, 128, 1, 256
+    for i, st in enumerate((128 * 256, 256, 256)):
+        a.cache.k_stride[i] = a.cache.v_stride[i] = st
+    a.workspace_bytes = 4 * 32 * 257 * 4
+    a.max_group_items = 4
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_decode_rejects_a_workspace_smaller_than_the_plan_needs(lib):
+    a = decode_args(workspace_bytes=4 * 32 * 257 * 4 - 16)
+    assert lib.oscar_attn_decode_v1(C.byref(a), None) == -22
+    assert b"workspace" in lib.oscar_last_error()
+    a = decode_args(max_group_items=5)
+    assert lib.oscar_attn_decode_v1(C.byref(a), None) == -22
+    assert b"max_group_items" in lib.oscar_last_error()

@@ -143,6 +143,49 @@ def test_decode_random_batches_match_oracle(cuda, seed):
     check(out, lse, ref_out, ref_lse, label)
 
 
+@pytest.mark.parametrize("gain", [1e3, 1e4], ids=["v1e3", "v1e4"])
+def test_decode_large_value_scales(cuda, gain):
+    """V magnitudes of 1e3 and 1e4 (per-token V scales far above 256): the reference's
+    rounding fp16(x) -> bf16 stays finite up to |V| = 65504, so the output must too.
+    The absolute tolerance scales with the value magnitude (2e-2 per unit of V)."""
+    c = cases.make_case([3000, 700, 129], [4, 1, 3], v_gain=gain)
+    out, lse, _ = run_decode(c, target=16)
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"])
+    assert np.isfinite(out).all(), "non-finite output"
+    err_o = np.abs(out - ref_out).max()
+    err_l = np.abs(lse - ref_lse).max()
+    print(f"V x {gain:g}: max|dO|={err_o:.3e} (max|V| {np.abs(c['v']).max():.0f}) "
+          f"max|dLSE|={err_l:.3e}", flush=True)
+    assert err_o <= OUT_TOL * gain
+    assert err_l <= LSE_TOL
+
+
+def test_decode_nan_propagates_through_merge(cuda):
+    """A NaN in one staged window value: the rows of that request that see the token are
+    NaN (out and LSE) after the split-K merge; every other request is unaffected
+    (slab_attention.py:341-356: NaN propagates)."""
+    c = cases.make_case([2000, 1500, 300], [4, 2, 1])
+    sk, sv, owner = c["stage"]
+    # request 1's first position is a staged sink token
+    blk = int(c["bt"][1, 0])
+    row = blk % owner.shape[0]
+    assert owner[row, 0] == blk
+    sk[row, 0, 0, 7] = np.nan
+    out, lse, _ = run_decode(c, target=64)
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"])
+    nan_rows = np.isnan(ref_lse)
+    assert nan_rows[4:6].all() and not nan_rows[:4].any() and not nan_rows[6:].any()
+    assert np.array_equal(np.isnan(lse), nan_rows), "NaN LSE rows differ"
+    assert np.isnan(out[nan_rows]).all(), "NaN rows not NaN in the output"
+    ok = ~nan_rows
+    err_o = np.abs(out[ok] - ref_out[ok]).max()
+    err_l = np.abs(lse[ok] - ref_lse[ok]).max()
+    print(f"nan case: other rows max|dO|={err_o:.3e} max|dLSE|={err_l:.3e}", flush=True)
+    assert err_o <= OUT_TOL and err_l <= LSE_TOL
+
+
 def test_decode_plan_covers_each_history_token_once(cuda):
     c = cases.make_case([24579] * 8, [4] * 8)
     from oscar_amd import ops

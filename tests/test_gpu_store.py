@@ -114,16 +114,21 @@ def test_store_prerotated_reference_sgemm_bits(cuda):
     assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
 
 
-def test_store_clip_bit_exact(cuda):
-    d, n, bs, nb = 256, 300, 128, 4
-    k = cases.kv_outliers(n, 1, d, 21)
-    v = cases.kv_outliers(n, 1, d, 22)
-    rk, rv = cases.hadamard_rotation(d, 23), cases.hadamard_rotation(d, 24)
+# the serve defaults 0.96 / 0.92 (delivery/serve_oscar.sh:32-33): calls of <= 64 tokens
+# take the one-launch path (clip on the vector handed over by the last column slice),
+# 300 tokens the two-launch path
+@pytest.mark.parametrize("n", [4, 23, 64, 300])
+@pytest.mark.parametrize("d,hk", [(256, 1), (256, 2), (128, 1)])
+def test_store_clip_bit_exact(cuda, d, hk, n):
+    bs, nb = 128, 4
+    k = cases.kv_outliers(n, hk, d, 21)
+    v = cases.kv_outliers(n, hk, d, 22)
+    rk, rv = cases.hadamard_rotation(d, 23), cases.qr_rotation(d, 24)
     slots = slot_mapping(n, nb * bs, 25)
-    k8, v8 = cases.empty_caches(nb, bs, 1, d)
+    k8, v8 = cases.empty_caches(nb, bs, hk, d)
     got_k, got_v = run_store(k, v, (k8, v8), slots, d, rk, rv, k_clip=0.96, v_clip=0.92)
     store_ref(clip(rotate(k, rk), 0.96), clip(rotate(v, rv), 0.92), k8, v8, slots)
-    assert np.array_equal(got_k, k8)
+    assert np.array_equal(got_k, k8), f"K bytes differ at {np.argwhere(got_k != k8)[:5]}"
     assert np.array_equal(got_v, v8)
 
 

@@ -105,7 +105,7 @@ def test_rotation_checkpoint_layouts(tmp_path):
     with pytest.raises(ValueError, match="orthogonal"):
         rotation.get_layer_rotation(str(bad), "model.layers.3.attn", 64, "cpu", strict=True)
     torch.save({3: torch.eye(32)}, bad)
-    rotation._load_checkpoint.cache_clear()
+    rotation.load_rotation_table.cache_clear()
     with pytest.raises(ValueError, match="shape"):
         rotation.get_layer_rotation(str(bad), "model.layers.3.attn", 64, "cpu")
 
@@ -119,8 +119,8 @@ def test_layer_index_parsing():
 def test_should_oscar_routes_only_full_decoder_layers_of_hybrid_models():
     hybrid = NS(is_hybrid=False, hf_text_config=NS(layer_types=["linear_attention", "full_attention"]))
     dense = NS(is_hybrid=False, hf_text_config=NS(layer_types=["attention", "attention"]))
-    assert plugin._is_hybrid_config(hybrid) and not plugin._is_hybrid_config(dense)
-    assert plugin._is_hybrid_config(NS(is_hybrid=True))
+    assert plugin.hybrid_model(hybrid) and not plugin.hybrid_model(dense)
+    assert plugin.hybrid_model(NS(is_hybrid=True))
     impl = NS(attn_type="decoder", sliding_window=None, sinks=None)
     full = NS(layer_name="model.layers.3.self_attn.attn")
     assert plugin._should_oscar(full, impl, hybrid)
