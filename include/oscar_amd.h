@@ -213,6 +213,21 @@ typedef struct oscar_attn_args_v1 {
 
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
 
+/* oscar_attn_decode_v1 that allocates nothing and takes no workspace: the item
+ * partials live in a library-owned static device array of
+ * OSCAR_DECODE_STATIC_MAX_ITEMS * 32 * 257 * 4 bytes (16.8 MB, held on every device
+ * the library runs on until the process ends).  No counterpart in the reference: it
+ * is for callers that cannot allocate (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  args->workspace / workspace_bytes are ignored; a plan of
+ * more than OSCAR_DECODE_STATIC_MAX_ITEMS items is rejected (-22).  The stream must
+ * belong to the current device.  Every call on a device shares that device's array
+ * (the split-K pass writes every partial the merge reads, so nothing needs clearing):
+ * calls that overlap on one device race, and phases 1 then 2 must not be separated
+ * by another call on the device.  The first call on a device looks up the array's
+ * address (hipGetSymbolAddress); make it outside graph capture. */
+#define OSCAR_DECODE_STATIC_MAX_ITEMS 512
+int oscar_attn_decode_static_v1(const oscar_attn_args_v1* args, void* stream);
+
 typedef struct oscar_prefill_args_v1 {
   const void* q;                /* [n, Hq, D] in q_dtype */
   int64_t q_stride_token;

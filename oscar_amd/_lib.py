@@ -16,6 +16,7 @@ STAGE_NONE, STAGE_INVALIDATE, STAGE_WRITE = 0, 1, 2
 WORK_INTS = 8
 GROUP_INTS = 8
 ABI_VERSION = 2
+DECODE_STATIC_MAX_ITEMS = 512
 
 vp = C.c_void_p
 i32, i64, f32 = C.c_int32, C.c_int64, C.c_float
@@ -93,6 +94,7 @@ SIGNATURES = {
                                      i32, i32, i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
                                      C.POINTER(Plan)]),
     "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "oscar_attn_decode_static_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),
     "oscar_attn_prefill_v1": (C.c_int, [C.POINTER(PrefillArgs), vp]),
 }

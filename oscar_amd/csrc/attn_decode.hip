@@ -48,6 +48,7 @@
 // values in LDS (rounded as the reference does), and one wave adds the tile to its
 // softmax state with P split into bf16 hi + lo parts while the next tile's loads
 // are in flight.
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -1258,48 +1259,105 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
   return (int)nitems;
 }
 
-extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream) {
-  if (!args) return fail(-22, "oscar_attn_decode_v1: null args");
-  const oscar_attn_args_v1& a = *args;
+namespace {
+
+// Argument checks shared by both decode entry points; `name` prefixes the messages.
+// `partials` / `partial_bytes`: where the item partials go and how much room there is.
+int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials, int64_t partial_bytes,
+                   hipStream_t s) {
   const int64_t D = a.cache.head_dim;
-  if (D != 128 && D != 256) return fail(-22, "oscar_attn_decode_v1: head_dim %lld unsupported", (long long)D);
+  if (D != 128 && D != 256) return fail(-22, "%s: head_dim %lld unsupported", name, (long long)D);
   if (a.num_items <= 0 || a.num_groups <= 0) return 0;
-  if (!a.q || !a.items || !a.groups || !a.workspace || !a.out_rot || !a.lse || !a.block_table ||
+  if (!a.q || !a.items || !a.groups || !partials || !a.out_rot || !a.lse || !a.block_table ||
       !a.query_start_loc || !a.seq_lens)
-    return fail(-22, "oscar_attn_decode_v1: missing pointer");
+    return fail(-22, "%s: missing pointer", name);
   if ((a.k_new == nullptr) != (a.v_new == nullptr))
-    return fail(-22, "oscar_attn_decode_v1: both new K and V must be supplied together");
-  if (a.phases < 0 || a.phases > 2) return fail(-22, "oscar_attn_decode_v1: phases must be 0, 1 or 2");
+    return fail(-22, "%s: both new K and V must be supplied together", name);
+  if (a.phases < 0 || a.phases > 2) return fail(-22, "%s: phases must be 0, 1 or 2", name);
   if (a.q_dtype != OSCAR_BF16 && a.q_dtype != OSCAR_F16)
-    return fail(-22, "oscar_attn_decode_v1: q_dtype must be OSCAR_BF16 or OSCAR_F16");
+    return fail(-22, "%s: q_dtype must be OSCAR_BF16 or OSCAR_F16", name);
   if (a.cache.num_kv_heads < 1 || a.num_q_heads % a.cache.num_kv_heads)
-    return fail(-22, "oscar_attn_decode_v1: Hq must be a multiple of Hk");
+    return fail(-22, "%s: Hq must be a multiple of Hk", name);
   if ((a.cache.k_stride[2] & 15) || (a.cache.v_stride[2] & 15) || (a.cache.k_stride[1] & 15) ||
       (a.cache.v_stride[1] & 15) || (a.cache.k_stride[0] & 15) || (a.cache.v_stride[0] & 15) ||
       (((uintptr_t)a.cache.k) & 15) || (((uintptr_t)a.cache.v) & 15))
-    return fail(-22, "oscar_attn_decode_v1: cache slots must be 16-byte aligned");
+    return fail(-22, "%s: cache slots must be 16-byte aligned", name);
   // queries and the current chunk are read as 16-byte vectors
   if ((a.q_stride_token & 7) || (((uintptr_t)a.q) & 15) ||
       (a.k_new && ((a.kv_new_stride_token & 7) || (((uintptr_t)a.k_new) & 15) || (((uintptr_t)a.v_new) & 15))))
-    return fail(-22, "oscar_attn_decode_v1: q / k_new / v_new rows must be 16-byte aligned");
+    return fail(-22, "%s: q / k_new / v_new rows must be 16-byte aligned", name);
   if (a.cache.block_size < kTile || a.cache.block_size % kTile || a.cache.block_size > (1 << 20))
-    return fail(-22, "oscar_attn_decode_v1: block_size %lld must be a multiple of %d (<= 2^20)",
+    return fail(-22, "%s: block_size %lld must be a multiple of %d (<= 2^20)", name,
                 (long long)a.cache.block_size, kTile);
   if (a.staging && (a.staging->rows < 1 || a.staging->rows * a.cache.block_size >= (1ll << 31) ||
                     (((uintptr_t)a.staging->stage_k) & 15) || (((uintptr_t)a.staging->stage_v) & 15)))
-    return fail(-22, "oscar_attn_decode_v1: staging arena rows out of range or unaligned");
-  if (a.workspace_bytes < (int64_t)a.num_items * 32 * (D + 1) * (int64_t)sizeof(float))
-    return fail(-22, "oscar_attn_decode_v1: workspace of %lld bytes < %lld for %d items",
-                (long long)a.workspace_bytes, (long long)a.num_items * 32 * (D + 1) * 4, a.num_items);
+    return fail(-22, "%s: staging arena rows out of range or unaligned", name);
+  const int64_t need = (int64_t)a.num_items * 32 * (D + 1) * (int64_t)sizeof(float);
+  if (partial_bytes < need)
+    return fail(-22, "%s: workspace of %lld bytes < %lld for %d items", name, (long long)partial_bytes,
+                (long long)need, a.num_items);
   if (a.max_group_items < 0 || a.max_group_items > a.num_items)
-    return fail(-22, "oscar_attn_decode_v1: max_group_items out of range");
+    return fail(-22, "%s: max_group_items out of range", name);
   AttnParams p{};
   p.a = a;
   p.has_stage = a.staging != nullptr;
   if (a.staging) p.st = *a.staging;
   p.group = (int)(a.num_q_heads / a.cache.num_kv_heads);
-  p.part_o = (float*)a.workspace;
+  p.part_o = (float*)partials;
   p.part_lse = p.part_o + (int64_t)a.num_items * 32 * D;
-  hipStream_t s = (hipStream_t)stream;
   return D == 256 ? launch_decode<256>(p, s) : launch_decode<128>(p, s);
+}
+
+// ---- the entry point that allocates nothing: item partials in a file-scope device
+// array.  Each device holds its own copy at its own address; host code must use the
+// address hipGetSymbolAddress returns for the device (the array's name is a host-side
+// stand-in), looked up once per device on the first call there.
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[OSCAR_DECODE_STATIC_MAX_ITEMS * 32 * (256 + 1) * sizeof(float)];
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int static_partials(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(-5, "oscar_attn_decode_static_v1: no current device");
+  if (s != nullptr) {
+    int sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess)
+      return fail(-22, "oscar_attn_decode_static_v1: cannot query the stream's device");
+    if (sdev != dev)
+      return fail(-22, "oscar_attn_decode_static_v1: the stream belongs to device %d, the current device is %d",
+                  sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(-22, "oscar_attn_decode_static_v1: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(-5, "oscar_attn_decode_static_v1: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream) {
+  if (!args) return fail(-22, "oscar_attn_decode_v1: null args");
+  return launch_checked(*args, "oscar_attn_decode_v1", args->workspace, args->workspace_bytes,
+                        (hipStream_t)stream);
+}
+
+extern "C" int oscar_attn_decode_static_v1(const oscar_attn_args_v1* args, void* stream) {
+  if (!args) return fail(-22, "oscar_attn_decode_static_v1: null args");
+  if (args->num_items > OSCAR_DECODE_STATIC_MAX_ITEMS)
+    return fail(-22, "oscar_attn_decode_static_v1: %d items exceed the static scratch (at most %d)",
+                args->num_items, OSCAR_DECODE_STATIC_MAX_ITEMS);
+  if (args->num_items <= 0 || args->num_groups <= 0) return 0;
+  void* partials = nullptr;
+  const int rc = static_partials((hipStream_t)stream, &partials);
+  if (rc != 0) return rc;
+  return launch_checked(*args, "oscar_attn_decode_static_v1", partials, (int64_t)sizeof(scratch),
+                        (hipStream_t)stream);
 }

@@ -339,10 +339,12 @@ def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None
 
 
 def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: DecodePlan, scale,
-                     stage=None, *, head_dim, out_rot=None, lse=None, phases=0):
+                     stage=None, *, head_dim, out_rot=None, lse=None, phases=0, static_scratch=False):
     """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32).
 
-    q (and k_new / v_new) are bf16 or fp16; history values are rounded q_dtype(fp16(x))."""
+    q (and k_new / v_new) are bf16 or fp16; history values are rounded q_dtype(fp16(x)).
+    static_scratch: call oscar_attn_decode_static_v1 (item partials in the library's
+    static device array, no workspace)."""
     _require_cuda(q, k_cache, v_cache, block_table)
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("OSCAR HIP attention requires bf16 or fp16 queries")
@@ -370,8 +372,6 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     if plan.items is None:
         raise ValueError("the decode plan has not been uploaded")
     _check_table(table, plan, k_cache.shape[1])
-    scratch = DeviceScratch.get(dev)
-    ws = scratch.attn_workspace(plan.partial_bytes)
     st = staging_struct(stage, k_cache, head_dim)
     a = _lib.AttnArgs()
     a.q, a.num_tokens, a.num_q_heads, a.q_stride_token = q.data_ptr(), n, hq, q.stride(0)
@@ -385,13 +385,16 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     a.scale = float(scale)
     a.items, a.num_items = plan.items.data_ptr(), plan.num_items
     a.groups, a.num_groups = plan.groups.data_ptr(), plan.num_groups
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    if not static_scratch:
+        ws = DeviceScratch.get(dev).attn_workspace(plan.partial_bytes)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.max_group_items = plan.max_group_items
     a.out_rot, a.lse = out_rot.data_ptr(), lse.data_ptr()
     a.phases = int(phases)
     a.q_dtype = _DTYPES[q.dtype]
     lib = _lib.load()
-    _lib.check(lib.oscar_attn_decode_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_attn_decode_v1")
+    entry = "oscar_attn_decode_static_v1" if static_scratch else "oscar_attn_decode_v1"
+    _lib.check(getattr(lib, entry)(C.byref(a), C.c_void_p(_stream(dev))), entry)
     return out_rot, lse
 
 

@@ -34,7 +34,7 @@ def header_functions() -> set:
 
 def test_library_exports_every_header_symbol(lib):
     names = header_functions()
-    assert len(names) == 9, names
+    assert len(names) == 10, names
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES)
@@ -267,6 +267,7 @@ def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(
     assert b"null" in lib.oscar_last_error()
     assert lib.oscar_rotate_v1(None, None) == -22
     assert lib.oscar_attn_decode_v1(None, None) == -22
+    assert lib.oscar_attn_decode_static_v1(None, None) == -22
     assert lib.oscar_attn_prefill_v1(None, None) == -22
     r = _lib.RotateArgs(rows=4, head_dim=96, x=1, r=1, out=1)
     assert lib.oscar_rotate_v1(C.byref(r), None) == -22 and b"head_dim" in lib.oscar_last_error()
@@ -306,3 +307,10 @@ def test_decode_rejects_a_workspace_smaller_than_the_plan_needs(lib):
     a = decode_args(max_group_items=5)
     assert lib.oscar_attn_decode_v1(C.byref(a), None) == -22
     assert b"max_group_items" in lib.oscar_last_error()
+
+
+def test_static_decode_rejects_plans_beyond_its_scratch(lib):
+    a = decode_args(num_items=_lib.DECODE_STATIC_MAX_ITEMS + 1,
+                    max_group_items=_lib.DECODE_STATIC_MAX_ITEMS + 1)
+    assert lib.oscar_attn_decode_static_v1(C.byref(a), None) == -22
+    assert b"static scratch" in lib.oscar_last_error()
