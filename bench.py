@@ -148,9 +148,11 @@ class Setup:
         self.out_rot = torch.zeros(B * n, hq, d, dtype=torch.float32, device=dev)
         self.lse = torch.zeros(B * n, hq, dtype=torch.float32, device=dev)
         self.out = torch.empty(B * n, hq, d, dtype=torch.bfloat16, device=dev)
-        self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=has_new, num_kv_heads=hk,
-                                    group=hq // hk, head_dim=d, device=dev,
-                                    window=(self.sink_eff, c["recent_tokens"]))
+        self.plan = None
+        if n * (hq // hk) <= 32:  # decode-shaped: the split-K plan of the benchmarked step
+            self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=has_new, num_kv_heads=hk,
+                                        group=hq // hk, head_dim=d, device=dev,
+                                        window=(self.sink_eff, c["recent_tokens"]))
 
     def step(self, layer, phases=0):
         from oscar_amd import ops
@@ -413,7 +415,96 @@ def config_prefill(dev, reps=5, layers=2):
                          "algorithmic_flops": flops}}
 
 
-def cpu_baseline(setup, budget_s=25.0, max_cores=16):
+class _Layer:
+    layer_name = "model.layers.0.self_attn.attn"
+
+
+class _Meta:
+    pass
+
+
+def forward_call(setup, layer_idx=0):
+    """The plugin impl's forward over one of setup's layers, as vLLM calls it: metadata
+    with host query starts / sequence lengths, the new tokens' slots and the block table."""
+    from oscar_amd.backend import OscarAttentionBackendImpl
+
+    c = CONFIG
+    d, hq, hk = c["d"], c["hq"], c["hk"]
+    impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
+    impl.head_size, impl.num_heads, impl.num_kv_heads, impl.scale = d, hq, hk, setup.scale
+    impl.key_cache = impl.value_cache = None
+    os.environ.setdefault("OSCAR_ASCEND_VERBOSE", "0")
+    impl._oscar_setup()
+    kc, vc, (sk, sv, own) = setup.layers[layer_idx]
+    layer = _Layer()
+    layer._oscar_rots = (setup.rk, setup.rv)
+    impl._set_caches((kc, vc))
+    # the layer's window arena as bench's history writes left it
+    layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner = sk, sv, own
+    layer._oscar_stage_rows = own.shape[0]
+    layer._oscar_stage_ready = impl._oscar_stage_ready = True
+    impl.stage_block = c["block_size"]
+    impl.sink_eff = setup.sink_eff
+    md = _Meta()
+    md.num_actual_tokens = setup.q.shape[0]
+    md.slot_mapping = setup.slots
+    md.query_start_loc_cpu = torch.tensor(setup.qsl, dtype=torch.int32)
+    md.seq_lens_list = list(setup.seqs)
+    md.block_tables = setup.bt
+    q = setup.q.view(setup.q.shape[0], -1)
+    k = setup.k_new.view(setup.k_new.shape[0], -1)
+    v = setup.v_new.view(setup.v_new.shape[0], -1)
+    out = torch.empty_like(q)
+    return lambda: impl.forward(layer, q, k, v, (kc, vc), md, output=out)
+
+
+def compare_calls_ms(fn, repeats=6):
+    """delivery/benchmark_utils.py:9-70 for one variant: device-synchronised calls, the
+    first call reported apart (first-use work), then `repeats` warm samples; median."""
+    def measure():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    first = measure()
+    warm = [measure() for _ in range(repeats)]
+    return {"first_call_ms": first, "median_ms": float(np.median(warm)), "samples_ms": warm}
+
+
+# tools/benchmark_streaming.py:16-20: (name, requests, prefix, query tokens)
+FORWARD_CASES = (("mtp", 1, 24579, 4), ("concurrent", 8, 24579, 4), ("prefill", 1, 15360, 9256))
+
+
+def forward_timings(dev):
+    """impl.forward per call at the reference's three bench cases (its scope: one layer's
+    full forward incl. write, window and rotations), host-timed around device syncs."""
+    res = {}
+    for name, batch, prefix, count in FORWARD_CASES:
+        setup = Setup(dev, [prefix] * batch, count, True, layers=1, seed=20261210)
+        call = forward_call(setup)
+        res[name] = compare_calls_ms(call)
+        log(f"forward {name}: first {res[name]['first_call_ms']:.3f} ms, warm median "
+            f"{res[name]['median_ms'] * 1e3:.1f} us")
+        del setup, call
+        torch.cuda.empty_cache()
+    return res
+
+
+def copy_ceiling_gbs(dev, mib=1024):
+    """Device-to-device copy rate (read + write bytes / time) of a 1 GiB buffer."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = event_ms(lambda r: dst.copy_(src), reps=5, warm=1)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * (mib << 20) / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(setup, budget_s=25.0, max_cores=16, cores=None):
     """The NumPy oracle of the same layer step (write 32 tokens + window, attention over
     8 x 24580 keys, inverse rotation) on this host: the first call is excluded, then
     warm samples until about budget_s of CPU work (at least 3), median reported."""
@@ -422,8 +513,9 @@ def cpu_baseline(setup, budget_s=25.0, max_cores=16):
     from oracle import backend as ob
     from oracle.store import Staging
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = min(cores, max_cores)  # the one-GPU share of the host
+    if cores is None:
+        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+        cores = min(cores, max_cores)  # the one-GPU share of the host
     c = CONFIG
     kc, vc, (sk, sv, owner) = setup.layers[1]
     layer = ob.OracleLayer(k8=kc.view(torch.uint8).cpu().numpy(), v8=vc.view(torch.uint8).cpu().numpy(),
@@ -551,6 +643,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=320)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-forward", action="store_true", help="skip the impl.forward timings")
     ap.add_argument("--config", default="4a", choices=["4a", "2", "3", "4b", "5"],
                     help="4a (default, the headline metric); 2 store; 3 single-request MTP; "
                          "4b 64 cache-only decodes; 5 continuation prefill")
@@ -622,6 +715,9 @@ def main(argv=None):
     achieved = b_main / (med_ms * 1e-3) / 1e9
     c = CONFIG
     kv_tokens = sum(setup.seqs)
+    traffic = measured_traffic()
+    ceiling = copy_ceiling_gbs(dev)
+    log(f"device copy ceiling {ceiling:.0f} GB/s")
     rec = {
         "metric": "INT2-KV attention tokens/s + HBM GB/s (% peak), 8x24K MTP, one MI355X",
         "value": kv_tokens / (ms_step * 1e-3),
@@ -644,11 +740,24 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "kernel": "attn_main_kernel<256>", "achieved": achieved,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "algorithmic_bytes": b_main, "kernel_us": med_ms * 1e3,
-                     "traffic": measured_traffic()},
+                     "traffic": traffic,
+                     "traffic_source": "from profile: " + str(TRAFFIC_FILE.relative_to(TRAFFIC_FILE.parents[1]))
+                                       + " (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)",
+                     "physical_gbs": None if traffic is None else traffic / (med_ms * 1e-3) / 1e9,
+                     "copy_ceiling_gbs": ceiling},
+        "ms_per_step_replays": extra,
     }
+    if not args.no_forward:
+        log("impl.forward per call at the reference's bench cases")
+        fw = forward_timings(dev)
+        rec["forward_us"] = {k: v["median_ms"] * 1e3 for k, v in fw.items()}
+        rec["forward_first_call_ms"] = {k: v["first_call_ms"] for k, v in fw.items()}
     if not args.no_cpu:
         log("cpu baseline (NumPy oracle, one layer step)")
         rec["cpu_baseline"] = cpu_baseline(setup)
+        log("cpu baseline at 2 threads (the reference tools' setting)")
+        two = cpu_baseline(setup, budget_s=12.0, cores=2)
+        rec["cpu_baseline_2threads"] = {k: two[k] for k in ("value", "unit", "cores", "kind")}
     print(json.dumps(rec), flush=True)
     return 0
 

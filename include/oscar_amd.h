@@ -257,6 +257,71 @@ typedef struct oscar_prefill_args_v1 {
 int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim);
 int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream);
 
+/* ---- native decode step ------------------------------------------------------
+ * One call per decode-shaped forward of the impl (backend.py:249-393 for batches whose
+ * requests all have history and <= 32 rows per KV head: decode, MTP verification,
+ * cache-only decode).  The call classifies the batch from the host metadata, builds
+ * the split-K plan on the host, stages every integer array the kernels read through
+ * the context's pinned ring in ONE host-to-device copy, and enqueues the store (or the
+ * query rotation when there are no new tokens), the split-K decode and merge, and the
+ * inverse rotation into `output` -- with no Python in between.  It returns
+ * OSCAR_STEP_NOT_DECODE (nothing enqueued) when a request is history-free, longer than
+ * 32 rows, or the requests do not tile [0, num_tokens): the caller then takes the
+ * general path.
+ *
+ * The context holds a ring of pinned host and device metadata slots, reused once the
+ * event recorded after the slot's last reader has completed; one per device, created
+ * once (it allocates), used from any thread. */
+typedef struct oscar_context_v1 oscar_context_v1;
+int oscar_context_create_v1(int32_t device, oscar_context_v1** ctx);
+int oscar_context_destroy_v1(oscar_context_v1* ctx);
+
+#define OSCAR_STEP_NOT_DECODE 1
+
+typedef struct oscar_step_args_v1 {
+  const void* query;            /* [num_tokens, Hq, D] rows in q_dtype, token stride Hq * D */
+  const void* key;              /* [num_tokens, Hk, D] or NULL (cache-only: no write) */
+  const void* value;
+  int64_t kv_stride_token;      /* elements */
+  int64_t num_tokens;           /* num_actual_tokens */
+  int64_t num_q_heads;
+  int32_t q_dtype;              /* OSCAR_BF16 or OSCAR_F16 (key / value / output too) */
+  int32_t stage_mode;           /* enum oscar_stage_mode, used when key != NULL */
+  const int64_t* slot_mapping;  /* device [num_tokens] (key != NULL) */
+  oscar_cache_v1 cache;
+  const int32_t* block_table;   /* device [num_reqs, max_blocks] */
+  int64_t block_table_stride;
+  const oscar_staging_v1* staging; /* NULL: no FP32 window */
+  int32_t sink_tokens_eff;
+  int32_t recent_tokens;
+  const float* rk;              /* [D, D] fp32, required */
+  const float* rv;
+  float k_clip_ratio;
+  float v_clip_ratio;
+  float scale;
+  int32_t target_items;         /* split-K items (0: one per compute unit) */
+  const int32_t* host_query_start_loc; /* host [num_reqs + 1] */
+  const int32_t* host_seq_lens;        /* host [num_reqs] */
+  int32_t num_reqs;
+  int32_t reserved;
+  void* output;                 /* [num_tokens, Hq, D] in q_dtype, token stride Hq * D */
+  /* store scratch, as in oscar_store_args_v1 */
+  int64_t* slot_claims;
+  int64_t* seat_claims;
+  int64_t* epoch_counter;
+  void* store_workspace;
+  int64_t store_workspace_bytes;
+  uint32_t* arrivals;
+  /* step workspace (rotated q / k / v, out_rot, lse, item partials), 256-byte aligned */
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t workspace_needed;     /* out: bytes this call needed (set when it returns -28) */
+} oscar_step_args_v1;
+
+int64_t oscar_step_workspace_bytes_v1(int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                                      int64_t head_dim, int64_t num_items);
+int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* args, void* stream);
+
 const char* oscar_last_error(void);
 int oscar_abi_version(void);
 

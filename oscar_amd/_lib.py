@@ -83,6 +83,23 @@ class PrefillArgs(C.Structure):
     ]
 
 
+class StepArgs(C.Structure):
+    _fields_ = [
+        ("query", vp), ("key", vp), ("value", vp), ("kv_stride_token", i64),
+        ("num_tokens", i64), ("num_q_heads", i64), ("q_dtype", i32), ("stage_mode", i32),
+        ("slot_mapping", vp), ("cache", Cache), ("block_table", vp), ("block_table_stride", i64),
+        ("staging", C.POINTER(Staging)), ("sink_tokens_eff", i32), ("recent_tokens", i32),
+        ("rk", vp), ("rv", vp), ("k_clip_ratio", f32), ("v_clip_ratio", f32), ("scale", f32),
+        ("target_items", i32), ("host_query_start_loc", vp), ("host_seq_lens", vp),
+        ("num_reqs", i32), ("reserved", i32), ("output", vp),
+        ("slot_claims", vp), ("seat_claims", vp), ("epoch_counter", vp),
+        ("store_workspace", vp), ("store_workspace_bytes", i64), ("arrivals", vp),
+        ("workspace", vp), ("workspace_bytes", i64), ("workspace_needed", i64),
+    ]
+
+
+STEP_NOT_DECODE = 1
+
 # name -> (restype, argtypes); every symbol declared in include/oscar_amd.h
 SIGNATURES = {
     "oscar_abi_version": (C.c_int, []),
@@ -97,6 +114,10 @@ SIGNATURES = {
     "oscar_attn_decode_static_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),
     "oscar_attn_prefill_v1": (C.c_int, [C.POINTER(PrefillArgs), vp]),
+    "oscar_context_create_v1": (C.c_int, [i32, C.POINTER(vp)]),
+    "oscar_context_destroy_v1": (C.c_int, [vp]),
+    "oscar_step_workspace_bytes_v1": (i64, [i64, i64, i64, i64, i64]),
+    "oscar_decode_step_v1": (C.c_int, [vp, C.POINTER(StepArgs), vp]),
 }
 
 _LIB = None

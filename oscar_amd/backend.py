@@ -20,6 +20,7 @@ CPU fallback: failures raise.
 """
 from __future__ import annotations
 
+from ctypes import pointer as ctypes_pointer
 from dataclasses import dataclass, field
 from importlib import import_module, util
 
@@ -69,6 +70,39 @@ def metadata_batch_lists(attn_metadata) -> tuple[list, list]:
 def _block_tables(md):
     bt = getattr(md, "block_tables", None)
     return bt if bt is not None else md.block_table
+
+
+def _host_int32(value):
+    """A host int32 array for the native step (zero-copy for a contiguous CPU int32
+    tensor); None when the value lives on the device (reading it would synchronise)."""
+    if value is None:
+        return None
+    if isinstance(value, torch.Tensor):
+        if value.device.type != "cpu":
+            return None
+        return value if value.dtype == torch.int32 and value.is_contiguous() else value.to(torch.int32).contiguous()
+    return np.asarray(value, np.int32)
+
+
+def _address(arr) -> int:
+    return arr.data_ptr() if isinstance(arr, torch.Tensor) else arr.ctypes.data
+
+
+def host_metadata_arrays(md):
+    """(query_start_loc, seq_lens) as host int32 arrays, consulted in the order of
+    metadata_batch_lists; None if only device copies exist."""
+    qsl = _host_int32(getattr(md, "query_start_loc_cpu", None))
+    if qsl is None:
+        ends = getattr(md, "actual_seq_lengths_q", None)
+        if ends is None or isinstance(ends, torch.Tensor) and ends.device.type != "cpu":
+            return None
+        qsl = np.concatenate([[0], np.asarray(_host_list(ends), np.int32)]).astype(np.int32)
+    for attr in _SEQ_LENS[:3]:
+        value = getattr(md, attr, None)
+        if value is not None:
+            seqs = _host_int32(value)
+            return (qsl, seqs) if seqs is not None else None
+    return None
 
 
 def _native_base():
@@ -272,7 +306,107 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         self._set_caches(kv_cache)
         if (key is None) != (value is None):
             raise ValueError("Both new K and V must be supplied together")
+        if self._native_step(layer, query, key, value, kv_cache, attn_metadata, output):
+            return output
         return self._run(layer, query, key, value, kv_cache, attn_metadata, output, write=True)
+
+    # ------------------------------------------------------------------ native decode step
+    def _native_step(self, layer, query, key, value, kv_cache, md, output) -> bool:
+        """Decode-shaped batches in one native call (oscar_decode_step_v1): classification,
+        plan, metadata upload, write + window, split-K decode and inverse rotation.  False
+        (nothing enqueued) sends the batch down the general path."""
+        if query.dtype not in (torch.bfloat16, torch.float16) or output.dtype != query.dtype:
+            return False
+        host = host_metadata_arrays(md)
+        if host is None:
+            return False
+        qsl, seqs = host
+        d, hq, hk = self.head_size, self.num_heads, self.num_kv_heads
+        n = min(query.shape[0], md.num_actual_tokens)
+        if n <= 0 or len(qsl) < 2 or len(seqs) < len(qsl) - 1:
+            return False
+        if not (query.is_contiguous() and output.is_contiguous()) or query.numel() // (hq * d) < n:
+            return False
+        has_new = key is not None
+        if has_new and self._oscar.window_enabled:
+            self._ensure_staging(layer, kv_cache)
+        a = self._step_args(layer, query.device, query.dtype)
+        if a is None:
+            return False
+        a.query, a.output, a.num_tokens = query.data_ptr(), output.data_ptr(), n
+        if has_new:
+            if key.stride(-1) != 1 or value.stride(-1) != 1 or key.stride(0) != value.stride(0) \
+                    or key.shape[0] < n or value.shape[0] < n:
+                return False
+            slots = md.slot_mapping
+            if slots.dtype != torch.int64 or not slots.is_contiguous() or slots.device != query.device:
+                slots = slots.to(device=query.device, dtype=torch.int64).contiguous()
+            a.key, a.value, a.kv_stride_token = key.data_ptr(), value.data_ptr(), key.stride(0)
+            a.slot_mapping = slots.data_ptr()
+            window = self._stage(layer) is not None
+            a.stage_mode = STAGE_WRITE if window else (
+                STAGE_INVALIDATE if getattr(layer, "_oscar_stage_ready", False) else STAGE_NONE)
+            ws = ops.DeviceScratch.get(query.device).store_workspace(2 * n * hk * d * 4)
+            a.store_workspace, a.store_workspace_bytes = ws.data_ptr(), ws.numel()
+        else:
+            a.key = a.value = a.slot_mapping = None
+        table = _block_tables(md)
+        if table.dtype != torch.int32 or table.stride(-1) != 1 or table.device != query.device:
+            table = table.to(device=query.device, dtype=torch.int32).contiguous()
+        a.block_table, a.block_table_stride = table.data_ptr(), table.stride(0)
+        a.host_query_start_loc, a.host_seq_lens = _address(qsl), _address(seqs)
+        a.num_reqs = len(qsl) - 1
+        ctx = ops.DeviceContext.get(query.device)
+        ws = ctx.step_workspace(0)  # shared by every layer of the device: current buffer
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        rc = ops.decode_step(ctx, a, torch.cuda.current_stream(query.device).cuda_stream)
+        if rc != 0:
+            return False
+        if n < query.shape[0]:
+            output[n:].zero_()
+        self._oscar_stats["reads"] += 1
+        if has_new:
+            self._oscar_stats["writes"] += 1
+            self._oscar_stats["kv_bytes_written"] += n * hk * 160
+        return True
+
+    def _step_args(self, layer, device, dtype):
+        """The layer's step arguments that stay fixed from call to call (caches, window
+        arena, rotations, settings, scratch), rebuilt only when one of them changes."""
+        d, hk = self.head_size, self.num_kv_heads
+        rk, rv = self._layer_rots(layer, device)
+        stage = self._stage(layer)
+        scratch = ops.DeviceScratch.get(device)
+        bs = self.key_cache.shape[1]
+        seats = 0 if stage is None else stage[2].shape[0] * bs
+        slot_claims, seat_claims = scratch.claims(self.key_cache.shape[0] * bs, seats)
+        arrivals = scratch.store_arrivals(hk)
+        key = (self.key_cache.data_ptr(), self.value_cache.data_ptr(), rk.data_ptr(), rv.data_ptr(),
+               None if stage is None else stage[2].data_ptr(), dtype, slot_claims.data_ptr(),
+               seat_claims.data_ptr(), arrivals.data_ptr())
+        cached = getattr(layer, "_oscar_step", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        from ._lib import StepArgs
+
+        a = StepArgs()
+        a.cache = ops.cache_struct(self.key_cache, self.value_cache, d)
+        keep = [rk, rv]
+        if stage is not None:
+            st = ops.staging_struct(stage, self.key_cache, d)
+            keep.append(st)
+            a.staging = ctypes_pointer(st)
+            a.sink_tokens_eff, a.recent_tokens = self.sink_eff, self._oscar.recent_tokens
+        a.num_q_heads = self.num_heads
+        a.q_dtype = ops.dtype_code(dtype)
+        a.rk, a.rv = rk.data_ptr(), rv.data_ptr()
+        a.k_clip_ratio, a.v_clip_ratio = self._oscar.k_clip_ratio, self._oscar.v_clip_ratio
+        a.scale = float(self.scale)
+        a.slot_claims, a.seat_claims = slot_claims.data_ptr(), seat_claims.data_ptr()
+        a.epoch_counter = scratch.epoch_counter.data_ptr()
+        a.arrivals = arrivals.data_ptr()
+        layer._oscar_step = (key, a, keep)
+        return a
 
     def _streaming_attention(self, layer, query, key, value, kv_cache, metadata, output):
         """backend.py:334-393: the read alone (the history and window are the state)."""

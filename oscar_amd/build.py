@@ -17,7 +17,7 @@ LIB = HERE / "liboscar_amd.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["capi.cpp", "store.hip", "rotate.hip", "attn_decode.hip", "attn_prefill.hip"]
+SOURCES = ["capi.cpp", "step.cpp", "store.hip", "rotate.hip", "attn_decode.hip", "attn_prefill.hip"]
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

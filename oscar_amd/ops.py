@@ -20,6 +20,10 @@ from ._lib import (GROUP_INTS, OSCAR_BF16, OSCAR_F16, OSCAR_F32, STAGE_INVALIDAT
 _DTYPES = {torch.float32: OSCAR_F32, torch.float16: OSCAR_F16, torch.bfloat16: OSCAR_BF16}
 
 
+def dtype_code(dtype: torch.dtype) -> int:
+    return _DTYPES[dtype]
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -151,6 +155,49 @@ class DeviceScratch:
         if self.attn_ws.numel() < nbytes:
             self.attn_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self.attn_ws
+
+
+class DeviceContext:
+    """The library's native context for one device (pinned + device metadata ring of the
+    decode step), created once per device and destroyed with the process."""
+
+    _by_device: dict = {}
+
+    def __init__(self, index: int):
+        lib = _lib.load()
+        ptr = C.c_void_p()
+        _lib.check(lib.oscar_context_create_v1(index, C.byref(ptr)), "oscar_context_create_v1")
+        self.ptr = ptr
+        self.index = index
+        self.step_ws = None
+
+    @classmethod
+    def get(cls, device: torch.device) -> "DeviceContext":
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        ctx = cls._by_device.get(index)
+        if ctx is None:
+            ctx = cls._by_device[index] = cls(index)
+        return ctx
+
+    def step_workspace(self, nbytes: int) -> torch.Tensor:
+        if self.step_ws is None or self.step_ws.numel() < nbytes:
+            self.step_ws = torch.empty(max(nbytes, 4 << 20), dtype=torch.uint8,
+                                       device=torch.device("cuda", self.index))
+        return self.step_ws
+
+
+def decode_step(ctx: DeviceContext, args: "_lib.StepArgs", stream: int) -> int:
+    """oscar_decode_step_v1; grows the step workspace and retries once when it is too
+    small.  Returns 0, or STEP_NOT_DECODE when the batch needs the general path."""
+    lib = _lib.load()
+    rc = lib.oscar_decode_step_v1(ctx.ptr, C.byref(args), C.c_void_p(stream))
+    if rc == -28 and args.workspace_needed > args.workspace_bytes:
+        ws = ctx.step_workspace(args.workspace_needed)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        rc = lib.oscar_decode_step_v1(ctx.ptr, C.byref(args), C.c_void_p(stream))
+    if rc < 0:
+        _lib.check(rc, "oscar_decode_step_v1")
+    return rc
 
 
 # ------------------------------------------------------------------------ store

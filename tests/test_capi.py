@@ -34,7 +34,7 @@ def header_functions() -> set:
 
 def test_library_exports_every_header_symbol(lib):
     names = header_functions()
-    assert len(names) == 10, names
+    assert len(names) == 14, names
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES)
@@ -49,7 +49,7 @@ STRUCTS = {
     "oscar_cache_v1": _lib.Cache, "oscar_staging_v1": _lib.Staging,
     "oscar_store_args_v1": _lib.StoreArgs, "oscar_rotate_args_v1": _lib.RotateArgs,
     "oscar_plan_v1": _lib.Plan, "oscar_attn_args_v1": _lib.AttnArgs,
-    "oscar_prefill_args_v1": _lib.PrefillArgs,
+    "oscar_prefill_args_v1": _lib.PrefillArgs, "oscar_step_args_v1": _lib.StepArgs,
 }
 
 

@@ -75,3 +75,69 @@ def test_forward_steps_match_oracle(cuda, qdt, ulp):
     assert np.array_equal(layer._oscar_slot_owner.cpu().numpy(), oracle_layer.staging.owner)
     assert np.array_equal(caches[0].view(torch.uint8).cpu().numpy(), oracle_layer.k8)
     assert np.array_equal(caches[1].view(torch.uint8).cpu().numpy(), oracle_layer.v8)
+
+
+@pytest.mark.parametrize("mode", ["mtp_window", "cache_only", "fp16_mtp"])
+def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
+    """forward() on decode-shaped batches takes oscar_decode_step_v1 (one native call);
+    the same batch through the general Python path (_run) and the oracle agree."""
+    from oscar_amd import backend as B
+    from oracle.attention import attention_ref
+
+    dev = torch.device("cuda", 0)
+    qdt = torch.float16 if mode == "fp16_mtp" else torch.bfloat16
+    fresh = mode != "cache_only"
+    prefixes, lengths = [3000, 129, 700, 24579], [4, 1, 3, 4]
+    c = cases.make_case(prefixes, lengths, fresh=fresh, seed=77)
+    d, hq, hk = 256, 6, 1
+    impl = OscarAttentionBackendImplFactory()
+    layer = _Layer()
+    eye = torch.eye(d, dtype=torch.float32, device=dev)
+    layer._oscar_rots = (eye, eye)
+    caches = [torch.from_numpy(c[x]).view(torch.int8).to(dev) for x in ("k8", "v8")]
+    impl._set_caches(caches)
+    impl._ensure_staging(layer, caches)
+    sk, sv, own = c["stage"]
+    layer._oscar_stage_k.copy_(torch.from_numpy(sk))
+    layer._oscar_stage_v.copy_(torch.from_numpy(sv))
+    layer._oscar_slot_owner.copy_(torch.from_numpy(own))
+    N = c["qsl"][-1]
+    md = _MD()
+    md.num_actual_tokens = N
+    # the current chunk is not written (slots -1): the history and window stay the state
+    md.slot_mapping = torch.full((N,), -1, dtype=torch.int64, device=dev)
+    md.query_start_loc_cpu = torch.tensor(c["qsl"], dtype=torch.int32)
+    md.seq_lens_cpu = torch.tensor(c["seqs"], dtype=torch.int32)
+    md.block_tables = torch.from_numpy(c["bt"]).to(dev)
+    tq = torch.from_numpy(c["q"]).to(dev).to(qdt).view(N, -1)
+    tk = None if c["k"] is None else torch.from_numpy(c["k"]).to(dev).to(qdt).view(N, -1)
+    tv = None if c["v"] is None else torch.from_numpy(c["v"]).to(dev).to(qdt).view(N, -1)
+    calls = {"reads": impl._oscar_stats["reads"]}
+    out_native = torch.empty(N, hq * d, dtype=qdt, device=dev)
+    assert impl._native_step(layer, tq, tk, tv, caches, md, out_native)
+    out_general = torch.empty_like(out_native)
+    impl._run(layer, tq, tk, tv, caches, md, out_general, write=True)
+    torch.cuda.synchronize()
+    assert impl._oscar_stats["reads"] == calls["reads"] + 2
+    q_dtype = "f16" if qdt == torch.float16 else "bf16"
+    ref_o, _ = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"], c["seqs"],
+                             c["scale"], c["stage"], q_dtype=q_dtype)
+    ulp = 2.0 ** -7 if qdt == torch.bfloat16 else 2.0 ** -10
+    for label, out in (("native", out_native), ("general", out_general)):
+        got = out.float().view(N, hq, d).cpu().numpy()
+        excess = float((np.abs(got - ref_o) - (2e-2 + ulp * np.abs(ref_o))).max())
+        print(f"{mode} {label}: max|out - oracle| = {np.abs(got - ref_o).max():.3e}", flush=True)
+        assert excess <= 0, f"{mode} {label} differs from the oracle"
+    diff = (out_native.float() - out_general.float()).abs().max().item()
+    print(f"{mode}: native vs general max diff {diff:.3e}", flush=True)
+    assert diff <= 2e-2
+
+
+def OscarAttentionBackendImplFactory():
+    from oscar_amd.backend import OscarAttentionBackendImpl
+
+    impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
+    impl.head_size, impl.num_heads, impl.num_kv_heads, impl.scale = 256, 6, 1, 256 ** -0.5
+    impl.key_cache = impl.value_cache = None
+    impl._oscar_setup()
+    return impl

@@ -179,3 +179,18 @@ def test_forward_requires_output_and_paired_kv():
     with pytest.raises(ValueError, match="together"):
         impl.forward(NS(), q, torch.zeros(1, 256, dtype=torch.bfloat16), None, cache,
                      meta([0], [1], [1]), output=out)
+
+
+def test_native_step_reads_host_metadata_in_the_accessor_order():
+    from oscar_amd.backend import host_metadata_arrays
+
+    md = NS(query_start_loc_cpu=torch.tensor([0, 4, 5], dtype=torch.int32),
+            seq_lens_list=[100, 7], seq_lens_cpu=torch.tensor([1, 1], dtype=torch.int32))
+    qsl, seqs = host_metadata_arrays(md)
+    assert qsl.data_ptr() == md.query_start_loc_cpu.data_ptr()   # zero-copy int32 tensor
+    assert list(seqs) == [100, 7]                                 # seq_lens_list first
+    md2 = NS(actual_seq_lengths_q=[4, 5], seq_lens_cpu=torch.tensor([9, 8]))
+    qsl, seqs = host_metadata_arrays(md2)
+    assert list(qsl) == [0, 4, 5] and seqs.dtype == torch.int32 and seqs.tolist() == [9, 8]
+    # device-only metadata: the native step is skipped (reading it would synchronise)
+    assert host_metadata_arrays(NS(query_start_loc=torch.tensor([0, 1]), seq_lens=torch.tensor([3]))) is None
