@@ -27,7 +27,7 @@ from importlib import import_module, util
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 from ._lib import STAGE_INVALIDATE, STAGE_NONE, STAGE_WRITE
 from .config import OscarConfig
 from .format import K_IDX_OFF, VALUES_PER_BYTE, check_d
@@ -346,7 +346,8 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             window = self._stage(layer) is not None
             a.stage_mode = STAGE_WRITE if window else (
                 STAGE_INVALIDATE if getattr(layer, "_oscar_stage_ready", False) else STAGE_NONE)
-            ws = ops.DeviceScratch.get(query.device).store_workspace(2 * n * hk * d * 4)
+            ws = ops.DeviceScratch.get(query.device).store_workspace(
+                _lib.load().oscar_store_workspace_bytes_v1(n, hk, d))
             a.store_workspace, a.store_workspace_bytes = ws.data_ptr(), ws.numel()
         else:
             a.key = a.value = a.slot_mapping = None

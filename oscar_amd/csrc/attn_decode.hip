@@ -106,14 +106,6 @@ __device__ __forceinline__ void store_through(f32x4* base, int index, f32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, index * 16, 0, 16 /* sc1 */);
 }
 
-// exchange with lane l^32
-__device__ __forceinline__ float swap_halves(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  // r[0]: lanes 0-31 keep their value, lanes 32-63 receive lanes 0-31's;
-  // r[1]: lanes 0-31 receive lanes 32-63's, lanes 32-63 keep theirs.
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
-
 // Query dtype QT (OSCAR_BF16 or OSCAR_F16): the dtype of the QK operands, of the
 // slow tiles' V values and of P in their PV.
 //

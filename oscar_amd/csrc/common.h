@@ -85,18 +85,38 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, float* v) {
 }
 
 // ---------------------------------------------------------------- wave helpers
-__device__ __forceinline__ float wave_max(float x) {
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+// x of another lane of the same 16-lane row, by a DPP control (quad_perm, mirrors)
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
 }
-__device__ __forceinline__ float wave_min(float x) {
-  for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
-  return x;
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
+
+// x of lane l ^ 32 (v_permlane32_swap: each half receives the other half's values)
+__device__ __forceinline__ float swap_halves(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  // r[0]: lanes 0-31 keep their value, lanes 32-63 receive lanes 0-31's;
+  // r[1]: lanes 0-31 receive lanes 32-63's, lanes 32-63 keep theirs.
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
-__device__ __forceinline__ float wave_sum(float x) {
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+
+// all-lane max / min of a full wave: four DPP steps inside each 16-lane row, then
+// the rows (lane l ^ 16, then l ^ 32).  max / min are exact, so the order is free.
+template <bool MAX>
+__device__ __forceinline__ float wave_extreme(float x) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); };
+  x = op(x, dpp_row<kDppXor1>(x));
+  x = op(x, dpp_row<kDppXor2>(x));
+  x = op(x, dpp_row<kDppHalfMirror>(x));
+  x = op(x, dpp_row<kDppMirror>(x));
+  x = op(x, __shfl_xor(x, 16));
+  return op(x, swap_halves(x));
 }
+__device__ __forceinline__ float wave_max(float x) { return wave_extreme<true>(x); }
+__device__ __forceinline__ float wave_min(float x) { return wave_extreme<false>(x); }
 
 // s_waitcnt lgkmcnt(0) leaving vmcnt/expcnt at their maxima (gfx9 encoding):
 // waits for this wave's LDS traffic without draining outstanding global loads.

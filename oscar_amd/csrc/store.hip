@@ -5,50 +5,44 @@
 // :130-148, do_kv_cache_update :151-198, _staging_write :513-555, and the
 // read-path rotations :370-373).
 //
-// Two launches:
-//   store_rotate_kernel  grid (vector tiles, 64-column blocks, kind in {K, V, Q}).
-//                        y = x @ R with fp64 accumulation: every product of a
-//                        bf16/fp16/fp32 input with an fp32 rotation entry is exact in
-//                        fp64 and the sum is rounded once, which yields the correctly
-//                        rounded fp32 value independent of summation order.  The
-//                        workgroup stages its 64 columns of R and its input vectors in
-//                        LDS with one batch of vector loads, then accumulates from LDS.
-//                        Writes y (fp32 workspace, K/V only) and the read-path copies
-//                        in the input dtype.  Column block 0 of the K kind also records
-//                        the last-writer claims (64-bit atomicMax of epoch<<24 | token)
-//                        for cache slots and staging seats, and performs the owner-tag
-//                        invalidation of a standalone KV update.
-//   store_quant_kernel   one wave per (token, kv head, K|V) vector: optional sort-clip,
-//                        fp16-rounded scale/zero, codes clamp(floor((x-zero)/scale+0.5),
-//                        0, 3), 2-bit packing and the byte writes of the slot winner;
-//                        staging winners write the owner tag and, inside the sink/recent
-//                        window, the unclipped fp32 rotated vector.  Its global reads
-//                        come in two rounds (slot, row, request bounds; then the claims).
+// The stored bytes are those of the correctly rounded rotation y = x @ R (fp32 result
+// of the exact sum), clipped and quantized as the reference does.  Two paths:
+//
+//   calls of <= kFusedTokens tokens (decode / MTP steps): store_small_kernel, one
+//   launch; y in fp64 (exact products, one rounding), winners by scanning the call's
+//   slot_mapping.
+//
+//   larger calls: store_prep_kernel (last-writer claims, window flags, fp16 planes of R),
+//   store_fused_kernel (MFMA rotation into LDS, then per vector: read-path copy,
+//   certification that every quantizer decision taken on the MFMA result is the one
+//   the exact y takes, quantization), store_exact_kernel (fp64 y for the vectors that
+//   were not certified and for those that keep an FP32 window copy).
 //
 // Claim epochs live on the device in two int64 words so that a captured graph
-// replays with fresh epochs and no extra launch: the rotate kernel uses
-// E = word0 + 1 and stores E in word1; the quant kernel reads word1 and copies it
+// replays with fresh epochs and no extra launch: the prep kernel uses
+// E = word0 + 1 and stores E in word1; the fused kernel reads word1 and copies it
 // to word0 for the next call.
+#include <atomic>
+
 #include "common.h"
 
 namespace oscar {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kCols = 64;     // output columns per rotate workgroup
-
 enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
 
 struct StoreParams {
   oscar_store_args_v1 a;
-  float* y;          // workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
+  float* y;          // small calls: workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
   int64_t capacity;  // num_blocks * block_size
-  int scan;          // small call: winners found by scanning slot_mapping (no claims)
+  int32_t* exact;    // large calls: [0] K count, [1] V count, [2 + kind * nvec + i] vectors
+                     // left to the exact pass (nvec = num_tokens * num_kv_heads)
+  int32_t* flags;    // large calls: [num_tokens] bit 0 = position inside the window
+  u32x4* planes;     // large calls: R_k, R_v as fp16 MFMA B fragments [2][D/32][D/16][2][64]
+  int32_t* bexp;     // large calls: [2][D] power-of-two column scale of the planes
+  float* colnorm;    // large calls: [2][D] ||R_:d||
 };
-
-// calls of at most this many tokens resolve last writers by scanning
-constexpr int64_t kScanTokens = 1024;
 
 __device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
   // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
@@ -77,224 +71,6 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
   }
 }
 
-// Last-writer claims and standalone invalidation for vectors [vec0, vec0 + count)
-// of the K kind (once per token: head 0); block (0, 0) publishes the call's epoch.
-__device__ void record_claims(const StoreParams& p, int64_t vec0, int count, int64_t heads, int64_t nvec) {
-  const oscar_store_args_v1& a = p.a;
-  const int64_t e0 = a.epoch_counter[0];
-  const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
-  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[1] = epoch;
-  for (int i = threadIdx.x; i < count; i += blockDim.x) {
-    const int64_t vec = vec0 + i;
-    if (vec >= nvec || vec % heads != 0) continue;
-    const int64_t t = vec / heads;
-    const int64_t s = a.slot_mapping[t];
-    if (s < 0 || s >= p.capacity) continue;
-    atomicMax((unsigned long long*)&a.slot_claims[s], (unsigned long long)claim_value(epoch, t));
-    if (a.stage_mode == OSCAR_STAGE_NONE) continue;
-    const int64_t seat = seat_of(s, a.cache.block_size, a.staging.rows);
-    if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
-    else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
-  }
-}
-
-// Small calls (decode steps): 16 vectors x 16 columns per workgroup, the
-// contraction split over the four waves (64-key quarters each, fp64 accumulate),
-// partial sums added in wave order in LDS, so a 32-token step spreads over ~1024
-// waves instead of a few long fp64 chains.
-constexpr int kSV = 16, kSC = 16;
-
-template <int D, int XT>
-__global__ __launch_bounds__(kThreads) void store_rotate_small_kernel(StoreParams p) {
-  const oscar_store_args_v1& a = p.a;
-  const int kind = blockIdx.z;
-  const int64_t heads = (kind == KIND_Q) ? a.num_q_heads : a.cache.num_kv_heads;
-  const int64_t nvec = a.num_tokens * heads;
-  const int64_t vec0 = (int64_t)blockIdx.x * kSV;
-  if (vec0 >= nvec) return;
-  const int col0 = blockIdx.y * kSC;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
-  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
-                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
-  const float* R = (kind == KIND_V) ? a.rv : a.rk;
-  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
-  float* y_out = (kind == KIND_Q) ? nullptr : p.y + (int64_t)kind * a.num_tokens * heads * D;
-
-  __shared__ __attribute__((aligned(16))) float s_r[D][kSC];
-  __shared__ float s_x[D][kSV + 1];
-  __shared__ double s_red[3][4][64];
-  constexpr int RN = D * kSC / 4;   // float4 of R
-  constexpr int XN = kSV * D / 8;   // 8-element x loads
-  constexpr int RI = (RN + kThreads - 1) / kThreads, XI = (XN + kThreads - 1) / kThreads;
-  f32x4 rr[RI];
-  float xv[XI][8];
-#pragma unroll
-  for (int i = 0; i < RI; ++i) {
-    const int e = tid + i * kThreads, k = e / (kSC / 4), c4 = e % (kSC / 4);
-    if (e >= RN) break;
-    if (R != nullptr) {
-      rr[i] = *(const f32x4*)(R + (int64_t)k * D + col0 + 4 * c4);
-    } else {
-      const int c = col0 + 4 * c4 - k;
-      rr[i] = f32x4{c == 0 ? 1.f : 0.f, c == -1 ? 1.f : 0.f, c == -2 ? 1.f : 0.f, c == -3 ? 1.f : 0.f};
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
-    if (e >= XN) break;
-    const int64_t vec = vec0 + v < nvec ? vec0 + v : vec0;
-    load8<XT>(src, (vec / heads) * src_stride + (vec % heads) * D + k8, xv[i]);
-    if (vec0 + v >= nvec) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
-    }
-  }
-  if (kind == KIND_K && blockIdx.y == 0 && !p.scan) record_claims(p, vec0, kSV, heads, nvec);
-#pragma unroll
-  for (int i = 0; i < RI; ++i) {
-    const int e = tid + i * kThreads, k = e / (kSC / 4), c4 = e % (kSC / 4);
-    if (e < RN) *(f32x4*)&s_r[k][4 * c4] = rr[i];
-  }
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
-    if (e < XN) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_x[k8 + j][v] = xv[i][j];
-    }
-  }
-  __syncthreads();
-  // lane -> vector v (16) x column group cg (4 columns); wave -> key quarter
-  const int v = lane >> 2, cg = lane & 3;
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  constexpr int KQ = D / 4;
-#pragma unroll 8
-  for (int kk = 0; kk < KQ; ++kk) {
-    const int k = wave * KQ + kk;
-    const f32x4 r4 = *(const f32x4*)&s_r[k][4 * cg];
-    const double x = s_x[k][v];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = fma(x, (double)r4[j], acc[j]);
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_red[wave - 1][j][lane] = acc[j];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < 3; ++w)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] += s_red[w][j][lane];
-  const int64_t vec = vec0 + v;
-  if (vec >= nvec) return;
-  const float y[4] = {(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]};
-  const int64_t base = vec * D + col0 + 4 * cg;
-  if (y_out != nullptr) *(f32x4*)(y_out + base) = f32x4{y[0], y[1], y[2], y[3]};
-  if (rot_out != nullptr) store4<XT>(rot_out, base, y);
-}
-
-template <int D, int TV, int XT>
-__global__ __launch_bounds__(kThreads) void store_rotate_kernel(StoreParams p) {
-  const oscar_store_args_v1& a = p.a;
-  const int kind = blockIdx.z;
-  const int64_t heads = (kind == KIND_Q) ? a.num_q_heads : a.cache.num_kv_heads;
-  const int64_t nvec = a.num_tokens * heads;
-  const int64_t vec0 = (int64_t)blockIdx.x * TV;
-  if (vec0 >= nvec) return;
-  const int col0 = blockIdx.y * kCols;
-  const int tid = threadIdx.x;
-
-  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
-  const int64_t src_stride = kind == KIND_K ? a.key_stride_token
-                           : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
-  const float* R = (kind == KIND_V) ? a.rv : a.rk;
-  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
-  float* y_out = (kind == KIND_Q) ? nullptr : p.y + (int64_t)kind * a.num_tokens * heads * D;
-
-  // ---- one batch of loads: this block's 64 columns of R and its TV input vectors
-  __shared__ __attribute__((aligned(16))) float s_r[D][kCols];
-  __shared__ float s_x[D][TV + 1];
-  constexpr int RV = D * kCols / 4 / kThreads;       // float4 of R per thread
-  constexpr int XV = TV * (D / 8) / kThreads;        // 8-element x loads per thread
-  static_assert(RV >= 1 && (TV * (D / 8)) % kThreads == 0, "tile shape");
-  f32x4 rr[RV];
-  float xv[XV][8];
-#pragma unroll
-  for (int i = 0; i < RV; ++i) {
-    const int e = tid + i * kThreads, k = e / (kCols / 4), c4 = e % (kCols / 4);
-    if (R != nullptr) {
-      rr[i] = *(const f32x4*)(R + (int64_t)k * D + col0 + 4 * c4);
-    } else {
-      const int c = col0 + 4 * c4 - k;
-      rr[i] = f32x4{c == 0 ? 1.f : 0.f, c == -1 ? 1.f : 0.f, c == -2 ? 1.f : 0.f, c == -3 ? 1.f : 0.f};
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < XV; ++i) {
-    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
-    const int64_t vec = vec0 + v < nvec ? vec0 + v : vec0;
-    const int64_t t = vec / heads, h = vec % heads;
-    load8<XT>(src, t * src_stride + h * D + k8, xv[i]);
-    if (vec0 + v >= nvec) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
-    }
-  }
-
-  if (kind == KIND_K && blockIdx.y == 0 && !p.scan) record_claims(p, vec0, TV, heads, nvec);
-
-#pragma unroll
-  for (int i = 0; i < RV; ++i) {
-    const int e = tid + i * kThreads, k = e / (kCols / 4), c4 = e % (kCols / 4);
-    *(f32x4*)&s_r[k][4 * c4] = rr[i];
-  }
-#pragma unroll
-  for (int i = 0; i < XV; ++i) {
-    const int e = tid + i * kThreads, v = e / (D / 8), k8 = (e % (D / 8)) * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s_x[k8 + j][v] = xv[i][j];
-  }
-  __syncthreads();
-
-  // thread tile: 4 consecutive columns x RPT vectors
-  constexpr int kColGroups = kCols / 4;              // 16
-  constexpr int kRowGroups = kThreads / kColGroups;  // 16
-  constexpr int RPT = TV / kRowGroups;
-  static_assert(RPT >= 1 && TV % kRowGroups == 0, "tile");
-  const int cg = tid % kColGroups, rg = tid / kColGroups;
-  double acc[RPT][4];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
-#pragma unroll 8
-  for (int k = 0; k < D; ++k) {
-    const f32x4 r4 = *(const f32x4*)&s_r[k][4 * cg];
-    const double r0 = r4[0], r1 = r4[1], r2 = r4[2], r3 = r4[3];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const double x = s_x[k][rg * RPT + i];
-      acc[i][0] = fma(x, r0, acc[i][0]);
-      acc[i][1] = fma(x, r1, acc[i][1]);
-      acc[i][2] = fma(x, r2, acc[i][2]);
-      acc[i][3] = fma(x, r3, acc[i][3]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int64_t vec = vec0 + rg * RPT + i;
-    if (vec >= nvec) continue;
-    const float y[4] = {(float)acc[i][0], (float)acc[i][1], (float)acc[i][2], (float)acc[i][3]};
-    const int64_t base = vec * D + col0 + cg * 4;
-    if (y_out != nullptr) *(f32x4*)(y_out + base) = f32x4{y[0], y[1], y[2], y[3]};
-    if (rot_out != nullptr) store4<XT>(rot_out, base, y);
-  }
-}
-
 // Sort-based clip threshold (backend.py:140-145): the idx-th smallest |x| of a
 // D-vector stored in LDS; ties are ordered by index so exactly one lane matches.
 template <int D>
@@ -315,23 +91,28 @@ __device__ float clip_threshold(const float* row, int idx, volatile float* slot)
 }
 
 // Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
-// the last writer of each, and its request's length and query end (for the window
-// rule).  Winners of duplicate slots / seats come from the claims (SCAN false) or
-// from scanning slot_mapping (SCAN true).  Computed by one wave, wave-uniform.
+// the last writer of each, and whether its position lies inside its request's sink /
+// recent window (backend.py:536-541: keep the FP32 copy, else drop the seat).
 struct Dest {
-  int64_t slot, seat, seq, end;
-  bool valid, slot_win, seat_win;
+  int64_t slot, seat;
+  bool valid, slot_win, seat_win, keep;
 };
 
-template <bool SCAN>
-__device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t, int64_t epoch) {
+// the window rule for token t of a request of length seq whose queries end at end
+__device__ __forceinline__ bool in_window(const oscar_store_args_v1& a, int64_t t, int64_t seq, int64_t end) {
+  const int64_t pos = seq - end + t;
+  return (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
+}
+
+// Destination of a small call's vector: winners of duplicate slots / seats by
+// scanning slot_mapping.  Computed by one wave, wave-uniform.
+__device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t) {
   const oscar_store_args_v1& a = p.a;
   const int lane = threadIdx.x & 63;
   const int64_t bs = a.cache.block_size;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   Dest d{};
-  // ---- one round of loads: slot, the request table (and, for a scan call, every
-  // slot of the call)
+  // ---- loads: slot, the request table and every slot of the call
   const int64_t slot = a.slot_mapping[t];
   // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
   // length and query end come from the same loads (qsl is non-decreasing)
@@ -353,15 +134,13 @@ __device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t, int64_t e
     }
   }
   d.slot = slot;
-  d.seq = seq;
-  d.end = end;
+  d.keep = window && in_window(a, t, seq, end);
   d.valid = slot >= 0 && slot < p.capacity;
   if (!d.valid) return d;
   const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
   d.seat = seat;
-  bool slot_win, seat_win;
-  if constexpr (SCAN) {
-    // last writer: no later valid token of the call has the same slot / seat
+  // last writer: no later valid token of the call has the same slot / seat
+  {
     bool later_slot = false, later_seat = false;
     for (int64_t c0 = 0; c0 < a.num_tokens; c0 += 64) {
       const int64_t t2 = c0 + lane;
@@ -370,18 +149,11 @@ __device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t, int64_t e
       later_slot |= later && s2 == slot;
       if (window) later_seat |= later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
     }
-    slot_win = !__any(later_slot);
-    seat_win = !__any(later_seat);
+    d.slot_win = !__any(later_slot);
+    d.seat_win = window && !__any(later_seat);
     // standalone KV update: every written seat loses its window copy
     if (a.stage_mode == OSCAR_STAGE_INVALIDATE && kind == KIND_K && lane == 0) a.staging.owner[seat] = -1;
-  } else {
-    // ---- second round: the claims
-    const long long mine = claim_value(epoch, t);
-    slot_win = (long long)a.slot_claims[slot] == mine;
-    seat_win = window && (long long)a.seat_claims[seat] == mine;
   }
-  d.slot_win = slot_win;
-  d.seat_win = seat_win;
   return d;
 }
 
@@ -399,14 +171,13 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
   const int64_t bs = a.cache.block_size;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   if (!d.valid) return;
-  const int64_t slot = d.slot, seat = d.seat, seq = d.seq, end = d.end;
+  const int64_t slot = d.slot, seat = d.seat;
   const bool slot_win = d.slot_win, seat_win = d.seat_win;
   const int64_t blk = slot / bs, off = slot % bs;
   if (active) *(f32x4*)&row[4 * lane] = x4;
 
   if (window && seat_win) {
-    const int64_t pos = seq - end + t;
-    const bool keep = (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
+    const bool keep = d.keep;
     if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
     if (keep && active) {
       float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) + (seat * hk + h) * D;
@@ -460,28 +231,6 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
   }
 }
 
-template <int D, bool SCAN>
-__global__ __launch_bounds__(kThreads) void store_quant_kernel(StoreParams p) {
-  const oscar_store_args_v1& a = p.a;
-  const int kind = blockIdx.y;  // K or V
-  const int64_t hk = a.cache.num_kv_heads;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // this call's epoch (word1, set by the rotate launch); word0 takes it for the next
-  // call (no other quant workgroup reads word0).  Scan calls use no claims.
-  int64_t epoch = 0;
-  if constexpr (!SCAN) {
-    epoch = a.epoch_counter[1];
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
-  }
-  const int64_t vec = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (vec >= a.num_tokens * hk) return;
-  const float* y = p.y + ((int64_t)kind * a.num_tokens * hk + vec) * D;
-  const f32x4 x4 = *(const f32x4*)(y + 4 * (lane < D / 4 ? lane : 0));
-  __shared__ float rows[kThreads / 64][D];
-  __shared__ float clip_slot[kThreads / 64];
-  const Dest d = vector_dest<SCAN>(p, kind, vec / hk, epoch);
-  quant_vector<D>(p, kind, vec / hk, vec % hk, d, x4, rows[wave], &clip_slot[wave]);
-}
 
 // Calls of at most kFusedTokens tokens (decode and MTP steps): one launch of
 // workgroups (token, vectors, column slice).  A workgroup rotates its vectors -- one
@@ -542,7 +291,7 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
   // the destination of a K / V vector: its loads overlap the rotation (only the last
   // slice to arrive uses it)
   Dest dest{};
-  if (kind != KIND_Q && wave == 0) dest = vector_dest<true>(p, kind, t, 0);
+  if (kind != KIND_Q && wave == 0) dest = vector_dest(p, kind, t);
   // the input vectors (fp32 in LDS; slots past nv are zero)
   for (int e = tid; e < kQPW * D; e += kSmallThreads)
     if (e >= nv * D) s_x[e / D][e % D] = 0.f;
@@ -622,44 +371,770 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
   quant_vector<D>(p, kind, t, h0, dest, x4, s_row, &s_clip);
 }
 
-template <int D, int TV>
-void launch_rotate(const StoreParams& p, dim3 grid, hipStream_t s) {
-  dim3 block(kThreads);
-  if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_BF16>), grid, block, 0, s, p);
-  else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_F16>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((store_rotate_kernel<D, TV, OSCAR_F32>), grid, block, 0, s, p);
+
+// Certified fp16 scale bits of the quantizer for (vmax, vmin): RN(vmax - vmin) / 3 (RN),
+// floored at 2^-14, to fp16 (RN) -- each step monotone in vmax - vmin.
+__device__ __forceinline__ unsigned short scale_bits_of(float vmax, float vmin) {
+  float scale = __fdiv_rn(vmax - vmin, 3.0f);
+  if (!(scale > 0x1p-14f)) scale = 0x1p-14f;
+  return f32_to_f16_bits(scale);
+}
+__device__ __forceinline__ int code_of(float x, float z16, float s16) {
+  const float q = fminf(fmaxf(floorf(__fdiv_rn(x - z16, s16) + 0.5f), 0.f), 3.f);
+  return (int)q;
+}
+
+// ---- 16-lane rows: a wave quantizes four vectors at once, lane l of a row holding
+// elements [l E, (l + 1) E) of its vector (E = D / 16)
+template <int CTRL>
+__device__ __forceinline__ int dpp_row_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);
+}
+template <bool MAX>
+__device__ __forceinline__ float row_extreme(float x) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); };
+  x = op(x, dpp_row<kDppXor1>(x));
+  x = op(x, dpp_row<kDppXor2>(x));
+  x = op(x, dpp_row<kDppHalfMirror>(x));
+  return op(x, dpp_row<kDppMirror>(x));
+}
+__device__ __forceinline__ int row_sum(int x) {
+  x += dpp_row_i<kDppXor1>(x);
+  x += dpp_row_i<kDppXor2>(x);
+  x += dpp_row_i<kDppHalfMirror>(x);
+  return x + dpp_row_i<kDppMirror>(x);
+}
+// the predicate holds on every lane of this lane's row
+__device__ __forceinline__ bool row_all(bool pred) {
+  const uint64_t m = __ballot(pred);
+  return ((m >> (threadIdx.x & 48)) & 0xffffull) == 0xffffull;
+}
+
+// idx-th smallest |y| of the row's D values (the sort-clip threshold, backend.py:140-145),
+// bit by bit from the top: the answer is the largest value v with count(|y| < v) <= idx
+template <int E>
+__device__ float row_kth_abs(const float* y, int idx) {
+  uint32_t u[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) u[j] = __float_as_uint(y[j]) & 0x7fffffffu;  // order of |y| (finite)
+  uint32_t v = 0;
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t cand = v | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) cnt += u[j] < cand;
+    if (row_sum(cnt) <= idx) v = cand;
+  }
+  return __uint_as_float(v);
+}
+
+// Certify and quantize the rows' vectors from y~ (lane: y[E] of its row's vector, e[E]
+// the bound on |y~ - y| of each element).  Every decision the quantizer takes -- the
+// sort-clip threshold (order statistics move by at most max e), the fp16 scale and
+// zero (from the intervals of vmin and vmax) and each code -- is evaluated at both ends
+// of y~ +- e; the quantizer's steps are monotone, so equal ends mean y gives the same
+// bytes.  Certified rows with write != 0 store their codes and meta (K slot kslot + 32 /
+// V slot vslot); the function returns whether this lane's row was certified.
+template <int D>
+__device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, const float* e,
+                                bool write, uint8_t* kslot, uint8_t* vslot) {
+  constexpr int E = D / 16;
+  const int l = threadIdx.x & 15;
+  const float clip = kind == KIND_K ? p.a.k_clip_ratio : p.a.v_clip_ratio;
+  bool finite = true;
+  float emax = 0.f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    finite &= __builtin_isfinite(y[j]) && __builtin_isfinite(e[j]);
+    emax = fmaxf(emax, e[j]);
+  }
+  if (!row_all(finite)) return false;  // NaN / inf: the exact pass reproduces the reference
+  emax = row_extreme<true>(emax);
+  float t_lo = INFINITY, t_hi = INFINITY;
+  if (clip > 0.f) {
+    int idx = (int)(clip * (float)D);
+    if (idx > D - 1) idx = D - 1;
+    const float t = row_kth_abs<E>(y, idx);
+    const float et = emax + t * 0x1p-22f;
+    t_lo = fmaxf(t - et, 0.f);
+    t_hi = t + et;
+  }
+  float lo[E], hi[E];
+  float vmin_lo = INFINITY, vmin_hi = INFINITY, vmax_lo = -INFINITY, vmax_hi = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    lo[j] = y[j] - e[j];
+    hi[j] = y[j] + e[j];
+    if (clip > 0.f) {
+      lo[j] = fmaxf(-t_hi, fminf(lo[j], t_lo));
+      hi[j] = fmaxf(-t_lo, fminf(hi[j], t_hi));
+    }
+    vmin_lo = fminf(vmin_lo, lo[j]);
+    vmin_hi = fminf(vmin_hi, hi[j]);
+    vmax_lo = fmaxf(vmax_lo, lo[j]);
+    vmax_hi = fmaxf(vmax_hi, hi[j]);
+  }
+  vmin_lo = row_extreme<false>(vmin_lo);
+  vmin_hi = row_extreme<false>(vmin_hi);
+  vmax_lo = row_extreme<true>(vmax_lo);
+  vmax_hi = row_extreme<true>(vmax_hi);
+  const unsigned short s_a = scale_bits_of(vmax_lo, vmin_hi), s_b = scale_bits_of(vmax_hi, vmin_lo);
+  const unsigned short z_a = f32_to_f16_bits(vmin_lo), z_b = f32_to_f16_bits(vmin_hi);
+  // a zero of either sign is left to the exact pass: its sign bit follows y exactly
+  if (s_a != s_b || z_a != z_b || (z_a & 0x7fff) == 0) return false;  // row-uniform
+  const float s16 = f16_bits_to_f32(s_a), z16 = f16_bits_to_f32(z_a);
+  // codes at both ends: q = (x - z) * (1 / s) is within a few ulp of the quantizer's
+  // RN(RN(x - z) / s), so floor(q + 0.5 -+ m) with the margin m = 2^-19 max(|q|, 1) (which
+  // also covers the rounding of + 0.5) brackets both ends' codes; only where the bracket
+  // is not one code are the exact divisions evaluated
+  const float inv = __builtin_amdgcn_rcpf(s16);
+  int code[E];
+  bool same = true;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const float ql = (lo[j] - z16) * inv, qh = (hi[j] - z16) * inv;
+    const float ml = 0x1p-19f * fmaxf(fabsf(ql), 1.f), mh = 0x1p-19f * fmaxf(fabsf(qh), 1.f);
+    const int cl = (int)fminf(fmaxf(floorf(ql + 0.5f - ml), 0.f), 3.f);
+    const int ch = (int)fminf(fmaxf(floorf(qh + 0.5f + mh), 0.f), 3.f);
+    if (cl == ch) {
+      code[j] = cl;
+    } else {
+      code[j] = code_of(lo[j], z16, s16);
+      same &= code[j] == code_of(hi[j], z16, s16);
+    }
+  }
+  if (!row_all(same)) return false;
+  if (write) {
+    // byte b holds the codes of elements 4b..4b+3, two bits each (format.py:84-87)
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) packed |= (uint32_t)code[j] << (2 * j);
+    uint8_t* dst = (kind == KIND_K ? kslot + 32 : vslot) + l * (E / 4);
+    if constexpr (E == 16) *(uint32_t*)dst = packed;
+    else if constexpr (E == 8) *(uint16_t*)dst = (uint16_t)packed;
+    else *dst = (uint8_t)packed;
+    if (l == 0) *(unsigned*)(kslot + (kind == KIND_K ? 0 : 4)) = (unsigned)s_a | ((unsigned)z_a << 16);
+  }
+  return true;
+}
+
+// ------------------------------------------------------------------ large calls
+// Calls of more than kFusedTokens tokens, in three launches:
+//
+//   store_prep_kernel    one thread per token: the last-writer claims of its slot and
+//                        seat (64-bit atomicMax of epoch<<24 | token), or the owner-tag
+//                        invalidation of a standalone update, and the token's window flag
+//                        (its position inside the sink / recent window of its request);
+//                        and one block per 32-column block of R_k and R_v: its two fp16
+//                        planes, scaled by a power of two per column, in MFMA B order.
+//   store_fused_kernel   8 waves over runs of row blocks (32 vectors each) of one kind.
+//                        Each wave keeps one 32-column block of R's planes in registers; a
+//                        row block's x is
+//                        staged in LDS as fp16 scaled by a power of two per vector (fp32
+//                        inputs in two planes); v_mfma_f32_32x32x16_f16 forms y~ = x R in
+//                        chains of kChainSteps K-steps whose sum is rounded once, into an LDS
+//                        tile of whole vectors.  Then each wave takes vectors from the tile:
+//                        read-path copy, destination, certification, quantization.
+//   store_exact_kernel   the vectors that were not certified or whose FP32 window copy
+//                        needs y itself: y in fp64 (exact products, one final rounding),
+//                        then the same quantizer.
+//
+// Error of y~ against y: the instruction's products are exact and it rounds C + (the
+// sum of its 16 products) once to fp32 (measured on gfx950), so a chain of kChainSteps
+// K-steps errs by <= kChainSteps * 2^-24 * sum_k |x_k R_kd|; the residual of R's two
+// fp16 planes is <= 2^-22 |R_kd| per entry, that of fp32 x's two planes <= 2^-22 |x_k|,
+// and the chain sum (exact two-sums, then one rounding) to fp32 (<= 2^-24 |y~|).  By Cauchy-Schwarz
+// sum_k |x_k R_kd| <= ||x|| ||R_:d||, so with kChainSteps = 4
+//     e = coef ||x|| ||R_:d|| + 2^-22 |y~|,  coef = 2^-20 (bf16 / fp16 x), 2^-19 (fp32 x)
+// bounds |y~ - y| with a margin of 2 or more (and still holds if the instruction rounded
+// twice).  Elements of x below 2^-31 max|x| or of R below 2^-31 max|R_:d| that fp16
+// cannot hold exactly after scaling add < 2^-28 of the bound.
+constexpr int kFusedThreads = 512;  // 8 waves
+constexpr int kChainSteps = 4;      // K-steps per accumulation chain
+constexpr int kExactThreads = 1024;
+constexpr int kExactGroup = 8;      // vectors per exact-pass group
+constexpr int kExactBuffer = 512;   // exact-pass vectors a fused workgroup gathers in LDS
+constexpr int kReqLds = 2048;       // request tables of up to this many entries go to LDS
+
+// power-of-two exponent s with m * 2^s in [2^14, 2^15) (m > 0 finite); 0 otherwise
+__device__ __forceinline__ int fp16_exponent(float m) {
+  if (!(m > 0.f) || !__builtin_isfinite(m)) return 0;
+  int e;
+  frexpf(m, &e);
+  return 15 - e;
+}
+
+__device__ __forceinline__ unsigned f16_pair(float lo, float hi) {
+  return (unsigned)f32_to_f16_bits(lo) | ((unsigned)f32_to_f16_bits(hi) << 16);
+}
+
+// fp16 planes of one 32-column block of R (which: 0 = R_k, 1 = R_v) in MFMA B order:
+// fragment (s, lane n + 32 g) holds R[16 s + 8 g + j][32 cb + n] * 2^bexp, j < 8, as
+// the rounded plane and the (exact) remainder rounded again
+template <int D>
+__device__ void rotation_planes(const StoreParams& p, int which, int cb) {
+  constexpr int KS = D / 16;
+  const float* R = which ? p.a.rv : p.a.rk;
+  const int tid = threadIdx.x, c = tid % 32, part = tid / 32;  // 8 parts of the rows
+  auto r_at = [&](int k, int col) { return R != nullptr ? R[(int64_t)k * D + col] : (k == col ? 1.f : 0.f); };
+  __shared__ float s_mx[8][32], s_sq[8][32];
+  __shared__ int s_e[32];
+  float mx = 0.f, sq = 0.f;
+  for (int k = part; k < D; k += 8) {
+    const float r = r_at(k, 32 * cb + c);
+    mx = fmaxf(mx, fabsf(r));
+    sq = fmaf(r, r, sq);
+  }
+  s_mx[part][c] = mx;
+  s_sq[part][c] = sq;
+  __syncthreads();
+  if (tid < 32) {
+    for (int i = 1; i < 8; ++i) {
+      mx = fmaxf(mx, s_mx[i][c]);
+      sq += s_sq[i][c];
+    }
+    s_e[c] = fp16_exponent(mx);
+    p.bexp[which * D + 32 * cb + c] = s_e[c];
+    p.colnorm[which * D + 32 * cb + c] = sqrtf(sq);
+  }
+  __syncthreads();
+  u32x4* out = p.planes + ((int64_t)(which * (D / 32) + cb) * KS) * 2 * 64;
+  for (int f = tid; f < KS * 64; f += blockDim.x) {
+    const int s = f / 64, lane = f % 64, n = lane % 32, g = lane / 32;
+    const int e = s_e[n];
+    u32x4 w0, w1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int k = 16 * s + 8 * g + 2 * w;
+      const float h0 = ldexpf(r_at(k, 32 * cb + n), e), h1 = ldexpf(r_at(k + 1, 32 * cb + n), e);
+      const float q0 = f16_bits_to_f32(f32_to_f16_bits(h0)), q1 = f16_bits_to_f32(f32_to_f16_bits(h1));
+      w0[w] = f16_pair(q0, q1);
+      w1[w] = f16_pair(h0 - q0, h1 - q1);  // exact differences
+    }
+    out[(s * 2 + 0) * 64 + lane] = w0;
+    out[(s * 2 + 1) * 64 + lane] = w1;
+  }
+}
+
+// ---- claims, window flags and the rotation planes: blocks [0, token blocks) take
+// 256 tokens each, the 2 * D / 32 blocks after them one column block of R_k or R_v
+template <int D>
+__global__ __launch_bounds__(256) void store_prep_kernel(StoreParams p) {
+  const oscar_store_args_v1& a = p.a;
+  const int64_t token_blocks = (a.num_tokens + 255) / 256;
+  if ((int64_t)blockIdx.x >= token_blocks) {
+    const int b = (int)(blockIdx.x - token_blocks);
+    rotation_planes<D>(p, b / (D / 32), b % (D / 32));
+    return;
+  }
+  const int64_t e0 = a.epoch_counter[0];
+  const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    a.epoch_counter[1] = epoch;
+    p.exact[0] = 0;
+    p.exact[1] = 0;
+  }
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  const bool lds = window && a.num_reqs <= kReqLds;
+  __shared__ int32_t s_qsl[kReqLds + 1];
+  if (lds) {
+    for (int r = threadIdx.x; r <= a.num_reqs; r += blockDim.x) s_qsl[r] = a.query_start_loc[r];
+    __syncthreads();
+  }
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.num_tokens) return;
+  const int64_t slot = a.slot_mapping[t];
+  if (window) {
+    // request of t: the last r < num_reqs with min(qsl[r], num_tokens) <= t (qsl is
+    // non-decreasing); none -> length 0, end 0
+    int lo = 0, hi = a.num_reqs;  // answer in [lo - 1, hi - 1]
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      int64_t st = lds ? s_qsl[mid] : a.query_start_loc[mid];
+      if (st > a.num_tokens) st = a.num_tokens;
+      if (st <= t) lo = mid + 1;
+      else hi = mid;
+    }
+    const int r = lo - 1;
+    const int64_t seq = r >= 0 ? a.seq_lens[r] : 0;
+    const int64_t end = r >= 0 ? (lds ? s_qsl[r + 1] : a.query_start_loc[r + 1]) : 0;
+    p.flags[t] = in_window(a, t, seq, end) ? 1 : 0;
+  }
+  if (slot < 0 || slot >= p.capacity) return;
+  atomicMax((unsigned long long*)&a.slot_claims[slot], (unsigned long long)claim_value(epoch, t));
+  if (a.stage_mode == OSCAR_STAGE_NONE) return;
+  const int64_t seat = seat_of(slot, a.cache.block_size, a.staging.rows);
+  if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
+  else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
+}
+
+// Destination of token t's vectors from the finished claims (slot already loaded)
+__device__ __forceinline__ Dest claimed_dest(const StoreParams& p, int64_t t, int64_t slot, int32_t flag,
+                                             int64_t epoch) {
+  const oscar_store_args_v1& a = p.a;
+  Dest d{};
+  d.slot = slot;
+  d.valid = slot >= 0 && slot < p.capacity;
+  if (!d.valid) return d;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  const long long mine = claim_value(epoch, t);
+  d.seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, a.cache.block_size, a.staging.rows) : 0;
+  d.slot_win = (long long)a.slot_claims[slot] == mine;
+  d.seat_win = window && (long long)a.seat_claims[d.seat] == mine;
+  d.keep = window && (flag & 1);
+  return d;
+}
+
+// ---- x staging: a thread holds 16 consecutive elements of one vector
+template <int XT>
+struct XChunk {
+  static constexpr int W = XT == OSCAR_F32 ? 4 : 2;  // 16-byte words
+  u32x4 w[W];
+  __device__ __forceinline__ void load(const void* base, int64_t i) {
+    if constexpr (XT == OSCAR_F32) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = *(const u32x4*)((const float*)base + i + 4 * k);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) w[k] = *(const u32x4*)((const uint16_t*)base + i + 8 * k);
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = u32x4{0u, 0u, 0u, 0u};
+  }
+  __device__ __forceinline__ void to_float(float* f) const {
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (XT == OSCAR_F32) {
+          f[4 * k + e] = __uint_as_float(w[k][e]);
+        } else if constexpr (XT == OSCAR_BF16) {
+          f[8 * k + 2 * e] = __uint_as_float(w[k][e] << 16);
+          f[8 * k + 2 * e + 1] = __uint_as_float(w[k][e] & 0xffff0000u);
+        } else {
+          f[8 * k + 2 * e] = f16_bits_to_f32((unsigned short)(w[k][e] & 0xffff));
+          f[8 * k + 2 * e + 1] = f16_bits_to_f32((unsigned short)(w[k][e] >> 16));
+        }
+      }
+  }
+};
+
+template <int D, int XT>
+__global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams p) {
+  constexpr int KS = D / 16;               // K-steps
+  constexpr int NC = KS / kChainSteps;     // accumulation chains
+  constexpr int CW = D / 32;               // column waves
+  constexpr int RG = 8 / CW;               // row blocks per round
+  constexpr int TV = RG * 32;              // vectors per round
+  constexpr int TPV = D / 16;              // staging threads per vector
+  constexpr int XP = XT == OSCAR_F32 ? 2 : 1;  // fp16 planes of x
+  constexpr int NVW = TV / 8;              // vectors per wave in the quantize phase
+  constexpr int E = D / 16;                // elements per lane in the quantize phase
+  constexpr int YS = D + 4;                // LDS row stride of the y tile
+  static_assert(KS % kChainSteps == 0 && TV * TPV == kFusedThreads, "fused tile shape");
+  const oscar_store_args_v1& a = p.a;
+  const int64_t hk = a.cache.num_kv_heads;
+  const int64_t kv_vec = a.num_tokens * hk;
+  const int64_t q_vec = a.query_rot != nullptr ? a.num_tokens * a.num_q_heads : 0;
+  const int64_t rounds_kv = (kv_vec + TV - 1) / TV, rounds_q = (q_vec + TV - 1) / TV;
+  const int64_t total = 2 * rounds_kv + rounds_q;
+  const int64_t per = (total + gridDim.x - 1) / gridDim.x;
+  const int64_t it0 = (int64_t)blockIdx.x * per;
+  const int64_t it1 = it0 + per < total ? it0 + per : total;
+  const int64_t epoch = a.epoch_counter[1];
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
+  if (it0 >= it1) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = wave % CW, rg = wave / CW;  // this wave's column block and row block
+  const int col = 32 * cb + m;               // this lane's output column
+
+  __shared__ u32x4 s_a[XP][RG][KS][64];      // A fragments (fp16), MFMA lane order
+  __shared__ __attribute__((aligned(16))) float s_y[TV][YS];
+  __shared__ int s_ax[TV];                   // per-vector exponent of x
+  __shared__ float s_nx[TV];                 // ||x||
+  __shared__ __attribute__((aligned(16))) float s_cn[D];  // ||R_:d||
+  __shared__ long long s_slot[TV];
+  __shared__ Dest s_dest[TV];
+
+  // an item is one round of one kind: K rounds, V rounds, then query rounds
+  auto item_kind = [&](int64_t it) { return it < rounds_kv ? KIND_K : (it < 2 * rounds_kv ? KIND_V : KIND_Q); };
+  auto item_base = [&](int64_t it) {
+    return (it < rounds_kv ? it : (it < 2 * rounds_kv ? it - rounds_kv : it - 2 * rounds_kv)) * TV;
+  };
+  const int sv = tid / TPV, sq = tid % TPV;  // staging: vector, 16-element chunk
+  auto load_x = [&](int64_t it, XChunk<XT>& xc) {
+    const int kind = item_kind(it);
+    const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
+    const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
+    const int64_t vec = item_base(it) + sv;
+    const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
+    const int64_t stride = kind == KIND_K ? a.key_stride_token
+                         : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
+    if (vec < nvec) xc.load(src, (vec / heads) * stride + (vec % heads) * D + 16 * sq);
+    else xc.zero();
+  };
+
+  // ---- B: R's 32-column block in registers, the two fp16 planes written by the prep
+  // kernel (lane (n, g) of K-step s: R[16 s + 8 g + j][col] * 2^bcol, j < 8)
+  u32x4 b0[KS], b1[KS];
+  int bcol = 0;
+  int rkind = -1;  // 0: R_k (K and query rounds), 1: R_v
+  auto load_b = [&](int which) {
+    const u32x4* src = p.planes + ((int64_t)(which * CW + cb) * KS) * 2 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      b0[s] = src[(2 * s) * 64];
+      b1[s] = src[(2 * s + 1) * 64];
+    }
+    bcol = p.bexp[which * D + col];
+    if (rg == 0 && g == 0) s_cn[col] = p.colnorm[which * D + col];
+  };
+
+  // destination inputs of vector tid (< TV) of a round, loaded one round ahead: slot and
+  // window flag; the claims follow at the start of the round, used after the MFMA phase
+  long long slot_n = -1;
+  int32_t flag_n = 0;
+  auto load_slot = [&](int64_t it) {
+    slot_n = -1;
+    flag_n = 0;
+    const int64_t vec = item_base(it) + tid;
+    if (item_kind(it) != KIND_Q && tid < TV && vec < kv_vec) {
+      slot_n = a.slot_mapping[vec / hk];
+      if (a.stage_mode == OSCAR_STAGE_WRITE) flag_n = p.flags[vec / hk];
+    }
+  };
+  // vectors left to the exact pass, gathered in LDS and appended to the global lists
+  // once per workgroup (a full buffer spills straight to the global list)
+  __shared__ int32_t s_xl[2][kExactBuffer];
+  __shared__ int s_xn[2], s_xbase[2];
+  if (tid < 2) s_xn[tid] = 0;
+
+  XChunk<XT> xc;
+  load_x(it0, xc);
+  load_slot(it0);
+  const bool fp32x = XT == OSCAR_F32;
+  const float coef = fp32x ? 0x1p-19f : 0x1p-20f;
+  for (int64_t it = it0; it < it1; ++it) {
+    const int kind = item_kind(it);
+    const int64_t base = item_base(it);
+    const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
+    const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
+    const int which = kind == KIND_V ? 1 : 0;
+    if (which != rkind) {
+      load_b(which);
+      rkind = which;
+    }
+    // ---- stage x: exponent, norm, fp16 planes in MFMA A order
+    {
+      float f[16];
+      xc.to_float(f);
+      float mx = 0.f, ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        mx = fmaxf(mx, fabsf(f[j]));
+        ss = fmaf(f[j], f[j], ss);
+      }
+#pragma unroll
+      for (int o = 1; o < TPV; o <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+        ss += __shfl_xor(ss, o);
+      }
+      const int ax = fp16_exponent(mx);
+      const int rb = sv / 32, mm = sv % 32;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // chunk 2 sq + h: K-step sq, lane half h
+        u32x4 w0, w1;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float h0 = ldexpf(f[8 * h + 2 * w], ax), h1 = ldexpf(f[8 * h + 2 * w + 1], ax);
+          const float q0 = f16_bits_to_f32(f32_to_f16_bits(h0)), q1 = f16_bits_to_f32(f32_to_f16_bits(h1));
+          w0[w] = f16_pair(q0, q1);
+          w1[w] = f16_pair(h0 - q0, h1 - q1);
+        }
+        s_a[0][rb][sq][mm + 32 * h] = w0;
+        if constexpr (XP == 2) s_a[XP - 1][rb][sq][mm + 32 * h] = w1;
+      }
+      if (sq == 0) {
+        s_ax[sv] = ax;
+        s_nx[sv] = sqrtf(ss);
+      }
+    }
+    // ---- this round's claims (in flight during the MFMA phase)
+    const long long slot = slot_n;
+    const int32_t flag = flag_n;
+    const bool claimed = slot >= 0 && slot < p.capacity;  // K / V rounds, tid < TV only
+    long long c_slot = -1, c_seat = -1;
+    int64_t seat = 0;
+    if (claimed) {
+      c_slot = (long long)a.slot_claims[slot];
+      if (a.stage_mode != OSCAR_STAGE_NONE) seat = seat_of(slot, a.cache.block_size, a.staging.rows);
+      if (a.stage_mode == OSCAR_STAGE_WRITE) c_seat = (long long)a.seat_claims[seat];
+    }
+    __syncthreads();
+    if (it + 1 < it1) {  // in flight during the MFMA and quantize phases
+      load_x(it + 1, xc);
+      load_slot(it + 1);
+    }
+
+    // ---- MFMA: y~ of this wave's row block x column block into the y tile
+    {
+      f32x16 chain[NC], small = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) chain[c] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const f16x8 a0 = __builtin_bit_cast(f16x8, s_a[0][rg][s][lane]);
+        const f16x8 f0 = __builtin_bit_cast(f16x8, b0[s]);
+        const f16x8 f1 = __builtin_bit_cast(f16x8, b1[s]);
+        chain[s / kChainSteps] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f0, chain[s / kChainSteps], 0, 0, 0);
+        small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f1, small, 0, 0, 0);
+        if constexpr (XP == 2) {
+          const f16x8 a1 = __builtin_bit_cast(f16x8, s_a[1][rg][s][lane]);
+          small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f0, small, 0, 0, 0);
+          small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f1, small, 0, 0, 0);
+        }
+      }
+      // C[i][n]: vector i = 8 (r / 4) + 4 g + r % 4 of the row block, column n = m
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int v = 32 * rg + 8 * (r >> 2) + 4 * g + (r & 3);
+        // chains + small summed with exact two-sums (the errors gathered in comp), then
+        // one rounding: the fp32 of the exact sum to within 2^-24 relative
+        float sum = small[r], comp = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const float b = chain[c][r];
+          const float t = sum + b, bb = t - sum;
+          comp += (sum - (t - bb)) + (b - bb);
+          sum = t;
+        }
+        s_y[v][col] = ldexpf(sum + comp, -(s_ax[v] + bcol));
+      }
+    }
+    // ---- destinations
+    if (kind != KIND_Q && tid < TV) {
+      Dest d{};
+      if (claimed) {
+        const long long mine = claim_value(epoch, (base + tid) / hk);
+        const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+        d.slot = slot;
+        d.seat = seat;
+        d.valid = true;
+        d.slot_win = c_slot == mine;
+        d.seat_win = window && c_seat == mine;
+        d.keep = window && (flag & 1);
+      }
+      s_dest[tid] = d;
+    }
+    __syncthreads();
+
+    // ---- four vectors at a time (one per 16-lane row, lane l holding elements
+    // [l E, (l + 1) E)): read-path copy, destination, certification, quantization
+    void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
+    const int row = lane >> 4, l = lane & 15;
+#pragma unroll 1
+    for (int j = 0; j < NVW / 4; ++j) {
+      const int v = wave * NVW + 4 * j + row;
+      const int64_t vec = base + v;
+      const bool live = vec < nvec;
+      float y[E];
+#pragma unroll
+      for (int q = 0; q < E; q += 4) *(f32x4*)&y[q] = *(const f32x4*)&s_y[v][l * E + q];
+      if (live && rot_out != nullptr) {
+#pragma unroll
+        for (int q = 0; q < E; q += 4) store4<XT>(rot_out, vec * D + l * E + q, &y[q]);
+      }
+      if (kind == KIND_Q) continue;
+      Dest d{};
+      if (live) d = s_dest[v];
+      bool exact = d.valid && d.seat_win && d.keep;  // the FP32 window copy is y itself
+      if (d.valid && !exact && d.slot_win) {
+        const int64_t h = vec % hk, blk = d.slot / a.cache.block_size, off = d.slot % a.cache.block_size;
+        uint8_t* kslot = a.cache.k + blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
+        uint8_t* vslot = a.cache.v + blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
+        const float nx = s_nx[v] * (1.f + 0x1p-10f);
+        float e[E];
+#pragma unroll
+        for (int q = 0; q < E; ++q)
+          e[q] = coef * nx * s_cn[l * E + q] * (1.f + 0x1p-10f) + fabsf(y[q]) * 0x1p-22f + 0x1p-126f;
+        exact = !certify_quant16<D>(p, kind, y, e, true, kslot, vslot);
+      }
+      if (exact && l == 0) {
+        const int i = atomicAdd(&s_xn[kind], 1);
+        if (i < kExactBuffer) {
+          s_xl[kind][i] = (int32_t)vec;
+        } else {
+          const int g = atomicAdd(&p.exact[kind], 1);
+          p.exact[2 + kind * kv_vec + g] = (int32_t)vec;
+        }
+      }
+      // a seat this token wins outside the window loses its FP32 copy (backend.py:536-541)
+      if (d.valid && !exact && d.seat_win && kind == KIND_K && l == 0) a.staging.owner[d.seat] = -1;
+    }
+    __syncthreads();
+  }
+  // ---- the gathered exact-pass vectors to the global lists
+  if (tid < 2) {
+    const int n = s_xn[tid] < kExactBuffer ? s_xn[tid] : kExactBuffer;
+    s_xbase[tid] = n > 0 ? atomicAdd(&p.exact[tid], n) : 0;
+  }
+  __syncthreads();
+  for (int k = 0; k < 2; ++k) {
+    const int n = s_xn[k] < kExactBuffer ? s_xn[k] : kExactBuffer;
+    for (int i = tid; i < n; i += kFusedThreads) p.exact[2 + k * kv_vec + s_xbase[k] + i] = s_xl[k][i];
+  }
+}
+
+// ---- exact pass: groups of kExactGroup vectors of one kind.  R streams through LDS in
+// chunks of ROWS rows (three buffers: while chunk c is used, c + 1 is in LDS and c + 2 in
+// flight).  Thread (col, vs) sums the products of vectors vs * VPT .. + VPT - 1 with R's
+// column col in fp64 over all rows (each product of an input element with an fp32 entry
+// is exact; one final rounding to fp32).
+template <int D, int XT>
+__global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams p) {
+  constexpr int VS = kExactThreads / D;              // vector sets
+  constexpr int EG = VS > kExactGroup ? VS : kExactGroup;  // vectors per group
+  constexpr int VPT = EG / VS;                       // vectors per thread
+  constexpr int ROWS = 8192 / D < D ? 8192 / D : D;  // rows per chunk (<= 32 KB)
+  constexpr int NCH = D / ROWS;                      // chunks
+  constexpr int F4 = ROWS * D / 4 / kExactThreads;   // float4 loads per thread per chunk
+  static_assert(VPT >= 1 && EG % VS == 0 && F4 >= 1 && NCH * ROWS == D, "exact tile shape");
+  const oscar_store_args_v1& a = p.a;
+  const int kind = blockIdx.y;
+  const int64_t hk = a.cache.num_kv_heads;
+  const int64_t nvec = a.num_tokens * hk;
+  const int count = p.exact[kind];
+  const int32_t* list = p.exact + 2 + kind * nvec;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t epoch = a.epoch_counter[1];
+  const float* R = kind == KIND_V ? a.rv : a.rk;
+  const void* src = kind == KIND_K ? a.key : a.value;
+  const int64_t stride = kind == KIND_K ? a.key_stride_token : a.value_stride_token;
+  __shared__ __attribute__((aligned(16))) float s_r[3][ROWS * D];
+  __shared__ __attribute__((aligned(16))) double s_xd[EG][D];
+  __shared__ __attribute__((aligned(16))) float s_x[EG][D];  // quantizer rows
+  __shared__ __attribute__((aligned(16))) float s_y[EG][D];
+  __shared__ int32_t s_id[EG];
+  __shared__ float s_clip[EG];
+  const int col = tid % D, vs = tid / D;
+  auto load_chunk = [&](int c, f32x4* dst) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+      const int e = 4 * (tid + i * kExactThreads);  // element of the chunk, row-major
+      const int k = c * ROWS + e / D, cc = e % D;
+      if (R != nullptr) {
+        dst[i] = *(const f32x4*)(R + (int64_t)k * D + cc);
+      } else {
+        const int o = k - cc;  // identity: 1 where the column equals the row
+        dst[i] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
+      }
+    }
+  };
+  auto store_chunk = [&](int buf, const f32x4* v4) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) *(f32x4*)&s_r[buf][4 * (tid + i * kExactThreads)] = v4[i];
+  };
+  for (int g0 = blockIdx.x * EG; g0 < count; g0 += gridDim.x * EG) {
+    f32x4 ra[F4], rb[F4];
+    load_chunk(0, ra);
+    if (NCH > 1) load_chunk(1, rb);
+    if (tid < EG) s_id[tid] = g0 + tid < count ? list[g0 + tid] : -1;
+    __syncthreads();
+    for (int i = tid; i < EG * D; i += kExactThreads) {
+      const int v = i / D, k = i % D;
+      const int32_t id = s_id[v];
+      s_xd[v][k] = id >= 0 ? (double)load_elem(src, XT, (id / hk) * stride + (id % hk) * D + k) : 0.0;
+    }
+    store_chunk(0, ra);
+    __syncthreads();
+    double acc[VPT];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) acc[v] = 0.0;
+    // one chunk: chunk c + 1 (registers `next`) to its buffer, chunk c + 2 into `free`
+    // (which held chunk c, already stored), then the products of chunk c
+    auto step = [&](int c, f32x4* next, f32x4* free) {
+      if (c + 1 < NCH) store_chunk((c + 1) % 3, next);
+      if (c + 2 < NCH) load_chunk(c + 2, free);
+      const float* rc = s_r[c % 3];
+#pragma unroll 2
+      for (int kk = 0; kk < ROWS; kk += 2) {
+        double r[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) r[j] = (double)rc[(kk + j) * D + col];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          const double* xv = &s_xd[vs * VPT + v][c * ROWS + kk];  // one address per set: broadcast
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[v] = fma(xv[j], r[j], acc[v]);
+        }
+      }
+      __syncthreads();  // chunk c + 1 stored; buffer c % 3 free for chunk c + 3
+    };
+#pragma unroll 1
+    for (int c = 0; c < NCH; c += 2) {
+      step(c, rb, ra);
+      if (c + 1 < NCH) step(c + 1, ra, rb);
+    }
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) s_y[vs * VPT + v][col] = (float)acc[v];
+    __syncthreads();
+    for (int v = wave; v < EG; v += kExactThreads / 64) {
+      const int32_t id = s_id[v];
+      if (id < 0) continue;
+      const int64_t t = id / hk;
+      const Dest d = claimed_dest(p, t, a.slot_mapping[t], a.stage_mode == OSCAR_STAGE_WRITE ? p.flags[t] : 0, epoch);
+      const f32x4 y4 = *(const f32x4*)&s_y[v][4 * (lane < D / 4 ? lane : 0)];
+      quant_vector<D>(p, kind, t, id % hk, d, y4, s_x[v], &s_clip[v]);  // s_x[v]: free row
+    }
+    __syncthreads();  // s_id, s_x, s_r are rewritten by the next group
+  }
+}
+
+template <int D, int XT>
+int launch_large(const StoreParams& p, int cu_count, hipStream_t s) {
+  constexpr int TV = (8 / (D / 32)) * 32;
+  const oscar_store_args_v1& a = p.a;
+  const int64_t kv_vec = a.num_tokens * a.cache.num_kv_heads;
+  const int64_t q_vec = a.query_rot != nullptr ? a.num_tokens * a.num_q_heads : 0;
+  const int64_t total = 2 * ((kv_vec + TV - 1) / TV) + (q_vec + TV - 1) / TV;
+  const int64_t prep_blocks = (a.num_tokens + 255) / 256 + 2 * (D / 32);
+  hipLaunchKernelGGL((store_prep_kernel<D>), dim3((unsigned)prep_blocks), dim3(256), 0, s, p);
+  OSCAR_CHECK_LAUNCH("store_prep_kernel");
+  // one workgroup per compute unit, each over a run of consecutive rounds
+  const int64_t grid = total < cu_count ? total : cu_count;
+  hipLaunchKernelGGL((store_fused_kernel<D, XT>), dim3((unsigned)grid), dim3(kFusedThreads), 0, s, p);
+  OSCAR_CHECK_LAUNCH("store_fused_kernel");
+  // persistent over the device-side counts: per kind at most half the compute units
+  // (the list is a few percent of the vectors plus the window's)
+  int64_t groups = (kv_vec + kExactGroup - 1) / kExactGroup;
+  const int64_t half_cus = cu_count / 2 > 0 ? cu_count / 2 : 1;
+  if (groups > half_cus) groups = half_cus;
+  hipLaunchKernelGGL((store_exact_kernel<D, XT>), dim3((unsigned)groups, 2), dim3(kExactThreads), 0, s, p);
+  OSCAR_CHECK_LAUNCH("store_exact_kernel");
+  return 0;
 }
 
 template <int D>
-int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_t s) {
-  if (p.a.num_tokens <= kFusedTokens && p.scan) {
+int launch_store(const StoreParams& p, int cu_count, hipStream_t s) {
+  const int XT = p.a.kv_dtype;
+  if (p.a.num_tokens <= kFusedTokens) {
     const int64_t hk = p.a.cache.num_kv_heads;
-    const int64_t qg = q_vec ? (p.a.num_q_heads + kQPW - 1) / kQPW : 0;
+    const int64_t qg = p.a.query_rot != nullptr ? (p.a.num_q_heads + kQPW - 1) / kQPW : 0;
     dim3 grid((unsigned)p.a.num_tokens, (unsigned)(2 * hk + qg), (unsigned)(D < kSliceCols ? 1 : D / kSliceCols));
-    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kSmallThreads), 0, s, p);
-    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kSmallThreads), 0, s, p);
+    if (XT == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kSmallThreads), 0, s, p);
+    else if (XT == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kSmallThreads), 0, s, p);
     else hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F32>), grid, dim3(kSmallThreads), 0, s, p);
     OSCAR_CHECK_LAUNCH("store_small_kernel");
     return 0;
   }
-  const int kinds = q_vec ? 3 : 2;
-  const int64_t max_vec = kv_vec > q_vec ? kv_vec : q_vec;
-  if (max_vec >= 4096) {
-    dim3 grid((unsigned)((max_vec + 63) / 64), D / kCols, kinds);
-    launch_rotate<D, 64>(p, grid, s);
-  } else {
-    dim3 grid((unsigned)((max_vec + kSV - 1) / kSV), D / kSC, kinds);
-    dim3 block(kThreads);
-    if (p.a.kv_dtype == OSCAR_BF16) hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_BF16>), grid, block, 0, s, p);
-    else if (p.a.kv_dtype == OSCAR_F16) hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_F16>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((store_rotate_small_kernel<D, OSCAR_F32>), grid, block, 0, s, p);
-  }
-  OSCAR_CHECK_LAUNCH("store_rotate_kernel");
-  dim3 qgrid((unsigned)((kv_vec + 3) / 4), 2);
-  if (p.scan) hipLaunchKernelGGL((store_quant_kernel<D, true>), qgrid, dim3(kThreads), 0, s, p);
-  else hipLaunchKernelGGL((store_quant_kernel<D, false>), qgrid, dim3(kThreads), 0, s, p);
-  OSCAR_CHECK_LAUNCH("store_quant_kernel");
-  return 0;
+  if (XT == OSCAR_BF16) return launch_large<D, OSCAR_BF16>(p, cu_count, s);
+  if (XT == OSCAR_F16) return launch_large<D, OSCAR_F16>(p, cu_count, s);
+  return launch_large<D, OSCAR_F32>(p, cu_count, s);
 }
 
 }  // namespace
@@ -668,9 +1143,34 @@ int launch_store(const StoreParams& p, int64_t kv_vec, int64_t q_vec, hipStream_
 
 using namespace oscar;
 
+// workspace: calls of <= kFusedTokens tokens: y [2][N][Hk][D] fp32 (the column slices);
+// larger calls: the exact-pass lists (2 + 2 N Hk int32) | window flags [N] int32
+static int64_t store_ws_list_bytes(int64_t n, int64_t hk) {
+  return ((2 + 2 * n * hk) * (int64_t)sizeof(int32_t) + 15) / 16 * 16;
+}
+
+static int64_t store_ws_flag_bytes(int64_t n) { return (n * (int64_t)sizeof(int32_t) + 15) / 16 * 16; }
+// fp16 planes of R_k and R_v (2 x D x D x 2 planes x 2 bytes), then bexp and colnorm [2][D] each
+static int64_t store_ws_plane_bytes(int64_t d) { return 8 * d * d + 16 * d; }
+
 extern "C" int64_t oscar_store_workspace_bytes_v1(int64_t num_tokens, int64_t num_kv_heads,
                                                  int64_t head_dim) {
-  return 2 * num_tokens * num_kv_heads * head_dim * (int64_t)sizeof(float);
+  if (num_tokens <= kFusedTokens) return 2 * num_tokens * num_kv_heads * head_dim * (int64_t)sizeof(float);
+  return store_ws_list_bytes(num_tokens, num_kv_heads) + store_ws_flag_bytes(num_tokens) +
+         store_ws_plane_bytes(head_dim);
+}
+
+// compute units of the current device (cached per device)
+static int current_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int cu = cache[dev].load(std::memory_order_relaxed);
+  if (cu <= 0) {
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0) cu = 256;
+    cache[dev].store(cu, std::memory_order_relaxed);
+  }
+  return cu;
 }
 
 extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
@@ -732,12 +1232,18 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
     return fail(-22, "oscar_store_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
   if (a.num_tokens <= kFusedTokens && (a.arrivals == nullptr || (((uintptr_t)a.arrivals) & 3)))
     return fail(-22, "oscar_store_v1: calls of <= %lld tokens need the arrivals counters", (long long)kFusedTokens);
-  StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size,
-                a.num_tokens <= kScanTokens};
-  const int64_t kv_vec = a.num_tokens * a.cache.num_kv_heads;
-  const int64_t q_vec = (a.query_rot != nullptr) ? a.num_tokens * a.num_q_heads : 0;
+  if (2 * a.num_tokens * a.cache.num_kv_heads >= (1ll << 31))
+    return fail(-22, "oscar_store_v1: num_tokens x num_kv_heads too large for one call");
+  StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size};
+  uint8_t* ws = (uint8_t*)a.workspace;
+  p.exact = (int32_t*)ws;
+  p.flags = (int32_t*)(ws + store_ws_list_bytes(a.num_tokens, a.cache.num_kv_heads));
+  p.planes = (u32x4*)((uint8_t*)p.flags + store_ws_flag_bytes(a.num_tokens));
+  p.bexp = (int32_t*)(p.planes + D * D / 2);
+  p.colnorm = (float*)(p.bexp + 2 * D);
+  const int cu = a.num_tokens <= kFusedTokens ? 0 : current_cu_count();
   hipStream_t s = (hipStream_t)stream;
-  if (D == 256) return launch_store<256>(p, kv_vec, q_vec, s);
-  if (D == 128) return launch_store<128>(p, kv_vec, q_vec, s);
-  return launch_store<64>(p, kv_vec, q_vec, s);
+  if (D == 256) return launch_store<256>(p, cu, s);
+  if (D == 128) return launch_store<128>(p, cu, s);
+  return launch_store<64>(p, cu, s);
 }

@@ -278,7 +278,11 @@ def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(
     assert lib.oscar_store_v1(C.byref(s), None) == -22
     s = _lib.StoreArgs(num_tokens=0)
     assert lib.oscar_store_v1(C.byref(s), None) == 0
+    # <= 64 tokens: the column slices y [2][N][Hk][D] fp32
     assert lib.oscar_store_workspace_bytes_v1(10, 2, 256) == 2 * 10 * 2 * 256 * 4
+    # larger: exact lists (2 + 2 N Hk int32, 16-B padded) + window flags [N] int32 + fp16
+    # planes of R_k and R_v (8 D^2 bytes) + column exponents and norms (16 D bytes)
+    assert lib.oscar_store_workspace_bytes_v1(100, 2, 256) == 1616 + 400 + 8 * 256 * 256 + 16 * 256
 
 
 def decode_args(**kw):
