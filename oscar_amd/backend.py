@@ -30,6 +30,7 @@ import torch
 from . import _lib, ops
 from ._lib import STAGE_INVALIDATE, STAGE_NONE, STAGE_WRITE
 from .config import OscarConfig
+from .integration import arena_rows
 from .format import K_IDX_OFF, VALUES_PER_BYTE, check_d
 from .rotation import get_layer_rotation
 
@@ -238,9 +239,7 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         bs = kv_cache[0].shape[1]
         self.stage_block = bs
         self.sink_eff = cfg.sink_tokens - cfg.sink_tokens % bs   # whole sink pages only
-        self.sink_pages = self.sink_eff // bs
-        self.tail_pages = -(-cfg.recent_tokens // bs) + 1
-        rows = max(-(-cfg.staging_tokens // bs), self.sink_pages + self.tail_pages + 2)
+        rows = arena_rows(cfg, bs)
         dev = kv_cache[0].device
         shape = (rows, bs, self.num_kv_heads, self.head_size)
         layer._oscar_stage_k = torch.zeros(shape, dtype=torch.float32, device=dev)

@@ -4,8 +4,11 @@
 ``vllm.model_executor.layers.attention.attention.Attention.__init__``; after a
 layer is constructed, FULL decoder layers of hybrid models have their
 ``impl.__class__`` swapped to ``OscarAttentionBackendImpl`` (class surgery that
-is rolled back if setup raises).  MTP draft layers, non-decoder layers, sliding
-windows and attention sinks are left on the native path.
+is rolled back if setup raises).  Non-decoder layers, sliding windows and attention
+sinks are left on the native path; MTP draft layers stay native too, in front of a
+bf16 shadow of the int8 pool (``oscar_amd.mtp_shadow``).  The worker hooks of
+``oscar_amd.integration`` (memory budget, cache initialization, READY manifest) are
+installed alongside when the worker classes import.
 
 Entry point to register (pyproject):
     [project.entry-points."vllm.general_plugins"]
@@ -15,7 +18,7 @@ from __future__ import annotations
 
 import os
 
-_HEARTBEAT: dict = {"loaded": 0, "layers": [], "errors": []}
+_HEARTBEAT: dict = {"loaded": 0, "layers": [], "shadow_layers": [], "errors": []}
 _PATCHED = False
 _SKIP_REASONS_LOGGED: set = set()
 
@@ -84,6 +87,22 @@ def _should_oscar(layer, impl, model_config=None) -> bool:
     return not reasons
 
 
+def _wants_shadow(layer, model_config=None) -> bool:
+    """MTP draft layers of models whose FULL layers OSCAR takes get the bf16 shadow pool
+    (their native attention cannot use the int8 pool geometry)."""
+    if not _is_mtp_draft(getattr(layer, "layer_name", "") or ""):
+        return False
+    try:
+        if model_config is None:
+            from vllm.config import get_current_vllm_config
+
+            model_config = get_current_vllm_config().model_config
+        return hybrid_model(model_config)
+    except Exception as e:  # pragma: no cover - reported, the layer stays native
+        _HEARTBEAT["errors"].append(f"shadow routing: {e}")
+        return False
+
+
 def _patch_attention_class(attention_cls, target_class=None) -> None:
     """Wrap ``attention_cls.__init__`` with the OSCAR after-hook."""
     orig_init = attention_cls.__init__
@@ -91,7 +110,15 @@ def _patch_attention_class(attention_cls, target_class=None) -> None:
     def _patched_init(self, *args, **kwargs):
         orig_init(self, *args, **kwargs)
         impl = getattr(self, "impl", None)
-        if impl is None or not _should_oscar(self, impl):
+        if impl is None:
+            return None
+        if _wants_shadow(self):
+            from .mtp_shadow import install_shadow
+
+            install_shadow(impl)  # native bf16 attention on a bf16 shadow of the int8 pool
+            _HEARTBEAT["shadow_layers"].append(getattr(self, "layer_name", "?"))
+            return None
+        if not _should_oscar(self, impl):
             return None
         try:
             from .backend import OscarAttentionBackendImpl
@@ -128,6 +155,14 @@ def load_plugin() -> None:
     _patch_attention_class(Attention)
     _PATCHED = True
     print("[oscar-amd] plugin installed: Attention.__init__ after-hook")
+    try:
+        from .integration import install_runner_hooks
+
+        install_runner_hooks()
+        print("[oscar-amd] worker hooks installed: memory budget, cache initialization, READY manifest")
+    except Exception as e:  # a worker without these seams keeps lazy arenas
+        _HEARTBEAT["errors"].append(f"worker hooks: {e}")
+        print(f"[oscar-amd] worker hooks not installed: {e}")
 
 
 def heartbeat() -> dict:
