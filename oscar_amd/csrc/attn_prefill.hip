@@ -19,8 +19,9 @@
 //                        32 are double-buffered in LDS: each thread prefetches its
 //                        share of tile t+2 into registers while tile t is computed, so
 //                        one barrier per tile separates the buffers.  Per wave:
-//                        S^T = K Q^T (v_mfma_f32_32x32x16_bf16), online softmax in fp32
-//                        (log2 domain) with a lazy reference max, O^T += V^T P^T with
+//                        S^T = K Q^T (v_mfma_f32_32x32x16_bf16 / _f16), online softmax
+//                        in fp32 (log2 domain) with a lazy reference max, O^T += V^T P^T
+//                        on v_mfma_f32_32x32x16_f16 (P and V in fp16, see kVShift) with
 //                        V^T read from LDS by ds_read_b64_tr_b16.
 #include "common.h"
 
@@ -36,6 +37,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.f;  // max drift (log2 units) before O is rescaled
 constexpr int kQK = 4;        // QK K-steps whose LDS operands are read together
+// PV runs on v_mfma_f32_32x32x16_f16 with P and V in fp16 for both query dtypes.  bf16
+// V values (8-bit significands) are held as fp16(v * 2^-kVShift): exact for |v| from
+// 2^-6 up to 2^23 (below, within 2^-17 absolutely), and O is scaled back by 2^kVShift.
+constexpr int kVShift = 8;
 typedef short __attribute__((ext_vector_type(4))) i16x4;
 typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
 typedef _Float16 __attribute__((ext_vector_type(2))) f16x2;
@@ -53,6 +58,13 @@ template <int QT>
 __device__ __forceinline__ unsigned q_bits(float x) {
   if constexpr (QT == OSCAR_F16) return f32_to_f16_bits(x);
   else return f32_to_bf16_bits(x);
+}
+// the PV operand bits of a value v already in the query dtype: fp16 as it is; a bf16
+// value scaled by 2^-kVShift into fp16 (exact, see kVShift)
+template <int QT>
+__device__ __forceinline__ unsigned pv_bits(float v) {
+  if constexpr (QT == OSCAR_F16) return f32_to_f16_bits(v);
+  else return f32_to_f16_bits(v * (1.f / (1 << kVShift)));
 }
 template <int QT> struct QVec { typedef bf16x8 type; typedef bf16x2 pair; typedef __bf16 elem; };
 template <> struct QVec<OSCAR_F16> { typedef f16x8 type; typedef f16x2 pair; typedef _Float16 elem; };
@@ -112,7 +124,12 @@ __global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
 #pragma unroll
   for (int i = 0; i < E / 2; ++i) {
     kw[i] = hist_bits<QT>(kv[2 * i]) | (hist_bits<QT>(kv[2 * i + 1]) << 16);
-    vw[i] = hist_bits<QT>(vv[2 * i]) | (hist_bits<QT>(vv[2 * i + 1]) << 16);
+    // V: the reference's history value in the query dtype, then the PV operand bits
+    const unsigned v0 = hist_bits<QT>(vv[2 * i]), v1 = hist_bits<QT>(vv[2 * i + 1]);
+    auto as_float = [](unsigned b) {
+      return QT == OSCAR_F16 ? f16_bits_to_f32((unsigned short)b) : bf16_bits_to_f32((unsigned short)b);
+    };
+    vw[i] = pv_bits<QT>(as_float(v0)) | (pv_bits<QT>(as_float(v1)) << 16);
   }
   uint16_t* dk = P.hist_k + vec * D + E * lane;
   uint16_t* dv = P.hist_v + vec * D + E * lane;
@@ -128,8 +145,6 @@ __global__ __launch_bounds__(256) void history_bf16_kernel(PrefillParams P) {
 template <int D, int QT>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   using QV = typename QVec<QT>::type;    // one MFMA operand in the query dtype
-  using QP = typename QVec<QT>::pair;
-  using QE = typename QVec<QT>::elem;
   const oscar_prefill_args_v1& A = P.a;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = lane & 31, g = lane >> 5;
@@ -158,6 +173,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   constexpr int NPASS = kKeys / KPP;
   const int fkey = tid / CPR, fcol = tid % CPR;
   u32x4 kr[NPASS], vr[NPASS];
+  bool vcur[NPASS];  // the V row is a current-chunk row (query dtype, not PV format)
   // branch-free, 32-bit element offsets (the host checks they fit): keys past the
   // chunk read current-chunk row 0, finite data whose scores the causal mask removes
   const uint16_t* hk_base = P.hist_k + kvh * D + 8 * fcol;
@@ -176,13 +192,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       const uint16_t* vs = in_hist ? hv_base + (unsigned)(p * hrow) : cv_base + (unsigned)(ci * crow);
       kr[i] = *(const u32x4*)ks;
       vr[i] = *(const u32x4*)vs;
+      vcur[i] = !in_hist;
     }
   };
   auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < NPASS; ++i) {
       *(u32x4*)&s_k[buf][i * KPP + fkey][8 * fcol] = kr[i];
-      *(u32x4*)&s_v[buf][i * KPP + fkey][8 * fcol] = vr[i];
+      u32x4 w = vr[i];
+      if constexpr (QT == OSCAR_BF16) {
+        if (vcur[i]) {  // bf16 current-chunk values to the PV format
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = pv_bits<QT>(__uint_as_float(vr[i][e] << 16)) | (pv_bits<QT>(__uint_as_float(vr[i][e] & 0xffff0000u)) << 16);
+        }
+      }
+      *(u32x4*)&s_v[buf][i * KPP + fkey][8 * fcol] = w;
     }
   };
 
@@ -266,21 +291,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       }
       // p = 2^(S c - m) (exp2 of -inf is 0); rows with no key yet keep m = -inf and p = 0
       const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
-      // P = hi + lo, both in the query dtype (the pair carries ~16 bits of p or more)
-      QV pb[2], pl[2];
+      // P in fp16 (p <= 2^kLazy; relative error 2^-12 per element)
+      f16x8 pb[2];
       float lsum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(S[r], c, nm));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(S[r + 1], c, nm));
         lsum += p0 + p1;
-        const QP h = __builtin_convertvector(f32x2{p0, p1}, QP);
-        const f32x2 hf = __builtin_convertvector(h, f32x2);
-        const QP lo = __builtin_convertvector(f32x2{p0 - hf[0], p1 - hf[1]}, QP);
+        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
         pb[r >> 3][r & 7] = h[0];
         pb[r >> 3][(r & 7) + 1] = h[1];
-        pl[r >> 3][r & 7] = lo[0];
-        pl[r >> 3][(r & 7) + 1] = lo[1];
       }
       l_run += lsum;
       // ---- O^T += V^T P^T; the V^T operands of two output blocks (8 transpose reads)
@@ -288,7 +309,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       const int G16 = lane >> 4, i16 = lane & 15;
 #pragma unroll
       for (int b0 = 0; b0 < D / 32; b0 += 2) {
-        QV va[2][2];
+        f16x8 va[2][2];
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
@@ -299,22 +320,15 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
               const uint16_t* addr = &s_v[buf][key][32 * (b0 + bb) + 16 * (G16 & 1) + 4 * (i16 & 3)];
               auto t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(addr));
 #pragma unroll
-              for (int e = 0; e < 4; ++e) va[bb][s][4 * h + e] = __builtin_bit_cast(QE, (unsigned short)t[e]);
+              for (int e = 0; e < 4; ++e) va[bb][s][4 * h + e] = __builtin_bit_cast(_Float16, (unsigned short)t[e]);
             }
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            if constexpr (QT == OSCAR_F16) {
-              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
-              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
-            } else {
-              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
-              O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[bb][s], pl[s], O[b0 + bb], 0, 0, 0);
-            }
-          }
+          for (int s = 0; s < 2; ++s)
+            O[b0 + bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bb][s], pb[s], O[b0 + bb], 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
       }
       // the prefetched tile kt+1 goes to the other buffer (last read before the previous
       // barrier), then tile kt+2 is prefetched; one barrier per tile
@@ -342,7 +356,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
     l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
   if (!row_ok) return;
-  const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+  // O back from the PV scale of bf16 V values (a power of two: exact)
+  const float inv = (l_tot > 0.f) ? (QT == OSCAR_F16 ? 1.f : (float)(1 << kVShift)) / l_tot : 0.f;
   const int64_t obase = qi * A.out_stride_token + (int64_t)head * D;
 #pragma unroll
   for (int b = 0; b < D / 32; ++b)
