@@ -108,15 +108,16 @@ typedef struct oscar_store_args_v1 {
   void* value_rot;              /* x @ R_v, unclipped (may be NULL) */
   /* scratch: last-writer claims, entries (epoch << 24 | token), num_tokens < 2^24;
    * zero-initialised once.
-   * The call's epoch is epoch_counter[0] + 1: the first launch stores it in
-   * epoch_counter[1], the second copies it to epoch_counter[0], so replays of a
-   * captured graph always claim with a fresh epoch (no host round trip). */
+   * The call's epoch is epoch_counter[0] + 1: the first launch of a call of more
+   * than 64 tokens stores it in epoch_counter[1], the next copies it to
+   * epoch_counter[0], so replays of a captured graph always claim with a fresh epoch
+   * (no host round trip).  Calls of <= 64 tokens find last writers by scanning. */
   int64_t* slot_claims;         /* [num_blocks * block_size] */
   int64_t* seat_claims;         /* [rows * block_size] (stage mode 2) */
   int64_t* epoch_counter;       /* device int64[2], zero-initialised once, shared per device */
-  /* fp32 rotated K/V between rotation and quantization (between the two launches of
-   * a large call, between the column-slice workgroups of a call of <= 64 tokens),
-   * 16-byte aligned, >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim) */
+  /* 16-byte aligned, >= oscar_store_workspace_bytes_v1(num_tokens, num_kv_heads, head_dim):
+   * calls of <= 64 tokens pass their fp32 column slices through it; larger calls keep
+   * the exact-pass lists, the per-token window flags and the fp16 planes of R_k / R_v */
   void* workspace;
   int64_t workspace_bytes;
   /* calls of <= 64 tokens: one arrival counter per K / V vector, uint32
