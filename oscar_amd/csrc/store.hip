@@ -32,17 +32,30 @@ namespace {
 
 enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
 
+// workgroups of the fused launch per kind at most (bounds the per-workgroup exact counts)
+constexpr int kMaxFusedGroups = 1024;
+
 struct StoreParams {
   oscar_store_args_v1 a;
   float* y;          // small calls: workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
   int64_t capacity;  // num_blocks * block_size
-  int32_t* exact;    // large calls: [0] K count, [1] V count, [2 + kind * nvec + i] vectors
-                     // left to the exact pass (nvec = num_tokens * num_kv_heads)
+  int32_t* exact;    // large calls: [0] K total, [1] V total (written by the exact pass),
+                     // [2 + kind * kMaxFusedGroups + w] vectors workgroup w of the fused launch
+                     // left to the exact pass, then the lists [kind][nvec] (nvec = num_tokens *
+                     // num_kv_heads): workgroup w's entries start at its first vector
   int32_t* flags;    // large calls: [num_tokens] bit 0 = position inside the window
   u32x4* planes;     // large calls: R_k, R_v as fp16 MFMA B fragments [2][D/32][D/16][2][64]
   int32_t* bexp;     // large calls: [2][D] power-of-two column scale of the planes
   float* colnorm;    // large calls: [2][D] ||R_:d||
+  int32_t fused_kv_groups;  // large calls: fused workgroups per kind for K and for V
 };
+
+__device__ __forceinline__ int32_t* exact_counts(const StoreParams& p, int kind) {
+  return p.exact + 2 + kind * kMaxFusedGroups;
+}
+__device__ __forceinline__ int32_t* exact_list(const StoreParams& p, int kind, int64_t nvec) {
+  return p.exact + 2 + 2 * kMaxFusedGroups + kind * nvec;
+}
 
 __device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
   // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
@@ -95,6 +108,7 @@ __device__ float clip_threshold(const float* row, int idx, volatile float* slot)
 // recent window (backend.py:536-541: keep the FP32 copy, else drop the seat).
 struct Dest {
   int64_t slot, seat;
+  int64_t koff, voff;  // fused kernel: byte offsets of the K and V slots in the caches
   bool valid, slot_win, seat_win, keep;
 };
 
@@ -390,13 +404,18 @@ template <int CTRL>
 __device__ __forceinline__ int dpp_row_i(int x) {
   return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);
 }
-template <bool MAX>
-__device__ __forceinline__ float row_extreme(float x) {
-  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); };
-  x = op(x, dpp_row<kDppXor1>(x));
-  x = op(x, dpp_row<kDppXor2>(x));
-  x = op(x, dpp_row<kDppHalfMirror>(x));
-  return op(x, dpp_row<kDppMirror>(x));
+// NaN-propagating minimum / maximum over the 16-lane row
+__device__ __forceinline__ float row_minimum(float x) {
+  x = __builtin_elementwise_minimum(x, dpp_row<kDppXor1>(x));
+  x = __builtin_elementwise_minimum(x, dpp_row<kDppXor2>(x));
+  x = __builtin_elementwise_minimum(x, dpp_row<kDppHalfMirror>(x));
+  return __builtin_elementwise_minimum(x, dpp_row<kDppMirror>(x));
+}
+__device__ __forceinline__ float row_maximum(float x) {
+  x = __builtin_elementwise_maximum(x, dpp_row<kDppXor1>(x));
+  x = __builtin_elementwise_maximum(x, dpp_row<kDppXor2>(x));
+  x = __builtin_elementwise_maximum(x, dpp_row<kDppHalfMirror>(x));
+  return __builtin_elementwise_maximum(x, dpp_row<kDppMirror>(x));
 }
 __device__ __forceinline__ int row_sum(int x) {
   x += dpp_row_i<kDppXor1>(x);
@@ -428,87 +447,94 @@ __device__ float row_kth_abs(const float* y, int idx) {
   return __uint_as_float(v);
 }
 
-// Certify and quantize the rows' vectors from y~ (lane: y[E] of its row's vector, e[E]
-// the bound on |y~ - y| of each element).  Every decision the quantizer takes -- the
-// sort-clip threshold (order statistics move by at most max e), the fp16 scale and
-// zero (from the intervals of vmin and vmax) and each code -- is evaluated at both ends
-// of y~ +- e; the quantizer's steps are monotone, so equal ends mean y gives the same
-// bytes.  Certified rows with write != 0 store their codes and meta (K slot kslot + 32 /
-// V slot vslot); the function returns whether this lane's row was certified.
+// Certify and quantize the rows' vectors from y~ (lane: y[E] of its row's vector).  The
+// bound on |y~_j - y_j| is taken row-uniform: eb = ex + 2^-22 max_j |y~_j| (ex: the row's
+// rotation term plus 2^-126), at least every element's own bound.  Every decision the
+// quantizer takes -- the sort-clip threshold (order statistics move by at most eb), the
+// fp16 scale and zero (from the intervals of vmin and vmax) and each code -- is evaluated
+// over the whole interval y~ +- eb; the quantizer's steps are monotone, so one outcome
+// over the interval means y gives the same bytes.  Certified rows with write != 0 store
+// their codes and meta (K slot kslot + 32 / V slot vslot); the function returns whether
+// this lane's row was certified.
 template <int D>
-__device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, const float* e,
+__device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, float ex,
                                 bool write, uint8_t* kslot, uint8_t* vslot) {
   constexpr int E = D / 16;
   const int l = threadIdx.x & 15;
   const float clip = kind == KIND_K ? p.a.k_clip_ratio : p.a.v_clip_ratio;
-  bool finite = true;
-  float emax = 0.f;
+  // row extremes with NaN-propagating minimum / maximum: a NaN or inf anywhere makes eb
+  // NaN or inf, and the row goes to the exact pass (which reproduces the reference)
+  float vmin = y[0], vmax = y[0];
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    finite &= __builtin_isfinite(y[j]) && __builtin_isfinite(e[j]);
-    emax = fmaxf(emax, e[j]);
+  for (int j = 1; j < E; ++j) {
+    vmin = __builtin_elementwise_minimum(vmin, y[j]);
+    vmax = __builtin_elementwise_maximum(vmax, y[j]);
   }
-  if (!row_all(finite)) return false;  // NaN / inf: the exact pass reproduces the reference
-  emax = row_extreme<true>(emax);
+  vmin = row_minimum(vmin);
+  vmax = row_maximum(vmax);
+  const float eb = ex + __builtin_elementwise_maximum(fabsf(vmin), fabsf(vmax)) * 0x1p-22f;
+  if (!row_all(eb <= 0x1.fffffep127f)) return false;
   float t_lo = INFINITY, t_hi = INFINITY;
   if (clip > 0.f) {
     int idx = (int)(clip * (float)D);
     if (idx > D - 1) idx = D - 1;
     const float t = row_kth_abs<E>(y, idx);
-    const float et = emax + t * 0x1p-22f;
+    const float et = eb + t * 0x1p-22f;
     t_lo = fmaxf(t - et, 0.f);
     t_hi = t + et;
   }
-  float lo[E], hi[E];
-  float vmin_lo = INFINITY, vmin_hi = INFINITY, vmax_lo = -INFINITY, vmax_hi = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < E; ++j) {
-    lo[j] = y[j] - e[j];
-    hi[j] = y[j] + e[j];
-    if (clip > 0.f) {
-      lo[j] = fmaxf(-t_hi, fminf(lo[j], t_lo));
-      hi[j] = fmaxf(-t_lo, fminf(hi[j], t_hi));
-    }
-    vmin_lo = fminf(vmin_lo, lo[j]);
-    vmin_hi = fminf(vmin_hi, hi[j]);
-    vmax_lo = fmaxf(vmax_lo, lo[j]);
-    vmax_hi = fmaxf(vmax_hi, hi[j]);
-  }
-  vmin_lo = row_extreme<false>(vmin_lo);
-  vmin_hi = row_extreme<false>(vmin_hi);
-  vmax_lo = row_extreme<true>(vmax_lo);
-  vmax_hi = row_extreme<true>(vmax_hi);
+  // the ends of an element's interval, clipped like the values themselves: lower ends
+  // into [-t_hi, t_lo], upper ends into [-t_lo, t_hi]; clipping and rounding are
+  // monotone, so the row extremes of the ends are the ends of the row extremes
+  auto lo_of = [&](float v) { return clip > 0.f ? fminf(fmaxf(v - eb, -t_hi), t_lo) : v - eb; };
+  auto hi_of = [&](float v) { return clip > 0.f ? fminf(fmaxf(v + eb, -t_lo), t_hi) : v + eb; };
+  const float vmin_lo = lo_of(vmin), vmin_hi = hi_of(vmin), vmax_lo = lo_of(vmax), vmax_hi = hi_of(vmax);
   const unsigned short s_a = scale_bits_of(vmax_lo, vmin_hi), s_b = scale_bits_of(vmax_hi, vmin_lo);
   const unsigned short z_a = f32_to_f16_bits(vmin_lo), z_b = f32_to_f16_bits(vmin_hi);
   // a zero of either sign is left to the exact pass: its sign bit follows y exactly
   if (s_a != s_b || z_a != z_b || (z_a & 0x7fff) == 0) return false;  // row-uniform
   const float s16 = f16_bits_to_f32(s_a), z16 = f16_bits_to_f32(z_a);
-  // codes at both ends: q = (x - z) * (1 / s) is within a few ulp of the quantizer's
-  // RN(RN(x - z) / s), so floor(q + 0.5 -+ m) with the margin m = 2^-19 max(|q|, 1) (which
-  // also covers the rounding of + 0.5) brackets both ends' codes; only where the bracket
-  // is not one code are the exact divisions evaluated
   const float inv = __builtin_amdgcn_rcpf(s16);
-  int code[E];
-  bool same = true;
+  // every element's q = (x - z) / s lies within the row's [q(vmin_lo), q(vmax_hi)]
+  const float qm = fmaxf(fmaxf(fabsf((vmin_lo - z16) * inv), fabsf((vmax_hi - z16) * inv)), 1.f);
+  if (!(qm <= 0x1p20f)) return false;  // also inf / NaN zero or scale (row-uniform)
+  // Codes.  An element's (clipped) value lies within ew of its center yc (clipping is
+  // 1-Lipschitz in the value and in the threshold, whose center is tc).  The quantizer's
+  // RN(RN(x - z) / s) + 0.5 for any x there is within w = ew (1 / s) + 2^-19 max(|q|, 1)
+  // of t = fma(yc - z, 1 / s, 0.5) (a few ulp of rounding, and 1 / s within one ulp), so
+  // where t is farther than w from every integer, all of them share floor(t)'s code.
+  const float tc = clip > 0.f ? 0.5f * (t_lo + t_hi) : INFINITY;
+  const float ew = clip > 0.f ? eb + (0.5f * (t_hi - t_lo) + tc * 0x1p-22f) * (1.f + 0x1p-20f) : eb;
+  const float w = ew * inv * (1.f + 0x1p-20f) + 0x1p-19f * qm;
+  auto center = [&](int j) { return fmaf((clip > 0.f ? fminf(fmaxf(y[j], -tc), tc) : y[j]) - z16, inv, 0.5f); };
+  auto code_at = [&](float t) {  // floor(t) clamped to [0, 3] (t truncated: equal after clamping)
+    const int c = (int)t;
+    return c < 0 ? 0 : (c > 3 ? 3 : c);
+  };
+  uint32_t packed = 0;  // byte b holds elements 4b..4b+3, two bits each (format.py:84-87)
+  float nearest = INFINITY;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const float ql = (lo[j] - z16) * inv, qh = (hi[j] - z16) * inv;
-    const float ml = 0x1p-19f * fmaxf(fabsf(ql), 1.f), mh = 0x1p-19f * fmaxf(fabsf(qh), 1.f);
-    const int cl = (int)fminf(fmaxf(floorf(ql + 0.5f - ml), 0.f), 3.f);
-    const int ch = (int)fminf(fmaxf(floorf(qh + 0.5f + mh), 0.f), 3.f);
-    if (cl == ch) {
-      code[j] = cl;
-    } else {
-      code[j] = code_of(lo[j], z16, s16);
-      same &= code[j] == code_of(hi[j], z16, s16);
+    const float t = center(j);
+    nearest = __builtin_elementwise_minimum(nearest, fabsf(t - rintf(t)));
+    packed |= (uint32_t)code_at(t) << (2 * j);
+  }
+  bool same = true;
+  if (!(nearest > w)) {  // an element near a code boundary: the exact codes at both ends
+    packed = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const float t = center(j);
+      int code = code_at(t);
+      if (!(fabsf(t - rintf(t)) > w)) {
+        code = code_of(lo_of(y[j]), z16, s16);
+        same &= code == code_of(hi_of(y[j]), z16, s16);
+      }
+      packed |= (uint32_t)code << (2 * j);
     }
   }
   if (!row_all(same)) return false;
   if (write) {
-    // byte b holds the codes of elements 4b..4b+3, two bits each (format.py:84-87)
-    uint32_t packed = 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) packed |= (uint32_t)code[j] << (2 * j);
     uint8_t* dst = (kind == KIND_K ? kslot + 32 : vslot) + l * (E / 4);
     if constexpr (E == 16) *(uint32_t*)dst = packed;
     else if constexpr (E == 8) *(uint16_t*)dst = (uint16_t)packed;
@@ -551,7 +577,7 @@ __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, 
 // cannot hold exactly after scaling add < 2^-28 of the bound.
 constexpr int kFusedThreads = 512;  // 8 waves
 constexpr int kChainSteps = 4;      // K-steps per accumulation chain
-constexpr int kExactThreads = 1024;
+constexpr int kExactThreads = 512;
 constexpr int kExactGroup = 8;      // vectors per exact-pass group
 constexpr int kExactBuffer = 512;   // exact-pass vectors a fused workgroup gathers in LDS
 constexpr int kReqLds = 2048;       // request tables of up to this many entries go to LDS
@@ -629,11 +655,7 @@ __global__ __launch_bounds__(256) void store_prep_kernel(StoreParams p) {
   }
   const int64_t e0 = a.epoch_counter[0];
   const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    a.epoch_counter[1] = epoch;
-    p.exact[0] = 0;
-    p.exact[1] = 0;
-  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[1] = epoch;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const bool lds = window && a.num_reqs <= kReqLds;
   __shared__ int32_t s_qsl[kReqLds + 1];
@@ -721,6 +743,28 @@ struct XChunk {
   }
 };
 
+// max / sum over aligned groups of N consecutive lanes (N = 4, 8, 16); every lane of a
+// group receives the same value (each step combines two equal-shaped halves, and + is
+// commutative)
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(N == 4 || N == 8 || N == 16, "group size");
+  x = fmaxf(x, dpp_row<kDppXor1>(x));
+  x = fmaxf(x, dpp_row<kDppXor2>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp_row<kDppHalfMirror>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_row<kDppMirror>(x));
+  return x;
+}
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 4 || N == 8 || N == 16, "group size");
+  x += dpp_row<kDppXor1>(x);
+  x += dpp_row<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp_row<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_row<kDppMirror>(x);
+  return x;
+}
+
 template <int D, int XT>
 __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams p) {
   constexpr int KS = D / 16;               // K-steps
@@ -738,14 +782,25 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   const int64_t hk = a.cache.num_kv_heads;
   const int64_t kv_vec = a.num_tokens * hk;
   const int64_t q_vec = a.query_rot != nullptr ? a.num_tokens * a.num_q_heads : 0;
-  const int64_t rounds_kv = (kv_vec + TV - 1) / TV, rounds_q = (q_vec + TV - 1) / TV;
-  const int64_t total = 2 * rounds_kv + rounds_q;
-  const int64_t per = (total + gridDim.x - 1) / gridDim.x;
-  const int64_t it0 = (int64_t)blockIdx.x * per;
-  const int64_t it1 = it0 + per < total ? it0 + per : total;
+  // this workgroup's kind and run of rounds: workgroups [0, g) take the key rounds,
+  // [g, 2 g) the value rounds and the rest the query rounds (g = p.fused_kv_groups)
+  const int64_t gkv = p.fused_kv_groups;
+  const int64_t b = blockIdx.x;
+  const int kind = b < gkv ? KIND_K : (b < 2 * gkv ? KIND_V : KIND_Q);
+  const int64_t wg = kind == KIND_K ? b : (kind == KIND_V ? b - gkv : b - 2 * gkv);
+  const int64_t nwg = kind == KIND_Q ? (int64_t)gridDim.x - 2 * gkv : gkv;
+  const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
+  const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
+  const int64_t rounds = (nvec + TV - 1) / TV;
+  const int64_t per = (rounds + nwg - 1) / nwg;
+  const int64_t it0 = wg * per, it1 = it0 + per < rounds ? it0 + per : rounds;
+  const int which = kind == KIND_V ? 1 : 0;  // R_v for values, R_k for keys and queries
+  const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
+  const int64_t stride = kind == KIND_K ? a.key_stride_token
+                       : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
+  void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const int64_t epoch = a.epoch_counter[1];
-  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[0] = epoch;
-  if (it0 >= it1) return;
 
   const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -753,96 +808,95 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   const int col = 32 * cb + m;               // this lane's output column
 
   __shared__ u32x4 s_a[XP][RG][KS][64];      // A fragments (fp16), MFMA lane order
-  __shared__ __attribute__((aligned(16))) float s_y[TV][YS];
+  // y tile, norms and destinations by round parity (one round is quantized while the
+  // next one's y is formed)
+  __shared__ __attribute__((aligned(16))) float s_y[2][TV][YS];
   __shared__ int s_ax[TV];                   // per-vector exponent of x
-  __shared__ float s_nx[TV];                 // ||x||
+  __shared__ float s_nx[2][TV];              // ||x||
   __shared__ __attribute__((aligned(16))) float s_cn[D];  // ||R_:d||
-  __shared__ long long s_slot[TV];
-  __shared__ Dest s_dest[TV];
+  __shared__ Dest s_dest[2][TV];
+  __shared__ int s_xn;                       // vectors this workgroup left to the exact pass
+  if (tid == 0) s_xn = 0;
 
-  // an item is one round of one kind: K rounds, V rounds, then query rounds
-  auto item_kind = [&](int64_t it) { return it < rounds_kv ? KIND_K : (it < 2 * rounds_kv ? KIND_V : KIND_Q); };
-  auto item_base = [&](int64_t it) {
-    return (it < rounds_kv ? it : (it < 2 * rounds_kv ? it - rounds_kv : it - 2 * rounds_kv)) * TV;
-  };
+  // every load below is issued unconditionally (indexes clamped into range, results
+  // masked at use), so the waits before their uses count exactly the loads issued since
   const int sv = tid / TPV, sq = tid % TPV;  // staging: vector, 16-element chunk
+  // vector indexes fit in 31 bits (checked on the host): 32-bit division
+  const uint32_t heads32 = (uint32_t)heads, hk32 = (uint32_t)hk;
   auto load_x = [&](int64_t it, XChunk<XT>& xc) {
-    const int kind = item_kind(it);
-    const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
-    const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
-    const int64_t vec = item_base(it) + sv;
-    const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
-    const int64_t stride = kind == KIND_K ? a.key_stride_token
-                         : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
-    if (vec < nvec) xc.load(src, (vec / heads) * stride + (vec % heads) * D + 16 * sq);
-    else xc.zero();
+    const int64_t vec = it * TV + sv;
+    const uint32_t vc = (uint32_t)(vec < nvec ? vec : nvec - 1);
+    xc.load(src, (int64_t)(vc / heads32) * stride + (vc % heads32) * D + 16 * sq);
   };
-
-  // ---- B: R's 32-column block in registers, the two fp16 planes written by the prep
-  // kernel (lane (n, g) of K-step s: R[16 s + 8 g + j][col] * 2^bcol, j < 8)
-  u32x4 b0[KS], b1[KS];
-  int bcol = 0;
-  int rkind = -1;  // 0: R_k (K and query rounds), 1: R_v
-  auto load_b = [&](int which) {
-    const u32x4* src = p.planes + ((int64_t)(which * CW + cb) * KS) * 2 * 64 + lane;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      b0[s] = src[(2 * s) * 64];
-      b1[s] = src[(2 * s + 1) * 64];
-    }
-    bcol = p.bexp[which * D + col];
-    if (rg == 0 && g == 0) s_cn[col] = p.colnorm[which * D + col];
-  };
-
-  // destination inputs of vector tid (< TV) of a round, loaded one round ahead: slot and
-  // window flag; the claims follow at the start of the round, used after the MFMA phase
+  // destination inputs of vector tid (< TV) of a K / V round, loaded one round ahead:
+  // slot and window flag; the claims follow at the start of the round
   long long slot_n = -1;
   int32_t flag_n = 0;
   auto load_slot = [&](int64_t it) {
-    slot_n = -1;
-    flag_n = 0;
-    const int64_t vec = item_base(it) + tid;
-    if (item_kind(it) != KIND_Q && tid < TV && vec < kv_vec) {
-      slot_n = a.slot_mapping[vec / hk];
-      if (a.stage_mode == OSCAR_STAGE_WRITE) flag_n = p.flags[vec / hk];
-    }
+    const int64_t vec = it * TV + tid;
+    const uint32_t t = (tid < TV && vec < kv_vec) ? (uint32_t)vec / hk32 : 0u;
+    slot_n = a.slot_mapping[t];
+    if (window) flag_n = p.flags[t];
   };
-  // vectors left to the exact pass, gathered in LDS and appended to the global lists
-  // once per workgroup (a full buffer spills straight to the global list)
-  __shared__ int32_t s_xl[2][kExactBuffer];
-  __shared__ int s_xn[2], s_xbase[2];
-  if (tid < 2) s_xn[tid] = 0;
 
+  // ---- B: R's 32-column block in registers, the two fp16 planes written by the prep
+  // kernel (lane (n, g) of K-step s: R[16 s + 8 g + j][col] * 2^bcol, j < 8), issued after
+  // the first round's x so that staging does not wait for it
+  const float cn = p.colnorm[which * D + col];
+  const int bcol = p.bexp[which * D + col];
   XChunk<XT> xc;
-  load_x(it0, xc);
-  load_slot(it0);
-  const bool fp32x = XT == OSCAR_F32;
-  const float coef = fp32x ? 0x1p-19f : 0x1p-20f;
-  for (int64_t it = it0; it < it1; ++it) {
-    const int kind = item_kind(it);
-    const int64_t base = item_base(it);
-    const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
-    const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
-    const int which = kind == KIND_V ? 1 : 0;
-    if (which != rkind) {
-      load_b(which);
-      rkind = which;
+  // the residual plane of the last KL K-steps is kept in LDS (each wave its own copy),
+  // the rest of B in registers
+  constexpr int KL = XP == 2 ? KS / 4 : KS / 2;
+  __shared__ u32x4 s_b1[8][KL][64];
+  u32x4 b0[KS], b1[KS - KL];
+  if (it0 < it1) {
+    load_x(it0, xc);
+    if (kind != KIND_Q) load_slot(it0);
+    const u32x4* bsrc = p.planes + ((int64_t)(which * CW + cb) * KS) * 2 * 64 + lane;
+    u32x4 bl[KL];
+#pragma unroll
+    for (int s = 0; s < KL; ++s) bl[s] = bsrc[(2 * (KS - KL + s) + 1) * 64];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      b0[s] = bsrc[(2 * s) * 64];
+      if (s < KS - KL) b1[s] = bsrc[(2 * s + 1) * 64];
     }
-    // ---- stage x: exponent, norm, fp16 planes in MFMA A order
-    {
+#pragma unroll
+    for (int s = 0; s < KL; ++s) s_b1[wave][s][lane] = bl[s];
+  }
+  if (rg == 0 && g == 0) s_cn[col] = cn;
+  float cx = 0.f;  // the rotation term of the certification bound per unit ||x|| (first round)
+  int32_t* xlist = exact_list(p, kind == KIND_V ? 1 : 0, kv_vec) + it0 * TV;  // K / V: this run's segment
+  const int seat_rows = a.staging.rows;
+
+  // Rounds in a two-stage pipeline: each pass of the loop stages round it's x, then forms
+  // round it's y~ (MFMA) and quantizes round it - 1.  The two waves that share a SIMD
+  // (w and w + 4) take these two in opposite orders, so one wave's MFMAs run beside the
+  // other's VALU work.
+  const bool mfma_first = (wave & 4) == 0;
+  static_assert(TV <= 4 * 64, "the destination threads form before they quantize");
+  for (int64_t it = it0; it <= it1 && it0 < it1; ++it) {
+    const bool mf = it < it1, qu = it > it0;  // this pass forms round it / quantizes it - 1
+    const int cur = (int)(it & 1), prv = cur ^ 1;
+    const int64_t base = it * TV;
+    long long slot = -1, c_slot = -1, c_seat = -1;
+    int32_t flag = 0;
+    int64_t seat = 0;
+    if (mf) {
+      // ---- stage x: exponent, norm, fp16 planes in MFMA A order
       float f[16];
       xc.to_float(f);
+      const bool live = base + sv < nvec;
       float mx = 0.f, ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
+        if (!live) f[j] = 0.f;
         mx = fmaxf(mx, fabsf(f[j]));
         ss = fmaf(f[j], f[j], ss);
       }
-#pragma unroll
-      for (int o = 1; o < TPV; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o));
-        ss += __shfl_xor(ss, o);
-      }
+      mx = group_max<TPV>(mx);
+      ss = group_sum<TPV>(ss);
       const int ax = fp16_exponent(mx);
       const int rb = sv / 32, mm = sv % 32;
 #pragma unroll
@@ -860,230 +914,273 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
       }
       if (sq == 0) {
         s_ax[sv] = ax;
-        s_nx[sv] = sqrtf(ss);
+        s_nx[cur][sv] = sqrtf(ss);
+      }
+      // ---- this round's claims (in flight until the destinations at the end of the pass)
+      if (kind != KIND_Q) {
+        slot = (tid < TV && base + tid < kv_vec) ? slot_n : -1;
+        flag = flag_n;
+        const int64_t cs = slot >= 0 && slot < p.capacity ? slot : 0;
+        c_slot = (long long)a.slot_claims[cs];
+        if (a.stage_mode != OSCAR_STAGE_NONE) seat = seat_of(cs, a.cache.block_size, seat_rows);
+        if (window) c_seat = (long long)a.seat_claims[seat];
       }
     }
-    // ---- this round's claims (in flight during the MFMA phase)
-    const long long slot = slot_n;
-    const int32_t flag = flag_n;
-    const bool claimed = slot >= 0 && slot < p.capacity;  // K / V rounds, tid < TV only
-    long long c_slot = -1, c_seat = -1;
-    int64_t seat = 0;
-    if (claimed) {
-      c_slot = (long long)a.slot_claims[slot];
-      if (a.stage_mode != OSCAR_STAGE_NONE) seat = seat_of(slot, a.cache.block_size, a.staging.rows);
-      if (a.stage_mode == OSCAR_STAGE_WRITE) c_seat = (long long)a.seat_claims[seat];
-    }
     __syncthreads();
-    if (it + 1 < it1) {  // in flight during the MFMA and quantize phases
-      load_x(it + 1, xc);
-      load_slot(it + 1);
+    if (it == it0) {
+      // coef (1 + 2^-10)^2 max_d ||R_:d|| (the factors cover the fp32 roundings of the norms)
+      float cnm = 0.f;
+      for (int c = lane; c < D; c += 64) cnm = fmaxf(cnm, s_cn[c]);
+      cx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(
+          (XT == OSCAR_F32 ? 0x1p-19f : 0x1p-20f) * (1.f + 0x1p-10f) * (1.f + 0x1p-10f) * wave_max(cnm))));
+    }
+    if (mf) {  // next round's x and slots, in flight until the next pass (the last round
+               // reloads its own: unconditional, so the waits count exactly)
+      const int64_t nx = it + 1 < it1 ? it + 1 : it;
+      load_x(nx, xc);
+      if (kind != KIND_Q) load_slot(nx);
     }
 
-    // ---- MFMA: y~ of this wave's row block x column block into the y tile
-    {
-      f32x16 chain[NC], small = f32x16{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) chain[c] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const f16x8 a0 = __builtin_bit_cast(f16x8, s_a[0][rg][s][lane]);
-        const f16x8 f0 = __builtin_bit_cast(f16x8, b0[s]);
-        const f16x8 f1 = __builtin_bit_cast(f16x8, b1[s]);
-        chain[s / kChainSteps] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f0, chain[s / kChainSteps], 0, 0, 0);
-        small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f1, small, 0, 0, 0);
-        if constexpr (XP == 2) {
-          const f16x8 a1 = __builtin_bit_cast(f16x8, s_a[1][rg][s][lane]);
-          small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f0, small, 0, 0, 0);
-          small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f1, small, 0, 0, 0);
+    // ---- round it's destinations, for its quantize pass in the next pass of the loop
+    auto dest_pass = [&]() {
+      if (kind != KIND_Q && tid < TV) {
+        Dest d{};
+        if (slot >= 0 && slot < p.capacity) {
+          const long long mine = claim_value(epoch, (uint32_t)(base + tid) / hk32);
+          d.slot = slot;
+          d.seat = seat;
+          d.valid = true;
+          d.slot_win = c_slot == mine;
+          d.seat_win = window && c_seat == mine;
+          d.keep = window && (flag & 1);
+          const int64_t h = (uint32_t)(base + tid) % hk32, blk = slot / a.cache.block_size,
+                        off = slot % a.cache.block_size;
+          d.koff = blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
+          d.voff = blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
         }
+        s_dest[cur][tid] = d;
+      }
+    };
+    auto mfma_pass = [&]() {
+      // ---- MFMA: y~ of this wave's row block x column block into the y tile.  Chains
+      // of kChainSteps K-steps, each added to the running sum in fp32 as it completes
+      // (each addition errs by <= 2^-24 sum_k |x_k R_kd|); the residual plane's products
+      // go to their own accumulator, added last.
+      f32x16 total = f32x16{}, small = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f32x16 chain = f32x16{};
+#pragma unroll
+        for (int k = 0; k < kChainSteps; ++k) {
+          const int s = c * kChainSteps + k;
+          const f16x8 a0 = __builtin_bit_cast(f16x8, s_a[0][rg][s][lane]);
+          const f16x8 f0 = __builtin_bit_cast(f16x8, b0[s]);
+          const f16x8 f1 = __builtin_bit_cast(f16x8, s < KS - KL ? b1[s < KS - KL ? s : 0] : s_b1[wave][s - (KS - KL)][lane]);
+          chain = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f0, chain, 0, 0, 0);
+          small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, f1, small, 0, 0, 0);
+          if constexpr (XP == 2) {
+            const f16x8 a1 = __builtin_bit_cast(f16x8, s_a[1][rg][s][lane]);
+            small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f0, small, 0, 0, 0);
+            small = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, f1, small, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) total[r] = c == 0 ? chain[r] : total[r] + chain[r];
+        // keep the A fragments' LDS reads with their chain (bounds the registers they take)
+        __builtin_amdgcn_sched_barrier(0);
       }
       // C[i][n]: vector i = 8 (r / 4) + 4 g + r % 4 of the row block, column n = m
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int v = 32 * rg + 8 * (r >> 2) + 4 * g + (r & 3);
-        // chains + small summed with exact two-sums (the errors gathered in comp), then
-        // one rounding: the fp32 of the exact sum to within 2^-24 relative
-        float sum = small[r], comp = 0.f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const float b = chain[c][r];
-          const float t = sum + b, bb = t - sum;
-          comp += (sum - (t - bb)) + (b - bb);
-          sum = t;
-        }
-        s_y[v][col] = ldexpf(sum + comp, -(s_ax[v] + bcol));
+        s_y[cur][v][col] = ldexpf(total[r] + small[r], -(s_ax[v] + bcol));
       }
-    }
-    // ---- destinations
-    if (kind != KIND_Q && tid < TV) {
-      Dest d{};
-      if (claimed) {
-        const long long mine = claim_value(epoch, (base + tid) / hk);
-        const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
-        d.slot = slot;
-        d.seat = seat;
-        d.valid = true;
-        d.slot_win = c_slot == mine;
-        d.seat_win = window && c_seat == mine;
-        d.keep = window && (flag & 1);
-      }
-      s_dest[tid] = d;
-    }
-    __syncthreads();
-
-    // ---- four vectors at a time (one per 16-lane row, lane l holding elements
-    // [l E, (l + 1) E)): read-path copy, destination, certification, quantization
-    void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
-    const int row = lane >> 4, l = lane & 15;
+    };
+    auto quant_pass = [&]() {
+      // ---- round it - 1, four vectors at a time (one per 16-lane row, lane l holding
+      // elements [l E, (l + 1) E)): read-path copy, destination, certification,
+      // quantization
+      const int64_t qbase = base - TV;
+      const int row = lane >> 4, l = lane & 15;
 #pragma unroll 1
-    for (int j = 0; j < NVW / 4; ++j) {
-      const int v = wave * NVW + 4 * j + row;
-      const int64_t vec = base + v;
-      const bool live = vec < nvec;
-      float y[E];
+      for (int j = 0; j < NVW / 4; ++j) {
+        const int v = wave * NVW + 4 * j + row;
+        const int64_t vec = qbase + v;
+        const bool live = vec < nvec;
+        float y[E];
 #pragma unroll
-      for (int q = 0; q < E; q += 4) *(f32x4*)&y[q] = *(const f32x4*)&s_y[v][l * E + q];
-      if (live && rot_out != nullptr) {
+        for (int q = 0; q < E; q += 4) *(f32x4*)&y[q] = *(const f32x4*)&s_y[prv][v][l * E + q];
+        if (live && rot_out != nullptr) {
 #pragma unroll
-        for (int q = 0; q < E; q += 4) store4<XT>(rot_out, vec * D + l * E + q, &y[q]);
-      }
-      if (kind == KIND_Q) continue;
-      Dest d{};
-      if (live) d = s_dest[v];
-      bool exact = d.valid && d.seat_win && d.keep;  // the FP32 window copy is y itself
-      if (d.valid && !exact && d.slot_win) {
-        const int64_t h = vec % hk, blk = d.slot / a.cache.block_size, off = d.slot % a.cache.block_size;
-        uint8_t* kslot = a.cache.k + blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
-        uint8_t* vslot = a.cache.v + blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
-        const float nx = s_nx[v] * (1.f + 0x1p-10f);
-        float e[E];
-#pragma unroll
-        for (int q = 0; q < E; ++q)
-          e[q] = coef * nx * s_cn[l * E + q] * (1.f + 0x1p-10f) + fabsf(y[q]) * 0x1p-22f + 0x1p-126f;
-        exact = !certify_quant16<D>(p, kind, y, e, true, kslot, vslot);
-      }
-      if (exact && l == 0) {
-        const int i = atomicAdd(&s_xn[kind], 1);
-        if (i < kExactBuffer) {
-          s_xl[kind][i] = (int32_t)vec;
-        } else {
-          const int g = atomicAdd(&p.exact[kind], 1);
-          p.exact[2 + kind * kv_vec + g] = (int32_t)vec;
+          for (int q = 0; q < E; q += 4) store4<XT>(rot_out, vec * D + l * E + q, &y[q]);
         }
+        if (kind == KIND_Q) continue;
+        Dest d{};
+        if (live) d = s_dest[prv][v];
+        bool exact = d.valid && d.seat_win && d.keep;  // the FP32 window copy is y itself
+        if (d.valid && !exact && d.slot_win) {
+          exact = !certify_quant16<D>(p, kind, y, fmaf(cx, s_nx[prv][v], 0x1p-126f), true,
+                                      a.cache.k + d.koff, a.cache.v + d.voff);
+        }
+        if (exact && l == 0) xlist[atomicAdd(&s_xn, 1)] = (int32_t)vec;
+        // a seat this token wins outside the window loses its FP32 copy (backend.py:536-541)
+        if (d.valid && !exact && d.seat_win && kind == KIND_K && l == 0) a.staging.owner[d.seat] = -1;
       }
-      // a seat this token wins outside the window loses its FP32 copy (backend.py:536-541)
-      if (d.valid && !exact && d.seat_win && kind == KIND_K && l == 0) a.staging.owner[d.seat] = -1;
+    };
+    // the claims are only needed by waves that form before they quantize (tid < TV)
+    if (mfma_first && mf) {
+      mfma_pass();
+      dest_pass();
     }
+    if (qu) quant_pass();
+    if (!mfma_first && mf) mfma_pass();
     __syncthreads();
   }
-  // ---- the gathered exact-pass vectors to the global lists
-  if (tid < 2) {
-    const int n = s_xn[tid] < kExactBuffer ? s_xn[tid] : kExactBuffer;
-    s_xbase[tid] = n > 0 ? atomicAdd(&p.exact[tid], n) : 0;
-  }
-  __syncthreads();
-  for (int k = 0; k < 2; ++k) {
-    const int n = s_xn[k] < kExactBuffer ? s_xn[k] : kExactBuffer;
-    for (int i = tid; i < n; i += kFusedThreads) p.exact[2 + k * kv_vec + s_xbase[k] + i] = s_xl[k][i];
-  }
+  if (kind != KIND_Q && tid == 0) exact_counts(p, kind)[wg] = s_xn;
+  if (b == 0 && tid == 0) a.epoch_counter[0] = epoch;
 }
 
-// ---- exact pass: groups of kExactGroup vectors of one kind.  R streams through LDS in
-// chunks of ROWS rows (three buffers: while chunk c is used, c + 1 is in LDS and c + 2 in
-// flight).  Thread (col, vs) sums the products of vectors vs * VPT .. + VPT - 1 with R's
-// column col in fp64 over all rows (each product of an input element with an fp32 entry
-// is exact; one final rounding to fp32).
+// ---- exact pass: groups of kExactGroup vectors of one kind.  Thread (slice, pair) sums
+// x_k R_kc in fp64 for the group's vectors, the two columns c = 2 pair, 2 pair + 1 and
+// the D / S rows k of its slice (each product of an input element with an fp32 entry is
+// exact in fp64); R's rows come straight from global memory in batches of RB, x_k of the
+// group from LDS (one broadcast address per wave).  The slices' partial sums are added in
+// slice order, then rounded once to fp32.
 template <int D, int XT>
 __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams p) {
-  constexpr int VS = kExactThreads / D;              // vector sets
-  constexpr int EG = VS > kExactGroup ? VS : kExactGroup;  // vectors per group
-  constexpr int VPT = EG / VS;                       // vectors per thread
-  constexpr int ROWS = 8192 / D < D ? 8192 / D : D;  // rows per chunk (<= 32 KB)
-  constexpr int NCH = D / ROWS;                      // chunks
-  constexpr int F4 = ROWS * D / 4 / kExactThreads;   // float4 loads per thread per chunk
-  static_assert(VPT >= 1 && EG % VS == 0 && F4 >= 1 && NCH * ROWS == D, "exact tile shape");
+  constexpr int G = kExactGroup;             // vectors per group
+  constexpr int NP = D / 2;                  // column pairs
+  constexpr int S = kExactThreads / NP;      // row slices
+  constexpr int RS = D / S;                  // rows per slice
+  constexpr int RB = RS < 8 ? RS : 8;        // rows per batch of loads
+  constexpr int NB = RS / RB;                // batches
+  static_assert(S * NP == kExactThreads && RS * S == D && NB * RB == RS && G % 2 == 0, "exact tile shape");
   const oscar_store_args_v1& a = p.a;
   const int kind = blockIdx.y;
   const int64_t hk = a.cache.num_kv_heads;
   const int64_t nvec = a.num_tokens * hk;
-  const int count = p.exact[kind];
-  const int32_t* list = p.exact + 2 + kind * nvec;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the fused workgroups' counts: s_pre[w] = vectors of workgroups before w; workgroup w's
+  // entries start at list[w * seg] (seg = its run of rounds, in vectors)
+  constexpr int TV = (8 / (D / 32)) * 32;
+  constexpr int PT = kMaxFusedGroups / kExactThreads;  // counts per thread
+  static_assert(PT * kExactThreads == kMaxFusedGroups, "counts per thread");
+  const int gkv = p.fused_kv_groups;
+  const int64_t seg = ((nvec + TV - 1) / TV + gkv - 1) / gkv * TV;
+  __shared__ int s_pre[kMaxFusedGroups + 1];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int w = tid + i * kExactThreads;
+    s_pre[w + 1] = w < gkv ? exact_counts(p, kind)[w] : 0;
+  }
+  if (tid == 0) s_pre[0] = 0;
+  __syncthreads();
+  for (int off = 1; off < gkv; off <<= 1) {  // inclusive scan of s_pre[1 ..]
+    int add[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int w = tid + i * kExactThreads;
+      add[i] = w >= off ? s_pre[w + 1 - off] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PT; ++i) s_pre[tid + i * kExactThreads + 1] += add[i];
+    __syncthreads();
+  }
+  const int count = s_pre[gkv];
+  if (blockIdx.x == 0 && tid == 0) p.exact[kind] = count;
+  const int32_t* list = exact_list(p, kind, nvec);
   const int64_t epoch = a.epoch_counter[1];
   const float* R = kind == KIND_V ? a.rv : a.rk;
   const void* src = kind == KIND_K ? a.key : a.value;
   const int64_t stride = kind == KIND_K ? a.key_stride_token : a.value_stride_token;
-  __shared__ __attribute__((aligned(16))) float s_r[3][ROWS * D];
-  __shared__ __attribute__((aligned(16))) double s_xd[EG][D];
-  __shared__ __attribute__((aligned(16))) float s_x[EG][D];  // quantizer rows
-  __shared__ __attribute__((aligned(16))) float s_y[EG][D];
-  __shared__ int32_t s_id[EG];
-  __shared__ float s_clip[EG];
-  const int col = tid % D, vs = tid / D;
-  auto load_chunk = [&](int c, f32x4* dst) {
+  __shared__ __attribute__((aligned(16))) double s_xd[D][G];  // x_k of the group, k-major
+  __shared__ __attribute__((aligned(16))) double s_part[S > 1 ? S - 1 : 1][G][D];
+  __shared__ __attribute__((aligned(16))) float s_x[G][D];    // quantizer rows
+  __shared__ __attribute__((aligned(16))) float s_y[G][D];
+  __shared__ int32_t s_id[G];
+  __shared__ float s_clip[G];
+  const int cp = tid % NP, sl = tid / NP;    // column pair, row slice
+  const int k0 = sl * RS;
+  auto load_rows = [&](int kb, float2* r) {  // R[k][2 cp], R[k][2 cp + 1], k = k0 + kb + j
 #pragma unroll
-    for (int i = 0; i < F4; ++i) {
-      const int e = 4 * (tid + i * kExactThreads);  // element of the chunk, row-major
-      const int k = c * ROWS + e / D, cc = e % D;
-      if (R != nullptr) {
-        dst[i] = *(const f32x4*)(R + (int64_t)k * D + cc);
-      } else {
-        const int o = k - cc;  // identity: 1 where the column equals the row
-        dst[i] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
-      }
+    for (int j = 0; j < RB; ++j) {
+      const int k = k0 + kb + j;
+      if (R != nullptr) r[j] = *(const float2*)(R + (int64_t)k * D + 2 * cp);
+      else r[j] = float2{k == 2 * cp ? 1.f : 0.f, k == 2 * cp + 1 ? 1.f : 0.f};  // identity
     }
   };
-  auto store_chunk = [&](int buf, const f32x4* v4) {
-#pragma unroll
-    for (int i = 0; i < F4; ++i) *(f32x4*)&s_r[buf][4 * (tid + i * kExactThreads)] = v4[i];
-  };
-  for (int g0 = blockIdx.x * EG; g0 < count; g0 += gridDim.x * EG) {
-    f32x4 ra[F4], rb[F4];
-    load_chunk(0, ra);
-    if (NCH > 1) load_chunk(1, rb);
-    if (tid < EG) s_id[tid] = g0 + tid < count ? list[g0 + tid] : -1;
+  for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
+    float2 ra[RB];
+    load_rows(0, ra);
+    if (tid < G) {
+      const int q = g0 + tid;
+      int32_t id = -1;
+      if (q < count) {  // the workgroup holding entry q: the last w with s_pre[w] <= q
+        int lo = 0, hi = gkv;
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (s_pre[mid] <= q) lo = mid;
+          else hi = mid;
+        }
+        id = list[lo * seg + (q - s_pre[lo])];
+      }
+      s_id[tid] = id;
+    }
     __syncthreads();
-    for (int i = tid; i < EG * D; i += kExactThreads) {
+    for (int i = tid; i < G * D; i += kExactThreads) {
       const int v = i / D, k = i % D;
       const int32_t id = s_id[v];
-      s_xd[v][k] = id >= 0 ? (double)load_elem(src, XT, (id / hk) * stride + (id % hk) * D + k) : 0.0;
+      s_xd[k][v] = id >= 0 ? (double)load_elem(src, XT, (id / hk) * stride + (id % hk) * D + k) : 0.0;
     }
-    store_chunk(0, ra);
     __syncthreads();
-    double acc[VPT];
+    double acc[G][2];
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) acc[v] = 0.0;
-    // one chunk: chunk c + 1 (registers `next`) to its buffer, chunk c + 2 into `free`
-    // (which held chunk c, already stored), then the products of chunk c
-    auto step = [&](int c, f32x4* next, f32x4* free) {
-      if (c + 1 < NCH) store_chunk((c + 1) % 3, next);
-      if (c + 2 < NCH) load_chunk(c + 2, free);
-      const float* rc = s_r[c % 3];
-#pragma unroll 2
-      for (int kk = 0; kk < ROWS; kk += 2) {
-        double r[2];
+    for (int v = 0; v < G; ++v) acc[v][0] = acc[v][1] = 0.0;
+    // batches of RB rows: the next batch's rows in flight during this one's products
+#pragma unroll 1
+    for (int kb = 0; kb < RS; kb += RB) {
+      float2 rn[RB];
+      if (kb + RB < RS) load_rows(kb + RB, rn);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) r[j] = (double)rc[(kk + j) * D + col];
+      for (int j = 0; j < RB; ++j) {
+        const int k = k0 + kb + j;
+        const double r0 = ra[j].x, r1 = ra[j].y;
 #pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          const double* xv = &s_xd[vs * VPT + v][c * ROWS + kk];  // one address per set: broadcast
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[v] = fma(xv[j], r[j], acc[v]);
+        for (int v = 0; v < G; v += 2) {
+          const double2 xv = *(const double2*)&s_xd[k][v];
+          acc[v][0] = fma(xv.x, r0, acc[v][0]);
+          acc[v][1] = fma(xv.x, r1, acc[v][1]);
+          acc[v + 1][0] = fma(xv.y, r0, acc[v + 1][0]);
+          acc[v + 1][1] = fma(xv.y, r1, acc[v + 1][1]);
         }
       }
-      __syncthreads();  // chunk c + 1 stored; buffer c % 3 free for chunk c + 3
-    };
-#pragma unroll 1
-    for (int c = 0; c < NCH; c += 2) {
-      step(c, rb, ra);
-      if (c + 1 < NCH) step(c + 1, ra, rb);
-    }
+      if (kb + RB < RS) {
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) s_y[vs * VPT + v][col] = (float)acc[v];
+        for (int j = 0; j < RB; ++j) ra[j] = rn[j];
+      }
+    }
+    if (sl > 0) {
+#pragma unroll
+      for (int v = 0; v < G; ++v) *(double2*)&s_part[sl - 1][v][2 * cp] = double2{acc[v][0], acc[v][1]};
+    }
     __syncthreads();
-    for (int v = wave; v < EG; v += kExactThreads / 64) {
+    if (sl == 0) {
+#pragma unroll 1
+      for (int s = 0; s < S - 1; ++s) {
+#pragma unroll
+        for (int v = 0; v < G; ++v) {
+          const double2 q = *(const double2*)&s_part[s][v][2 * cp];
+          acc[v][0] += q.x;
+          acc[v][1] += q.y;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < G; ++v) *(float2*)&s_y[v][2 * cp] = float2{(float)acc[v][0], (float)acc[v][1]};
+    }
+    __syncthreads();
+    for (int v = wave; v < G; v += kExactThreads / 64) {
       const int32_t id = s_id[v];
       if (id < 0) continue;
       const int64_t t = id / hk;
@@ -1091,7 +1188,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       const f32x4 y4 = *(const f32x4*)&s_y[v][4 * (lane < D / 4 ? lane : 0)];
       quant_vector<D>(p, kind, t, id % hk, d, y4, s_x[v], &s_clip[v]);  // s_x[v]: free row
     }
-    __syncthreads();  // s_id, s_x, s_r are rewritten by the next group
+    __syncthreads();  // s_id, s_xd, s_part, s_x are rewritten by the next group
   }
 }
 
@@ -1105,16 +1202,29 @@ int launch_large(const StoreParams& p, int cu_count, hipStream_t s) {
   const int64_t prep_blocks = (a.num_tokens + 255) / 256 + 2 * (D / 32);
   hipLaunchKernelGGL((store_prep_kernel<D>), dim3((unsigned)prep_blocks), dim3(256), 0, s, p);
   OSCAR_CHECK_LAUNCH("store_prep_kernel");
-  // one workgroup per compute unit, each over a run of consecutive rounds
-  const int64_t grid = total < cu_count ? total : cu_count;
-  hipLaunchKernelGGL((store_fused_kernel<D, XT>), dim3((unsigned)grid), dim3(kFusedThreads), 0, s, p);
+  // one workgroup per compute unit, each over a run of consecutive rounds of one kind:
+  // the query rounds get their share of the workgroups, K and V the rest in halves
+  const int64_t rq = (q_vec + TV - 1) / TV;
+  int64_t grid = total < cu_count ? total : cu_count;
+  if (grid > 2 * kMaxFusedGroups) grid = 2 * kMaxFusedGroups;
+  if (grid < (rq > 0 ? 3 : 2)) grid = rq > 0 ? 3 : 2;
+  int64_t gq = 0;
+  if (rq > 0) {
+    gq = grid * rq / total;
+    if (gq < 1) gq = 1;
+    if (gq > grid - 2) gq = grid - 2;
+  }
+  StoreParams q = p;
+  q.fused_kv_groups = (int32_t)((grid - gq) / 2);
+  grid = 2 * q.fused_kv_groups + gq;
+  hipLaunchKernelGGL((store_fused_kernel<D, XT>), dim3((unsigned)grid), dim3(kFusedThreads), 0, s, q);
   OSCAR_CHECK_LAUNCH("store_fused_kernel");
   // persistent over the device-side counts: per kind at most half the compute units
   // (the list is a few percent of the vectors plus the window's)
   int64_t groups = (kv_vec + kExactGroup - 1) / kExactGroup;
   const int64_t half_cus = cu_count / 2 > 0 ? cu_count / 2 : 1;
   if (groups > half_cus) groups = half_cus;
-  hipLaunchKernelGGL((store_exact_kernel<D, XT>), dim3((unsigned)groups, 2), dim3(kExactThreads), 0, s, p);
+  hipLaunchKernelGGL((store_exact_kernel<D, XT>), dim3((unsigned)groups, 2), dim3(kExactThreads), 0, s, q);
   OSCAR_CHECK_LAUNCH("store_exact_kernel");
   return 0;
 }
@@ -1144,9 +1254,10 @@ int launch_store(const StoreParams& p, int cu_count, hipStream_t s) {
 using namespace oscar;
 
 // workspace: calls of <= kFusedTokens tokens: y [2][N][Hk][D] fp32 (the column slices);
-// larger calls: the exact-pass lists (2 + 2 N Hk int32) | window flags [N] int32
+// larger calls: the exact-pass totals, per-workgroup counts and lists
+// (2 + 2 kMaxFusedGroups + 2 N Hk int32) | window flags [N] int32
 static int64_t store_ws_list_bytes(int64_t n, int64_t hk) {
-  return ((2 + 2 * n * hk) * (int64_t)sizeof(int32_t) + 15) / 16 * 16;
+  return ((2 + 2 * kMaxFusedGroups + 2 * n * hk) * (int64_t)sizeof(int32_t) + 15) / 16 * 16;
 }
 
 static int64_t store_ws_flag_bytes(int64_t n) { return (n * (int64_t)sizeof(int32_t) + 15) / 16 * 16; }
@@ -1232,8 +1343,9 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
     return fail(-22, "oscar_store_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
   if (a.num_tokens <= kFusedTokens && (a.arrivals == nullptr || (((uintptr_t)a.arrivals) & 3)))
     return fail(-22, "oscar_store_v1: calls of <= %lld tokens need the arrivals counters", (long long)kFusedTokens);
-  if (2 * a.num_tokens * a.cache.num_kv_heads >= (1ll << 31))
-    return fail(-22, "oscar_store_v1: num_tokens x num_kv_heads too large for one call");
+  if (2 * a.num_tokens * a.cache.num_kv_heads >= (1ll << 31) ||
+      (a.query_rot != nullptr && a.num_tokens * a.num_q_heads >= (1ll << 31)))
+    return fail(-22, "oscar_store_v1: num_tokens x heads too large for one call");
   StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size};
   uint8_t* ws = (uint8_t*)a.workspace;
   p.exact = (int32_t*)ws;

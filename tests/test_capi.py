@@ -280,9 +280,11 @@ def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(
     assert lib.oscar_store_v1(C.byref(s), None) == 0
     # <= 64 tokens: the column slices y [2][N][Hk][D] fp32
     assert lib.oscar_store_workspace_bytes_v1(10, 2, 256) == 2 * 10 * 2 * 256 * 4
-    # larger: exact lists (2 + 2 N Hk int32, 16-B padded) + window flags [N] int32 + fp16
-    # planes of R_k and R_v (8 D^2 bytes) + column exponents and norms (16 D bytes)
-    assert lib.oscar_store_workspace_bytes_v1(100, 2, 256) == 1616 + 400 + 8 * 256 * 256 + 16 * 256
+    # larger: exact-pass totals, per-workgroup counts (2 x 1024) and lists (2 N Hk), int32,
+    # 16-B padded + window flags [N] int32 + fp16 planes of R_k and R_v (8 D^2 bytes) +
+    # column exponents and norms (16 D bytes)
+    lists = ((2 + 2 * 1024 + 2 * 100 * 2) * 4 + 15) // 16 * 16
+    assert lib.oscar_store_workspace_bytes_v1(100, 2, 256) == lists + 400 + 8 * 256 * 256 + 16 * 256
 
 
 def decode_args(**kw):

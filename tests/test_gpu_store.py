@@ -93,8 +93,8 @@ def test_store_bytes_bit_exact(cuda, d, hk, rot, n):
 
 
 def exact_pass_count(n, hk, d):
-    """Vectors the last large call sent to the fp64 pass: the K and V counts that open
-    the store workspace of a call of more than 64 tokens."""
+    """Vectors the last large call sent to the fp64 pass: the K and V totals that open
+    the store workspace of a call of more than 64 tokens (written by the exact pass)."""
     from oscar_amd import ops
 
     ws = ops.DeviceScratch.get(torch.device("cuda", torch.cuda.current_device())).store_ws
