@@ -596,18 +596,39 @@ __device__ __forceinline__ unsigned f16_pair(float lo, float hi) {
 
 // fp16 planes of one 32-column block of R (which: 0 = R_k, 1 = R_v) in MFMA B order:
 // fragment (s, lane n + 32 g) holds R[16 s + 8 g + j][32 cb + n] * 2^bexp, j < 8, as
-// the rounded plane and the (exact) remainder rounded again
+// the rounded plane and the (exact) remainder rounded again.  The block's D x 32 entries
+// are staged in LDS first (all loads in flight at once).
 template <int D>
 __device__ void rotation_planes(const StoreParams& p, int which, int cb) {
   constexpr int KS = D / 16;
+  constexpr int NT = 256;                  // threads of the prep kernel
+  constexpr int F4 = D * 8 / NT;           // float4 loads per thread
   const float* R = which ? p.a.rv : p.a.rk;
   const int tid = threadIdx.x, c = tid % 32, part = tid / 32;  // 8 parts of the rows
-  auto r_at = [&](int k, int col) { return R != nullptr ? R[(int64_t)k * D + col] : (k == col ? 1.f : 0.f); };
+  __shared__ float s_r[D][33];
   __shared__ float s_mx[8][32], s_sq[8][32];
   __shared__ int s_e[32];
+  f32x4 v[F4];
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {  // float4 i of the thread: row (tid + i NT) / 8, columns 4 ((tid + i NT) % 8) ..
+    const int q = tid + i * NT, k = q / 8, c0 = 32 * cb + 4 * (q % 8);
+    if (R != nullptr) {
+      v[i] = *(const f32x4*)(R + (int64_t)k * D + c0);
+    } else {
+      const int o = k - c0;  // identity: 1 where the column equals the row
+      v[i] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {
+    const int q = tid + i * NT, k = q / 8, cc = 4 * (q % 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_r[k][cc + j] = v[i][j];
+  }
+  __syncthreads();
   float mx = 0.f, sq = 0.f;
   for (int k = part; k < D; k += 8) {
-    const float r = r_at(k, 32 * cb + c);
+    const float r = s_r[k][c];
     mx = fmaxf(mx, fabsf(r));
     sq = fmaf(r, r, sq);
   }
@@ -625,14 +646,14 @@ __device__ void rotation_planes(const StoreParams& p, int which, int cb) {
   }
   __syncthreads();
   u32x4* out = p.planes + ((int64_t)(which * (D / 32) + cb) * KS) * 2 * 64;
-  for (int f = tid; f < KS * 64; f += blockDim.x) {
+  for (int f = tid; f < KS * 64; f += NT) {
     const int s = f / 64, lane = f % 64, n = lane % 32, g = lane / 32;
     const int e = s_e[n];
     u32x4 w0, w1;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const int k = 16 * s + 8 * g + 2 * w;
-      const float h0 = ldexpf(r_at(k, 32 * cb + n), e), h1 = ldexpf(r_at(k + 1, 32 * cb + n), e);
+      const float h0 = ldexpf(s_r[k][n], e), h1 = ldexpf(s_r[k + 1][n], e);
       const float q0 = f16_bits_to_f32(f32_to_f16_bits(h0)), q1 = f16_bits_to_f32(f32_to_f16_bits(h1));
       w0[w] = f16_pair(q0, q1);
       w1[w] = f16_pair(h0 - q0, h1 - q1);  // exact differences
@@ -642,20 +663,19 @@ __device__ void rotation_planes(const StoreParams& p, int which, int cb) {
   }
 }
 
-// ---- claims, window flags and the rotation planes: blocks [0, token blocks) take
-// 256 tokens each, the 2 * D / 32 blocks after them one column block of R_k or R_v
+// ---- claims, window flags and the rotation planes: blocks [0, 2 D / 32) take one
+// column block of R_k or R_v, the blocks after them 256 tokens each
 template <int D>
 __global__ __launch_bounds__(256) void store_prep_kernel(StoreParams p) {
   const oscar_store_args_v1& a = p.a;
-  const int64_t token_blocks = (a.num_tokens + 255) / 256;
-  if ((int64_t)blockIdx.x >= token_blocks) {
-    const int b = (int)(blockIdx.x - token_blocks);
-    rotation_planes<D>(p, b / (D / 32), b % (D / 32));
+  constexpr int PB = 2 * (D / 32);  // plane blocks
+  if (blockIdx.x < PB) {
+    rotation_planes<D>(p, blockIdx.x / (D / 32), blockIdx.x % (D / 32));
     return;
   }
   const int64_t e0 = a.epoch_counter[0];
   const int64_t epoch = e0 < kMaxEpoch ? e0 + 1 : kMaxEpoch;
-  if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch_counter[1] = epoch;
+  if (blockIdx.x == PB && threadIdx.x == 0) a.epoch_counter[1] = epoch;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const bool lds = window && a.num_reqs <= kReqLds;
   __shared__ int32_t s_qsl[kReqLds + 1];
@@ -663,7 +683,7 @@ __global__ __launch_bounds__(256) void store_prep_kernel(StoreParams p) {
     for (int r = threadIdx.x; r <= a.num_reqs; r += blockDim.x) s_qsl[r] = a.query_start_loc[r];
     __syncthreads();
   }
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = (int64_t)(blockIdx.x - PB) * blockDim.x + threadIdx.x;
   if (t >= a.num_tokens) return;
   const int64_t slot = a.slot_mapping[t];
   if (window) {
@@ -1040,120 +1060,147 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   if (b == 0 && tid == 0) a.epoch_counter[0] = epoch;
 }
 
-// ---- exact pass: groups of kExactGroup vectors of one kind.  Thread (slice, pair) sums
-// x_k R_kc in fp64 for the group's vectors, the two columns c = 2 pair, 2 pair + 1 and
-// the D / S rows k of its slice (each product of an input element with an fp32 entry is
-// exact in fp64); R's rows come straight from global memory in batches of RB, x_k of the
-// group from LDS (one broadcast address per wave).  The slices' partial sums are added in
-// slice order, then rounded once to fp32.
+// ---- exact pass: groups of kExactGroup vectors of one kind.  Thread (slice, quad) sums
+// x_k R_kc in fp64 for the group's vectors, the four columns c = 4 quad .. 4 quad + 3
+// and the D / S rows k of its slice (each product of an input element with an fp32
+// entry is exact in fp64); R's rows come straight from global memory in batches of RB,
+// x_k of the group from LDS (one broadcast address per wave).  The slices' partial sums
+// are added in slice order, then rounded once to fp32.
 template <int D, int XT>
 __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams p) {
   constexpr int G = kExactGroup;             // vectors per group
-  constexpr int NP = D / 2;                  // column pairs
-  constexpr int S = kExactThreads / NP;      // row slices
+  constexpr int NQ = D / 4;                  // column quads
+  constexpr int S = kExactThreads / NQ;      // row slices
   constexpr int RS = D / S;                  // rows per slice
-  constexpr int RB = RS < 8 ? RS : 8;        // rows per batch of loads
-  constexpr int NB = RS / RB;                // batches
-  static_assert(S * NP == kExactThreads && RS * S == D && NB * RB == RS && G % 2 == 0, "exact tile shape");
+  constexpr int RB = RS < 4 ? RS : 4;        // rows per batch of loads
+  constexpr int TV = (8 / (D / 32)) * 32;    // vectors per round of the fused kernel
+  constexpr int PT = kMaxFusedGroups / kExactThreads;  // counts per thread
+  static_assert(S * NQ == kExactThreads && RS * S == D && RS % RB == 0 && G % 2 == 0, "exact tile shape");
+  static_assert(PT * kExactThreads == kMaxFusedGroups && G <= 64, "counts per thread");
   const oscar_store_args_v1& a = p.a;
   const int kind = blockIdx.y;
   const int64_t hk = a.cache.num_kv_heads;
   const int64_t nvec = a.num_tokens * hk;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // the fused workgroups' counts: s_pre[w] = vectors of workgroups before w; workgroup w's
-  // entries start at list[w * seg] (seg = its run of rounds, in vectors)
-  constexpr int TV = (8 / (D / 32)) * 32;
-  constexpr int PT = kMaxFusedGroups / kExactThreads;  // counts per thread
-  static_assert(PT * kExactThreads == kMaxFusedGroups, "counts per thread");
-  const int gkv = p.fused_kv_groups;
-  const int64_t seg = ((nvec + TV - 1) / TV + gkv - 1) / gkv * TV;
-  __shared__ int s_pre[kMaxFusedGroups + 1];
-#pragma unroll
-  for (int i = 0; i < PT; ++i) {
-    const int w = tid + i * kExactThreads;
-    s_pre[w + 1] = w < gkv ? exact_counts(p, kind)[w] : 0;
-  }
-  if (tid == 0) s_pre[0] = 0;
-  __syncthreads();
-  for (int off = 1; off < gkv; off <<= 1) {  // inclusive scan of s_pre[1 ..]
-    int add[PT];
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      const int w = tid + i * kExactThreads;
-      add[i] = w >= off ? s_pre[w + 1 - off] : 0;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < PT; ++i) s_pre[tid + i * kExactThreads + 1] += add[i];
-    __syncthreads();
-  }
-  const int count = s_pre[gkv];
-  if (blockIdx.x == 0 && tid == 0) p.exact[kind] = count;
-  const int32_t* list = exact_list(p, kind, nvec);
   const int64_t epoch = a.epoch_counter[1];
   const float* R = kind == KIND_V ? a.rv : a.rk;
   const void* src = kind == KIND_K ? a.key : a.value;
   const int64_t stride = kind == KIND_K ? a.key_stride_token : a.value_stride_token;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  const int cq = tid % NQ, sl = tid / NQ;    // column quad, row slice
+  const int k0 = sl * RS;
+  auto load_rows = [&](int kb, f32x4* r) {   // R[k][4 cq ..], k = k0 + kb + j
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const int k = k0 + kb + j, o = k - 4 * cq;
+      if (R != nullptr) r[j] = *(const f32x4*)(R + (int64_t)k * D + 4 * cq);
+      else r[j] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
+    }
+  };
+  f32x4 ra[RB];
+  load_rows(0, ra);  // the first rows of R are in flight during the scan
+
+  // ---- the fused workgroups' counts: this thread's PT consecutive workgroups w and the
+  // exclusive prefix pre[w] of all counts before them (a wave scan, then the waves)
+  const int gkv = p.fused_kv_groups;
+  const int64_t seg = ((nvec + TV - 1) / TV + gkv - 1) / gkv * TV;  // list entries per workgroup
+  int cnt[PT], tsum = 0;
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int w = PT * tid + i;
+    cnt[i] = w < gkv ? exact_counts(p, kind)[w] : 0;
+    tsum += cnt[i];
+  }
+  int incl = tsum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int up = __shfl_up(incl, o);
+    if (lane >= o) incl += up;
+  }
+  __shared__ int s_wsum[kExactThreads / 64];
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  int before = incl - tsum, count = 0;
+#pragma unroll
+  for (int i = 0; i < kExactThreads / 64; ++i) {
+    const int ws = s_wsum[i];
+    if (i < wave) before += ws;
+    count += ws;
+  }
+  if (blockIdx.x == 0 && tid == 0) p.exact[kind] = count;
+  const int32_t* list = exact_list(p, kind, nvec);
+
   __shared__ __attribute__((aligned(16))) double s_xd[D][G];  // x_k of the group, k-major
-  __shared__ __attribute__((aligned(16))) double s_part[S > 1 ? S - 1 : 1][G][D];
-  __shared__ __attribute__((aligned(16))) float s_x[G][D];    // quantizer rows
+  // the slices' partial sums: [slice][vector][column pair half][quad], one double2 each
+  // (consecutive quads in consecutive 16-byte words)
+  __shared__ __attribute__((aligned(16))) double2 s_part[S][G][2][NQ];
+  // y, then the quantizer's scratch row of the same vector (its wave reads y first)
   __shared__ __attribute__((aligned(16))) float s_y[G][D];
   __shared__ int32_t s_id[G];
   __shared__ float s_clip[G];
-  const int cp = tid % NP, sl = tid / NP;    // column pair, row slice
-  const int k0 = sl * RS;
-  auto load_rows = [&](int kb, float2* r) {  // R[k][2 cp], R[k][2 cp + 1], k = k0 + kb + j
-#pragma unroll
-    for (int j = 0; j < RB; ++j) {
-      const int k = k0 + kb + j;
-      if (R != nullptr) r[j] = *(const float2*)(R + (int64_t)k * D + 2 * cp);
-      else r[j] = float2{k == 2 * cp ? 1.f : 0.f, k == 2 * cp + 1 ? 1.f : 0.f};  // identity
-    }
-  };
+  __shared__ Dest s_dst[G];
   for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
-    float2 ra[RB];
-    load_rows(0, ra);
-    if (tid < G) {
-      const int q = g0 + tid;
-      int32_t id = -1;
-      if (q < count) {  // the workgroup holding entry q: the last w with s_pre[w] <= q
-        int lo = 0, hi = gkv;
-        while (hi - lo > 1) {
-          const int mid = (lo + hi) >> 1;
-          if (s_pre[mid] <= q) lo = mid;
-          else hi = mid;
-        }
-        id = list[lo * seg + (q - s_pre[lo])];
+    // ---- the group's entries: each list position g0 .. g0 + G - 1 below count lies in
+    // exactly one workgroup's segment; the thread owning that workgroup fills it
+    {
+      int pre = before;
+#pragma unroll
+      for (int i = 0; i < PT; ++i) {
+        const int w = PT * tid + i;
+        const int lo = pre > g0 ? pre : g0, hi = pre + cnt[i] < g0 + G ? pre + cnt[i] : g0 + G;
+        for (int q = lo; q < hi; ++q) s_id[q - g0] = list[w * seg + (q - pre)];
+        pre += cnt[i];
       }
-      s_id[tid] = id;
+      if (tid < G && g0 + tid >= count) s_id[tid] = -1;
     }
     __syncthreads();
+    // destination inputs of vector tid < G: slot and window flag now, the claims after
+    // the staging (in flight during the products)
+    int64_t d_slot = -1, d_t = 0;
+    int32_t d_flag = 0;
+    if (tid < G && s_id[tid] >= 0) {
+      d_t = s_id[tid] / hk;
+      d_slot = a.slot_mapping[d_t];
+      if (window) d_flag = p.flags[d_t];
+    }
     for (int i = tid; i < G * D; i += kExactThreads) {
       const int v = i / D, k = i % D;
       const int32_t id = s_id[v];
       s_xd[k][v] = id >= 0 ? (double)load_elem(src, XT, (id / hk) * stride + (id % hk) * D + k) : 0.0;
     }
     __syncthreads();
-    double acc[G][2];
+    long long d_cs = -1, d_cseat = -1;
+    int64_t d_seat = 0;
+    const bool d_valid = d_slot >= 0 && d_slot < p.capacity;
+    if (tid < G && d_valid) {
+      d_cs = (long long)a.slot_claims[d_slot];
+      if (a.stage_mode != OSCAR_STAGE_NONE) d_seat = seat_of(d_slot, a.cache.block_size, a.staging.rows);
+      if (window) d_cseat = (long long)a.seat_claims[d_seat];
+    }
+    double acc[G][4];
 #pragma unroll
-    for (int v = 0; v < G; ++v) acc[v][0] = acc[v][1] = 0.0;
+    for (int v = 0; v < G; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0;
     // batches of RB rows: the next batch's rows in flight during this one's products
 #pragma unroll 1
     for (int kb = 0; kb < RS; kb += RB) {
-      float2 rn[RB];
+      f32x4 rn[RB];
       if (kb + RB < RS) load_rows(kb + RB, rn);
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
         const int k = k0 + kb + j;
-        const double r0 = ra[j].x, r1 = ra[j].y;
+        const double r0 = ra[j][0], r1 = ra[j][1], r2 = ra[j][2], r3 = ra[j][3];
 #pragma unroll
         for (int v = 0; v < G; v += 2) {
           const double2 xv = *(const double2*)&s_xd[k][v];
           acc[v][0] = fma(xv.x, r0, acc[v][0]);
           acc[v][1] = fma(xv.x, r1, acc[v][1]);
+          acc[v][2] = fma(xv.x, r2, acc[v][2]);
+          acc[v][3] = fma(xv.x, r3, acc[v][3]);
           acc[v + 1][0] = fma(xv.y, r0, acc[v + 1][0]);
           acc[v + 1][1] = fma(xv.y, r1, acc[v + 1][1]);
+          acc[v + 1][2] = fma(xv.y, r2, acc[v + 1][2]);
+          acc[v + 1][3] = fma(xv.y, r3, acc[v + 1][3]);
         }
       }
       if (kb + RB < RS) {
@@ -1161,34 +1208,48 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
         for (int j = 0; j < RB; ++j) ra[j] = rn[j];
       }
     }
-    if (sl > 0) {
 #pragma unroll
-      for (int v = 0; v < G; ++v) *(double2*)&s_part[sl - 1][v][2 * cp] = double2{acc[v][0], acc[v][1]};
+    for (int v = 0; v < G; ++v) {
+      s_part[sl][v][0][cq] = double2{acc[v][0], acc[v][1]};
+      s_part[sl][v][1][cq] = double2{acc[v][2], acc[v][3]};
+    }
+    if (tid < G) {  // the destination of vector tid, from its claims
+      Dest d{};
+      d.slot = d_slot;
+      d.valid = d_valid;
+      if (d_valid) {
+        const long long mine = claim_value(epoch, d_t);
+        d.seat = d_seat;
+        d.slot_win = d_cs == mine;
+        d.seat_win = window && d_cseat == mine;
+        d.keep = window && (d_flag & 1);
+      }
+      s_dst[tid] = d;
     }
     __syncthreads();
-    if (sl == 0) {
-#pragma unroll 1
-      for (int s = 0; s < S - 1; ++s) {
-#pragma unroll
-        for (int v = 0; v < G; ++v) {
-          const double2 q = *(const double2*)&s_part[s][v][2 * cp];
-          acc[v][0] += q.x;
-          acc[v][1] += q.y;
-        }
+    for (int i = tid; i < G * NQ; i += kExactThreads) {  // four columns of one vector each
+      const int v = i / NQ, q = i % NQ;
+      double y0 = 0.0, y1 = 0.0, y2 = 0.0, y3 = 0.0;
+#pragma unroll 4
+      for (int s = 0; s < S; ++s) {
+        const double2 q0 = s_part[s][v][0][q];
+        const double2 q1 = s_part[s][v][1][q];
+        y0 += q0.x;
+        y1 += q0.y;
+        y2 += q1.x;
+        y3 += q1.y;
       }
-#pragma unroll
-      for (int v = 0; v < G; ++v) *(float2*)&s_y[v][2 * cp] = float2{(float)acc[v][0], (float)acc[v][1]};
+      *(f32x4*)&s_y[v][4 * q] = f32x4{(float)y0, (float)y1, (float)y2, (float)y3};
     }
     __syncthreads();
     for (int v = wave; v < G; v += kExactThreads / 64) {
       const int32_t id = s_id[v];
       if (id < 0) continue;
-      const int64_t t = id / hk;
-      const Dest d = claimed_dest(p, t, a.slot_mapping[t], a.stage_mode == OSCAR_STAGE_WRITE ? p.flags[t] : 0, epoch);
       const f32x4 y4 = *(const f32x4*)&s_y[v][4 * (lane < D / 4 ? lane : 0)];
-      quant_vector<D>(p, kind, t, id % hk, d, y4, s_x[v], &s_clip[v]);  // s_x[v]: free row
+      quant_vector<D>(p, kind, id / hk, id % hk, s_dst[v], y4, s_y[v], &s_clip[v]);
     }
-    __syncthreads();  // s_id, s_xd, s_part, s_x are rewritten by the next group
+    __syncthreads();  // s_id, s_xd, s_part, s_y, s_dst are rewritten by the next group
+    load_rows(0, ra);  // the next group's first rows (ra holds this group's last batch)
   }
 }
 
