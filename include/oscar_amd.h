@@ -120,9 +120,10 @@ typedef struct oscar_store_args_v1 {
    * the exact-pass lists, the per-token window flags and the fp16 planes of R_k / R_v */
   void* workspace;
   int64_t workspace_bytes;
-  /* calls of <= 64 tokens: one arrival counter per K / V vector, uint32
-   * [2 * 64 * num_kv_heads], zero-initialised once and shared per device (every
-   * call leaves it zero; calls that overlap on one device race on it) */
+  /* calls of <= 64 tokens: uint32 [2 * 64 * num_kv_heads], zero-initialised once and
+   * shared per device; one arrival counter per group of 8 K or V vectors uses the
+   * first 2 * ceil(num_tokens * num_kv_heads / 8) words (every call leaves them zero;
+   * calls that overlap on one device race on them) */
   uint32_t* arrivals;
 } oscar_store_args_v1;
 

@@ -9,8 +9,8 @@
 // of the exact sum), clipped and quantized as the reference does.  Two paths:
 //
 //   calls of <= kFusedTokens tokens (decode / MTP steps): store_small_kernel, one
-//   launch; y in fp64 (exact products, one rounding), winners by scanning the call's
-//   slot_mapping.
+//   launch of (32-column slice, group of 8 vectors) workgroups; y in fp64 (exact
+//   products, one rounding), winners by scanning the call's slot_mapping.
 //
 //   larger calls: store_prep_kernel (last-writer claims, window flags, fp16 planes of R),
 //   store_fused_kernel (MFMA rotation into LDS, then per vector: read-path copy,
@@ -31,6 +31,8 @@ namespace oscar {
 namespace {
 
 enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
+
+typedef float __attribute__((ext_vector_type(2))) f32x2;
 
 // workgroups of the fused launch per kind at most (bounds the per-workgroup exact counts)
 constexpr int kMaxFusedGroups = 1024;
@@ -119,15 +121,37 @@ __device__ __forceinline__ bool in_window(const oscar_store_args_v1& a, int64_t 
 }
 
 // Destination of a small call's vector: winners of duplicate slots / seats by
-// scanning slot_mapping.  Computed by one wave, wave-uniform.
-__device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t) {
+// scanning slot_mapping.  Computed by one wave, wave-uniform, in two steps so that
+// the loads go out early and their results are used late: dest_loads issues every
+// load (the token's slot, lane l's request-table entry and lane l's slot of the
+// call), dest_finish decides.  A call has at most kFusedTokens (64) tokens, so one
+// slot per lane covers it; requests past the first 64 are read in dest_finish.
+struct DestLoads {
+  int64_t slot;     // slot_mapping[t]
+  int64_t s2;       // slot_mapping[lane] (-1 past the call)
+  int64_t st, nx, sq;  // query_start_loc[lane], [lane + 1], seq_lens[lane]
+};
+
+__device__ __forceinline__ DestLoads dest_loads(const StoreParams& p, int64_t t) {
+  const oscar_store_args_v1& a = p.a;
+  const int lane = threadIdx.x & 63;
+  DestLoads l;
+  l.slot = a.slot_mapping[t];
+  l.s2 = lane < a.num_tokens ? a.slot_mapping[lane] : -1;
+  const bool in = lane < a.num_reqs && a.stage_mode == OSCAR_STAGE_WRITE;
+  l.st = in ? a.query_start_loc[lane] : a.num_tokens;
+  l.nx = in ? a.query_start_loc[lane + 1] : a.num_tokens;
+  l.sq = in ? a.seq_lens[lane] : 0;
+  return l;
+}
+
+__device__ Dest dest_finish(const StoreParams& p, int kind, int64_t t, const DestLoads& l) {
   const oscar_store_args_v1& a = p.a;
   const int lane = threadIdx.x & 63;
   const int64_t bs = a.cache.block_size;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   Dest d{};
-  // ---- loads: slot, the request table and every slot of the call
-  const int64_t slot = a.slot_mapping[t];
+  const int64_t slot = l.slot;
   // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
   // length and query end come from the same loads (qsl is non-decreasing)
   int64_t seq = 0, end = 0;
@@ -135,9 +159,12 @@ __device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t) {
     for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
       const int r = c0 + lane;
       const bool in = r < a.num_reqs;
-      const int64_t st = in ? a.query_start_loc[r] : a.num_tokens;
-      const int64_t nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
-      const int64_t sq = in ? a.seq_lens[r] : 0;
+      int64_t st = l.st, nx = l.nx, sq = l.sq;
+      if (c0 > 0) {
+        st = in ? a.query_start_loc[r] : a.num_tokens;
+        nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
+        sq = in ? a.seq_lens[r] : 0;
+      }
       const int64_t start = st < a.num_tokens ? st : a.num_tokens;
       const uint64_t bal = __ballot(in && start <= t);
       if (bal) {
@@ -155,14 +182,10 @@ __device__ Dest vector_dest(const StoreParams& p, int kind, int64_t t) {
   d.seat = seat;
   // last writer: no later valid token of the call has the same slot / seat
   {
-    bool later_slot = false, later_seat = false;
-    for (int64_t c0 = 0; c0 < a.num_tokens; c0 += 64) {
-      const int64_t t2 = c0 + lane;
-      const int64_t s2 = t2 < a.num_tokens ? a.slot_mapping[t2] : -1;
-      const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
-      later_slot |= later && s2 == slot;
-      if (window) later_seat |= later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
-    }
+    const int64_t t2 = lane, s2 = l.s2;
+    const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
+    const bool later_slot = later && s2 == slot;
+    const bool later_seat = window && later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
     d.slot_win = !__any(later_slot);
     d.seat_win = window && !__any(later_seat);
     // standalone KV update: every written seat loses its window copy
@@ -247,142 +270,147 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
 
 
 // Calls of at most kFusedTokens tokens (decode and MTP steps): one launch of
-// workgroups (token, vectors, column slice).  A workgroup rotates its vectors -- one
-// K or V vector (token, kv head), or kQPW query heads of a token -- for one slice of
-// kSliceCols output columns, so that no compute unit streams more than D x kSliceCols
-// of R: each thread loads RPT rows x 4 columns of the slice straight into registers,
-// the products accumulate in fp64 and the KP parts of the contraction are added in
-// order (the fp32 result is the correctly rounded one).  Query slices go to
+// workgroups (slice, vector group).  The vectors of a kind -- K and V rows (token, kv
+// head), query rows (token, q head) -- are cut into groups of kSmallVecs consecutive
+// rows; a workgroup rotates one group for one slice of kSmallCols output columns, so
+// that it streams D x kSmallCols of R (32 KB) for kSmallVecs vectors.  Thread
+// (column pair cp, part kp) holds rows kp + kSmallParts * i of the slice's two
+// columns in registers, the products accumulate in fp64 (exact: bf16/fp16/fp32
+// inputs times fp32) and the kSmallParts parts of each output are added in order in
+// LDS, so the fp32 result is the correctly rounded one.  Query slices go to
 // query_rot.  K / V slices go to the read-path copies and to the workspace; the last
-// slice workgroup of a vector to arrive (one counter per vector that atomicInc wraps
-// back to zero) reads the whole vector back and quantizes, packs and scatters it in
-// place (quant_vector, winners by scanning).  The slices pass through the workspace
-// with agent-scope stores and loads, which bypass the per-XCD L2, ordered by the
-// store wait, the barrier and the counter; an agent-scope fence would instead write
-// back and invalidate the whole L2 in every workgroup.
+// slice workgroup of a group to arrive (one counter per group that atomicInc wraps
+// back to zero) reads the group's vectors back and quantizes, packs and scatters
+// them in place, one wave per vector (quant_vector; destinations and winners by
+// scanning the call's slot_mapping, computed by every slice workgroup while its
+// slice stores complete).  The slices pass through the workspace with agent-scope
+// stores and loads, which bypass the per-XCD L2, ordered by the store wait, the
+// barrier and the counter; an agent-scope fence would instead write back and
+// invalidate the whole L2 in every workgroup.
 constexpr int64_t kFusedTokens = 64;
-constexpr int kQPW = 2;         // query heads per fused workgroup
-constexpr int kSliceCols = 128;  // output columns per fused workgroup
+constexpr int kSmallVecs = 8;     // vectors per workgroup (one quantizing wave each)
+constexpr int kSmallCols = 32;    // output columns per workgroup
+constexpr int kSmallParts = 32;   // parts of the contraction (16 column pairs x 32 = 512 threads)
 constexpr int kSmallThreads = 512;
+static_assert(kFusedTokens <= 64, "dest_loads reads one slot of the call per lane");
+
+// vector groups of each kind of a small call
+__host__ __device__ inline int64_t small_groups(int64_t vectors) { return (vectors + kSmallVecs - 1) / kSmallVecs; }
 
 template <int D, int XT>
 __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams p) {
-  constexpr int SC = D < kSliceCols ? D : kSliceCols;
-  constexpr int NS = D / SC;            // column slices of a vector
-  constexpr int CG = SC / 4;            // 4-column groups of a slice
-  constexpr int KP = kSmallThreads / CG;     // parts of the contraction
-  constexpr int RPT = D / KP;           // rows of R per thread
-  static_assert(RPT >= 1 && D % KP == 0 && kQPW * 4 * CG <= kSmallThreads, "slice shape");
+  constexpr int NS = D / kSmallCols;   // slices of a vector
+  constexpr int RPT = D / kSmallParts;  // rows of R per thread (consecutive)
+  static_assert(kSmallVecs * kSmallCols <= kSmallThreads && kSmallThreads == 16 * kSmallParts && RPT % 2 == 0,
+                "slice shape");
   const oscar_store_args_v1& a = p.a;
   const int64_t hk = a.cache.num_kv_heads;
-  const int64_t t = blockIdx.x;
-  const int yb = blockIdx.y;
-  const int c0 = blockIdx.z * SC;
-  const int kind = yb < hk ? KIND_K : (yb < 2 * hk ? KIND_V : KIND_Q);
-  const int64_t h0 = kind == KIND_K ? yb : (kind == KIND_V ? yb - hk : (int64_t)(yb - 2 * hk) * kQPW);
+  const int64_t nkv = a.num_tokens * hk, nq = a.num_tokens * a.num_q_heads;
+  const int64_t gkv = small_groups(nkv);
+  const int c0 = blockIdx.x * kSmallCols;
+  const int64_t gy = blockIdx.y;
+  const int kind = gy < gkv ? KIND_K : (gy < 2 * gkv ? KIND_V : KIND_Q);
+  const int64_t grp = kind == KIND_K ? gy : (kind == KIND_V ? gy - gkv : gy - 2 * gkv);
   const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
-  const int nv = kind == KIND_Q ? (heads - h0 < kQPW ? (int)(heads - h0) : kQPW) : 1;
+  const int64_t count = kind == KIND_Q ? nq : nkv;
+  const int64_t v0 = grp * kSmallVecs;  // first vector (token * heads + head) of the group
+  const int nv = count - v0 < kSmallVecs ? (int)(count - v0) : kSmallVecs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cg = tid % CG, kp = tid / CG;
+  const int cp = tid & 15, kp = tid >> 4;
+  const bool kv = kind != KIND_Q;
   const void* src = kind == KIND_K ? a.key : (kind == KIND_V ? a.value : a.query);
   const int64_t src_stride = kind == KIND_K ? a.key_stride_token
                            : (kind == KIND_V ? a.value_stride_token : a.query_stride_token);
   const float* R = (kind == KIND_V) ? a.rv : a.rk;
   void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
 
-  __shared__ float s_x[kQPW][D];
-  __shared__ double s_red[KP][kQPW * 4 * CG];
-  __shared__ float s_y[kQPW][SC];
-  __shared__ float s_row[D];
-  __shared__ float s_clip;
+  __shared__ __attribute__((aligned(16))) double s_x[kSmallVecs][D];
+  __shared__ double s_red[kSmallParts][kSmallVecs * kSmallCols];
+  __shared__ float s_row[kSmallVecs][D];
+  __shared__ float s_clip[kSmallVecs];
   __shared__ int s_last;
-  // this thread's rows kp + KP * i of the slice: issued first, used after the barrier
-  f32x4 r4[RPT];
+  // this thread's rows kp * RPT + i of the slice's columns c0 + 2 cp, + 1: issued
+  // first, used after the barrier
+  f32x2 r2[RPT];
   if (R != nullptr) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) r4[i] = *(const f32x4*)(R + (int64_t)(kp + KP * i) * D + c0 + 4 * cg);
+    for (int i = 0; i < RPT; ++i) r2[i] = *(const f32x2*)(R + (int64_t)(kp * RPT + i) * D + c0 + 2 * cp);
   }
-  // the destination of a K / V vector: its loads overlap the rotation (only the last
-  // slice to arrive uses it)
-  Dest dest{};
-  if (kind != KIND_Q && wave == 0) dest = vector_dest(p, kind, t);
-  // the input vectors (fp32 in LDS; slots past nv are zero)
-  for (int e = tid; e < kQPW * D; e += kSmallThreads)
-    if (e >= nv * D) s_x[e / D][e % D] = 0.f;
-  for (int e = tid; e < nv * (D / 8); e += kSmallThreads) {
+  // the group's input vectors (fp64 in LDS; rows past nv are zero)
+  for (int e = tid; e < kSmallVecs * (D / 8); e += kSmallThreads) {
     const int v = e / (D / 8), k8 = (e % (D / 8)) * 8;
-    float xv[8];
-    load8<XT>(src, t * src_stride + (h0 + v) * D + k8, xv);
+    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (v < nv) {
+      const int64_t vi = v0 + v;
+      load8<XT>(src, (vi / heads) * src_stride + (vi % heads) * D + k8, xv);
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s_x[v][k8 + j] = xv[j];
+    for (int j = 0; j < 8; ++j) s_x[v][k8 + j] = (double)xv[j];
   }
+  // the destination loads of this wave's K / V vector (the token of vector v0 +
+  // wave): out with the operands, used after the products
+  const int64_t vw = v0 + wave, t = vw / hk, h = vw % hk;
+  DestLoads dl{};
+  if (kv && wave < nv) dl = dest_loads(p, t);
   __syncthreads();
-  double acc[kQPW][4];
+  double acc[kSmallVecs][2];
   if (R != nullptr) {
 #pragma unroll
-    for (int v = 0; v < kQPW; ++v)
+    for (int v = 0; v < kSmallVecs; ++v) acc[v][0] = acc[v][1] = 0.0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[v][j] = 0.0;
+    for (int i = 0; i < RPT; i += 2) {
+      const double r00 = r2[i][0], r01 = r2[i][1], r10 = r2[i + 1][0], r11 = r2[i + 1][1];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-#pragma unroll
-      for (int v = 0; v < kQPW; ++v) {
-        const double x = s_x[v][kp + KP * i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[v][j] = fma(x, (double)r4[i][j], acc[v][j]);
-      }
-  } else {
-#pragma unroll
-    for (int v = 0; v < kQPW; ++v)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[v][j] = kp == 0 ? (double)s_x[v][c0 + 4 * cg + j] : 0.0;
-  }
-  // the KP parts to LDS; thread e < kQPW * SC adds the parts of output e in order
-#pragma unroll
-  for (int v = 0; v < kQPW; ++v)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_red[kp][(v * 4 + j) * CG + cg] = acc[v][j];
-  __syncthreads();
-  if (tid < kQPW * 4 * CG) {
-    double sum = 0.0;
-#pragma unroll 8
-    for (int w = 0; w < KP; ++w) sum += s_red[w][tid];
-    const int v = tid / (4 * CG), j = (tid / CG) % 4, g4 = tid % CG;
-    s_y[v][4 * g4 + j] = (float)sum;
-  }
-  __syncthreads();
-  if (tid < kQPW * CG) {
-    const int v = tid / CG, g4 = tid % CG;
-    if (v < nv) {
-      const f32x4 y4 = *(const f32x4*)&s_y[v][4 * g4];
-      float y[4] = {y4[0], y4[1], y4[2], y4[3]};
-      const int64_t hq = kind == KIND_Q ? a.num_q_heads : hk;
-      if (rot_out != nullptr) store4<XT>(rot_out, (t * hq + h0 + v) * D + c0 + 4 * g4, y);
-      if (kind != KIND_Q) {
-        // agent-coherent stores (past this XCD's L2), read back the same way below
-        float* yw = p.y + (((int64_t)kind * a.num_tokens + t) * hk + h0) * D + c0 + 4 * g4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) __hip_atomic_store(yw + j, y[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int v = 0; v < kSmallVecs; ++v) {
+        const double2 x = *(const double2*)&s_x[v][kp * RPT + i];
+        acc[v][0] = fma(x.y, r10, fma(x.x, r00, acc[v][0]));
+        acc[v][1] = fma(x.y, r11, fma(x.x, r01, acc[v][1]));
       }
     }
+  } else {
+#pragma unroll
+    for (int v = 0; v < kSmallVecs; ++v)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[v][j] = kp == 0 ? s_x[v][c0 + 2 * cp + j] : 0.0;
   }
-  if (kind == KIND_Q) return;
+  // the parts to LDS; thread e < kSmallVecs * kSmallCols adds the parts of output e
+  // (vector e / kSmallCols, column e % kSmallCols) in order
+#pragma unroll
+  for (int v = 0; v < kSmallVecs; ++v)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) s_red[kp][v * kSmallCols + 2 * cp + j] = acc[v][j];
+  __syncthreads();
+  if (tid < kSmallVecs * kSmallCols) {
+    double sum = 0.0;
+#pragma unroll 8
+    for (int w = 0; w < kSmallParts; ++w) sum += s_red[w][tid];
+    const int v = tid / kSmallCols, col = c0 + tid % kSmallCols;
+    if (v < nv) {
+      const float y = (float)sum;
+      const int64_t vi = v0 + v;
+      if (rot_out != nullptr) store_elem(rot_out, XT, vi * D + col, y);
+      // agent-coherent stores (past this XCD's L2), read back the same way below
+      if (kv) __hip_atomic_store(p.y + ((int64_t)kind * nkv + vi) * D + col, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (!kv) return;
+  Dest dest{};
+  if (wave < nv) dest = dest_finish(p, kind, t, dl);
   // the slice is written (stores complete before the barrier): count it in; the last
-  // of the vector's slices to arrive goes on
+  // of the group's slices to arrive goes on
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if constexpr (NS > 1) {
-    if (tid == 0)
-      s_last = atomicInc(&a.arrivals[((int64_t)kind * a.num_tokens + t) * hk + h0], NS - 1) == NS - 1;
+    if (tid == 0) s_last = atomicInc(&a.arrivals[(int64_t)kind * gkv + grp], NS - 1) == NS - 1;
     __syncthreads();
     if (!s_last) return;
   }
-  if (wave != 0) return;
-  const float* yv = p.y + (((int64_t)kind * a.num_tokens + t) * hk + h0) * D + 4 * (lane < D / 4 ? lane : 0);
+  if (wave >= nv) return;
+  const float* yv = p.y + ((int64_t)kind * nkv + vw) * D + 4 * (lane < D / 4 ? lane : 0);
   f32x4 x4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) x4[j] = __hip_atomic_load(yv + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  quant_vector<D>(p, kind, t, h0, dest, x4, s_row, &s_clip);
+  quant_vector<D>(p, kind, t, h, dest, x4, s_row[wave], &s_clip[wave]);
 }
 
 
@@ -1295,8 +1323,8 @@ int launch_store(const StoreParams& p, int cu_count, hipStream_t s) {
   const int XT = p.a.kv_dtype;
   if (p.a.num_tokens <= kFusedTokens) {
     const int64_t hk = p.a.cache.num_kv_heads;
-    const int64_t qg = p.a.query_rot != nullptr ? (p.a.num_q_heads + kQPW - 1) / kQPW : 0;
-    dim3 grid((unsigned)p.a.num_tokens, (unsigned)(2 * hk + qg), (unsigned)(D < kSliceCols ? 1 : D / kSliceCols));
+    const int64_t qg = p.a.query_rot != nullptr ? small_groups(p.a.num_tokens * p.a.num_q_heads) : 0;
+    dim3 grid((unsigned)(D / kSmallCols), (unsigned)(2 * small_groups(p.a.num_tokens * hk) + qg));
     if (XT == OSCAR_BF16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_BF16>), grid, dim3(kSmallThreads), 0, s, p);
     else if (XT == OSCAR_F16) hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F16>), grid, dim3(kSmallThreads), 0, s, p);
     else hipLaunchKernelGGL((store_small_kernel<D, OSCAR_F32>), grid, dim3(kSmallThreads), 0, s, p);
