@@ -161,11 +161,19 @@ int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
  * of their own, the history tiles between them to the others, each range
  * round-robin (item i of k: tiles first + i, first + i + k, ...), or the whole
  * group as one range where that takes fewer items, so that the most expensive
- * item is as cheap as target_items allows.  Item record, int32[8]:
- *   [0] request  [1] kv_head | n_q << 16  [2] first tile  [3] tile stride
+ * item is as cheap as target_items allows.  A request with more than 32 rows per
+ * kv head (n_q * group > 32; group <= 32) is planned as sub-requests of 32 / group
+ * query tokens, each a group of its own: sub-request [a, b) of a request of n_q
+ * queries and length seq has seq - n_q + b keys, its query i sees keys
+ * [0, seq - n_q + a + i + 1), and with has_new the keys from seq - n_q on are the
+ * current chunk's rows (a = the sub-request's offset in the chunk).  Item record,
+ * int32[8]:
+ *   [0] request  [1] kv_head | n_q << 16  [2] first tile
+ *   [3] tile stride (bits 0-11) | offset a in the chunk << 12
  *   [4] tile count  [5] partial slot  [6] first query token  [7] seq length
- * Group record, int32[OSCAR_GROUP_INTS]: request, kv head, first partial slot,
- * slot count, first query token, query count, 0, 0. */
+ * (n_q, first query token and seq length of the sub-request).  Group record,
+ * int32[OSCAR_GROUP_INTS]: request, kv head, first partial slot, slot count, first
+ * query token, query count, 0, 0. */
 #define OSCAR_WORK_INTS 8
 #define OSCAR_GROUP_INTS 8
 typedef struct oscar_plan_v1 {
@@ -261,14 +269,15 @@ int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream);
 
 /* ---- native decode step ------------------------------------------------------
  * One call per decode-shaped forward of the impl (backend.py:249-393 for batches whose
- * requests all have history and <= 32 rows per KV head: decode, MTP verification,
- * cache-only decode).  The call classifies the batch from the host metadata, builds
+ * requests all have history: decode, MTP verification, cache-only decode, and cached
+ * chunks of up to 16384 rows per KV head, which the plan cuts into 32-row sub-requests).  The call classifies the batch from the host metadata, builds
  * the split-K plan on the host, stages every integer array the kernels read through
  * the context's pinned ring in ONE host-to-device copy, and enqueues the store (or the
  * query rotation when there are no new tokens), the split-K decode and merge, and the
  * inverse rotation into `output` -- with no Python in between.  It returns
- * OSCAR_STEP_NOT_DECODE (nothing enqueued) when a request is history-free, longer than
- * 32 rows, or the requests do not tile [0, num_tokens): the caller then takes the
+ * OSCAR_STEP_NOT_DECODE (nothing enqueued) when a request is history-free, its current
+ * chunk has more than 16384 rows per KV head, Hq / Hk exceeds 32, the plan outgrows a
+ * ring slot, or the requests do not tile [0, num_tokens): the caller then takes the
  * general path.
  *
  * The context holds a ring of pinned host and device metadata slots, reused once the

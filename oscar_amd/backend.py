@@ -8,8 +8,9 @@ arithmetic runs in liboscar_amd.so:
 * write  ``ops.store``: rotate (correctly rounded), sort-clip, INT2 quantize / pack /
          scatter with last-writer-wins, owner tags and FP32 window, plus the rotated
          q/k/v the read path needs;
-* read   ``ops.attention_decode`` (requests of <= 32 rows per KV head),
-         ``ops.attention_prefill`` (long continuation chunks; history-free requests in
+* read   ``ops.attention_decode`` (cached requests; chunks of more than 32 rows per KV
+         head as 32-row sub-requests of the plan, up to MAX_SPLIT_ROWS),
+         ``ops.attention_prefill`` (longer continuation chunks; history-free requests in
          the original domain), then the inverse rotation ``ops.rotate(out_rot, R_v^T)``.
 
 Host work per call is bounded: the batch is classified on the host from the
@@ -35,6 +36,12 @@ from .format import K_IDX_OFF, VALUES_PER_BYTE, check_d
 from .rotation import get_layer_rotation
 
 MAX_DECODE_ROWS = 32  # rows (query tokens x heads per KV head) of one decode MFMA tile
+# A cached chunk of more rows per KV head runs through the split-K decode as
+# sub-requests of MAX_DECODE_ROWS rows (each streams the request's history once), up to
+# this many rows; longer chunks go to the MFMA prefill, which decodes the history once
+# and shares it between query tiles but walks it serially per query tile (at 24576
+# history tokens: 24-156 us for chunks of 8-400 tokens against 1.1 ms).
+MAX_SPLIT_ROWS = 32 * 512
 
 
 # ---------------------------------------------------------------- metadata
@@ -130,8 +137,9 @@ class _Batch:
     seqs: list
     actual: int
     fresh: list = field(default_factory=list)   # no history: original-domain prefill
-    short: list = field(default_factory=list)   # cached, <= 32 rows per KV head: decode
-    long: list = field(default_factory=list)    # cached, more rows: prefill / split
+    short: list = field(default_factory=list)   # cached, split-K decode (sub-requests of
+                                                # <= 32 rows per KV head for longer chunks)
+    long: list = field(default_factory=list)    # cached chunk of more than MAX_SPLIT_ROWS: prefill
 
     @classmethod
     def classify(cls, qsl, seqs, actual, has_new, group):
@@ -142,7 +150,7 @@ class _Batch:
                 continue
             if has_new and b.seqs[i] == n:
                 b.fresh.append(i)
-            elif n * group <= MAX_DECODE_ROWS:
+            elif group <= MAX_DECODE_ROWS and (not has_new or n * group <= MAX_SPLIT_ROWS):
                 b.short.append(i)
             else:
                 b.long.append(i)
@@ -152,7 +160,8 @@ class _Batch:
 
     @property
     def decode_only(self) -> bool:
-        """Every active request decode-shaped: the plan runs over the batch as it is."""
+        """Every active request goes to the split-K decode: the plan runs over the batch
+        as it is."""
         return not self.fresh and not self.long
 
     @property
@@ -447,8 +456,8 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             store_qsl = [min(s, n_md) for s in qsl]
             parts += [np.asarray(store_qsl, np.int32), np.asarray(seqs[:len(qsl) - 1] or [0], np.int32)]
         plan, route = None, None
-        if batch.short or (batch.long and not has_new):
-            route = self._decode_route(batch, has_new, group)
+        if batch.short:
+            route = self._decode_route(batch)
             plan = ops.plan_decode(route["qsl"], route["seqs"], has_new=has_new, num_kv_heads=hk,
                                    group=group, head_dim=d, device=dev, window=window,
                                    upload_now=False)
@@ -526,23 +535,19 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         self._last_lse = lse
         return output
 
-    def _decode_route(self, batch: _Batch, has_new: bool, group: int) -> dict:
-        """Requests for the split-K decode.  A decode-only batch is planned as it is (the
-        plan's request r is metadata request r: no gathers).  Otherwise the decode-shaped
-        requests, and (cache-only) the long ones cut into sub-requests of <= 32 rows,
-        form a compact batch: sub-request j of request i keeps right-aligned causality by
-        seeing the keys up to its own last query."""
+    def _decode_route(self, batch: _Batch) -> dict:
+        """Requests for the split-K decode (the planner cuts chunks of more than 32 rows
+        per KV head into sub-requests).  A decode-only batch is planned as it is (the
+        plan's request r is metadata request r: no gathers); otherwise the decode
+        requests form a compact batch, gathered by row and block-table row."""
         if batch.decode_only:
             return dict(identity=True, qsl=batch.qsl, seqs=batch.seqs, index_parts=[])
-        step = max(1, MAX_DECODE_ROWS // group)
         sub_qsl, sub_seqs, ids, req = [0], [], [], []
-        for i in batch.short + ([] if has_new else batch.long):
-            a, b, seq = batch.qsl[i], batch.qsl[i + 1], batch.seqs[i]
-            for s in range(a, b, step):
-                e = min(b, s + step)
-                ids.extend(range(s, e))
-                req.append(i)
-                sub_qsl.append(sub_qsl[-1] + e - s)
-                sub_seqs.append(seq - (b - e))
+        for i in batch.short:
+            a, b = batch.qsl[i], batch.qsl[i + 1]
+            ids.extend(range(a, b))
+            req.append(i)
+            sub_qsl.append(sub_qsl[-1] + b - a)
+            sub_seqs.append(batch.seqs[i])
         return dict(identity=False, qsl=sub_qsl, seqs=sub_seqs,
                     index_parts=[np.asarray(ids, np.int64), np.asarray(req, np.int64)])

@@ -62,6 +62,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 32;
 constexpr int kMaxItemTokens = 8192; // keys per item (32 tiles per wave)
 constexpr int kMaxPages = kMaxItemTokens / kTile + 2;
+constexpr int kMaxStride = 0xfff;     // item record: tile stride in bits 0-11 of word 3
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.f;         // max drift (log2 units) before O is rescaled
@@ -254,19 +255,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   // j < count (32 keys each), partial slot, the request's first query token and length
   const int32_t* it = A.items + (int64_t)blockIdx.x * OSCAR_WORK_INTS;
   const int req = it[0], kvh = it[1] & 0xffff, nq = it[1] >> 16;
-  const int first = it[2], stride = it[3], count = it[4], part = it[5];
+  const int first = it[2], stride = it[3] & kMaxStride, off = it[3] >> 12, count = it[4], part = it[5];
   const int qa = it[6], seq = it[7];
   const int G = P.group;
   const bool has_new = A.k_new != nullptr;
-  const int hist = has_new ? seq - nq : seq;
+  // keys [hist, seq) are the current chunk's; this (sub-)request's queries start at
+  // offset `off` of the chunk, whose first token is qa - off
+  const int hist = has_new ? seq - nq - off : seq;
+  const int cur0 = qa - off;
   const int nrows = nq * G;
   const int bs = (int)A.cache.block_size;  // a multiple of 32
   const int64_t hk = A.cache.num_kv_heads;
   if (part < 0 || part >= A.num_items) return;
   // an item that breaks oscar_attn_plan_v1's rules poisons its partial (NaN LSE, so
   // the merged rows are NaN) instead of reading out of bounds
-  if (req < 0 || req >= A.num_reqs || kvh >= hk || nq < 1 || nrows > 32 || hist < 0 ||
-      qa < 0 || qa + nq > A.num_tokens || first < 0 || stride < 1 || count < 0 ||
+  if (req < 0 || req >= A.num_reqs || kvh >= hk || nq < 1 || nrows > 32 || hist < 0 || off < 0 ||
+      cur0 < 0 || qa + nq > A.num_tokens || first < 0 || stride < 1 || count < 0 ||
       count > kMaxItemTokens / kTile ||
       (count > 0 && (first + (int64_t)stride * (count - 1)) * kTile >= seq)) {
     if (tid < 32) P.part_lse[(int64_t)part * 32 + tid] = NAN;
@@ -521,7 +525,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
     const int bp = t0 + bt;
     const uint8_t* ks = kbase + (int64_t)blk * ks0 + (int64_t)(off0 + bt) * ks1;
     const uint8_t* vs = vbase + (int64_t)blk * vs0 + (int64_t)(off0 + bt) * vs1;
-    const int64_t cur_off = (int64_t)(qa + (b_cur ? bp - hist : 0)) * A.kv_new_stride_token + (int64_t)kvh * D;
+    const int64_t cur_off = (int64_t)(cur0 + (b_cur ? bp - hist : 0)) * A.kv_new_stride_token + (int64_t)kvh * D;
     const int64_t seat_row = ((int64_t)seat0 + off0 + bt) * hk + kvh;  // staged row of the token
     smeta = b_codes ? *(const u32x2*)ks : u32x2{0u, 0u};
 #pragma unroll
@@ -1064,6 +1068,7 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // expected recent window and the slow-path tiles at the end).
 struct PlanGroup {
   int req, kvh, n, he, ts;
+  int qa, nq, seq, off;  // the (sub-)request: first query token, queries, visible keys, offset in the chunk
   int first_slot;
   int64_t kh, kb, kt;  // items of head, body, tail (split), or kb items over all tiles
   bool split;
@@ -1139,37 +1144,52 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
   // is dealt as one range.  The bound C on an item's cost (history tiles + kSlowCost
   // per expected slow tile) is the smallest that keeps the item count within
   // target_items (at least one item per group; at most chunk_tokens keys per item).
+  // A request with more than 32 rows per KV head is planned as sub-requests of
+  // sub = 32 / group query tokens each (one 32-row MFMA tile): sub-request [a, b) of a
+  // request of nq queries and length seq sees seq - nq + b keys and keeps the
+  // request's causality (its query i sees keys [0, seq - nq + a + i + 1)); with a
+  // current chunk, keys from seq - nq on are the chunk's, which the item record
+  // carries as the sub-request's offset a in the chunk.
+  if (group > 32) return fail(-22, "oscar_attn_plan_v1: %d query heads per KV head > 32", group);
+  const int sub = 32 / group;
   int ngroups = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int nq = qsl[r + 1] - qsl[r];
     if (nq <= 0) continue;
-    if (nq * group > 32) return fail(-22, "oscar_attn_plan_v1: request %d has %d rows > 32", r, nq * group);
     if (seqs[r] < 0 || (has_new && seqs[r] < nq))
       return fail(-22, "oscar_attn_plan_v1: sequence length must cover its query chunk");
-    ngroups += num_kv_heads;
+    if (has_new && nq > (1 << 19)) return fail(-22, "oscar_attn_plan_v1: query chunk of request %d too long", r);
+    ngroups += (int)ceil_div(nq, sub) * num_kv_heads;
     if (ngroups > (1 << 24)) return fail(-22, "oscar_attn_plan_v1: too many request x kv-head groups");
   }
   std::vector<PlanGroup> gl;
   gl.reserve((size_t)ngroups);
   for (int r = 0; r < num_reqs; ++r) {
-    const int nq = qsl[r + 1] - qsl[r];
-    if (nq <= 0) continue;
-    const int seq = seqs[r];
-    const int hist = has_new ? seq - nq : seq;
-    const int n = (int)ceil_div(seq, kTile);
-    // the slow path takes every tile that reaches the first masked or current key
-    int fe = hist < seq - nq + 1 ? hist : seq - nq + 1;
-    if (fe < 0) fe = 0;
-    int ts = fe / kTile;
-    if (recent_tokens > 0) {
-      const int w0 = seq - recent_tokens > 0 ? seq - recent_tokens : 0;
-      if (w0 / kTile < ts) ts = w0 / kTile;
+    const int nq_all = qsl[r + 1] - qsl[r];
+    for (int a = 0; a < nq_all; a += sub) {
+      const int b = a + sub < nq_all ? a + sub : nq_all;
+      const int nq = b - a;
+      // (cache-only requests may be shorter than their queries: a sub-request that sees
+      // no key keeps 0 keys, which leaves its rows empty as the request's own limit does)
+      const int seq = seqs[r] - (nq_all - b) > 0 ? seqs[r] - (nq_all - b) : 0;
+      const int off = has_new ? a : 0;
+      const int hist = has_new ? seq - nq - off : seq;
+      const int n = (int)ceil_div(seq, kTile);
+      // the slow path takes every tile that reaches the first masked or current key
+      int fe = hist < seq - nq + 1 ? hist : seq - nq + 1;
+      if (fe < 0) fe = 0;
+      int ts = fe / kTile;
+      if (recent_tokens > 0) {
+        const int w0 = seq - recent_tokens > 0 ? seq - recent_tokens : 0;
+        if (w0 / kTile < ts) ts = w0 / kTile;
+      }
+      if (ts > n) ts = n;
+      int he = 0;
+      if (sink_tokens > 0) he = (int)ceil_div(sink_tokens < hist ? sink_tokens : hist, kTile);
+      if (he >= ts) he = ts = 0;  // the expected window covers the group
+      for (int h = 0; h < num_kv_heads; ++h)
+        gl.push_back({r, h, n, he, ts, qsl[r] + a, nq, seq, off, 0, 0, 0, 0, false});
     }
-    if (ts > n) ts = n;
-    int he = 0;
-    if (sink_tokens > 0) he = (int)ceil_div(sink_tokens < hist ? sink_tokens : hist, kTile);
-    if (he >= ts) he = ts = 0;  // the expected window covers the group
-    for (int h = 0; h < num_kv_heads; ++h) gl.push_back({r, h, n, he, ts, 0, 0, 0, 0, false});
   }
   const int64_t max_tiles = chunk_tokens / kTile;
   auto items_for = [&](int64_t C) {
@@ -1192,6 +1212,8 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
     if (k > max_k) max_k = k;
     if (nitems > (1 << 26)) return fail(-22, "oscar_attn_plan_v1: too many work items");
   }
+  // the item record keeps the tile stride (<= items of a group) in 12 bits
+  if (max_k > kMaxStride) return fail(-22, "oscar_attn_plan_v1: %lld items in one group > %d", (long long)max_k, kMaxStride);
   plan->num_items = (int32_t)nitems;
   plan->num_groups = ngroups;
   plan->partial_bytes = nitems * 32 * (head_dim + 1) * (int64_t)sizeof(float);
@@ -1225,17 +1247,16 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
       const int64_t k = G.split ? G.kh + G.kb + G.kt : G.kb;
       if (pos >= k) continue;
       int32_t* it = items + idx++ * OSCAR_WORK_INTS;
-      const int nq = qsl[G.req + 1] - qsl[G.req];
       int first, stride, count;
       group_item(G, pos, first, stride, count);
       it[0] = G.req;
-      it[1] = G.kvh | (nq << 16);
+      it[1] = G.kvh | (G.nq << 16);
       it[2] = first;
-      it[3] = stride;
+      it[3] = stride | (G.off << 12);
       it[4] = count;
       it[5] = G.first_slot + (int)pos;
-      it[6] = qsl[G.req];
-      it[7] = seqs[G.req];
+      it[6] = G.qa;
+      it[7] = G.seq;
     }
   for (int q = 0; q < ngroups; ++q) {
     const PlanGroup& G = gl[(size_t)q];
@@ -1244,8 +1265,8 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
     gr[1] = G.kvh;
     gr[2] = G.first_slot;
     gr[3] = (int)(G.split ? G.kh + G.kb + G.kt : G.kb);
-    gr[4] = qsl[G.req];
-    gr[5] = qsl[G.req + 1] - qsl[G.req];
+    gr[4] = G.qa;
+    gr[5] = G.nq;
     gr[6] = gr[7] = 0;
   }
   return (int)nitems;

@@ -2,7 +2,8 @@
 //
 // Replaces the Python orchestration of oscar_ascend/backend.py:249-393 (forward ->
 // write + window -> _streaming_attention -> inverse rotation) for batches whose
-// requests all have history and at most 32 rows per KV head.  Per call: classify the
+// requests all have history (chunks of more than 32 rows per KV head run as sub-requests
+// of the split-K decode, up to kMaxSplitRows).  Per call: classify the
 // batch from the host metadata, build the split-K plan (oscar_attn_plan_v1) straight
 // into a pinned ring slot next to the request table, one host-to-device copy of the
 // slot, then the store (or the query rotation), the split-K decode + merge and the
@@ -16,6 +17,9 @@ namespace oscar {
 namespace {
 
 constexpr int kRingSlots = 32;
+// longest current chunk (rows per KV head) of a request the step takes: more rows go to
+// the prefill path, which decodes the history once for all of its query tiles
+constexpr int64_t kMaxSplitRows = 32 * 512;
 constexpr int64_t kSlotBytes = 64 << 10;  // request table + plan of up to ~1900 items
 constexpr int64_t kAlign = 256;
 
@@ -119,6 +123,7 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
   if (has_new != (a.value != nullptr)) return fail(-22, "oscar_decode_step_v1: key and value go together");
   if (has_new && !a.slot_mapping) return fail(-22, "oscar_decode_step_v1: slot_mapping required with new K/V");
   const int G = (int)(hq / hk);
+  if (G > 32) return OSCAR_STEP_NOT_DECODE;  // no 32-row tile holds one token's heads
   // ---- classify: every request decode-shaped, the requests tile [0, n)
   const int32_t* qsl = a.host_query_start_loc;
   const int32_t* seqs = a.host_seq_lens;
@@ -129,7 +134,8 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
     if (q1 < q0) return fail(-22, "oscar_decode_step_v1: query_start_loc must be non-decreasing");
     const int64_t nq = q1 - q0;
     if (nq == 0) continue;
-    if (nq * G > 32) return OSCAR_STEP_NOT_DECODE;
+    // chunks of more than 32 rows per KV head run as sub-requests, up to kMaxSplitRows
+    if (has_new && nq * G > kMaxSplitRows) return OSCAR_STEP_NOT_DECODE;
     if (has_new && seqs[r] == nq) return OSCAR_STEP_NOT_DECODE;  // history-free: prefill
     if (has_new && seqs[r] < nq) return fail(-22, "oscar_decode_step_v1: sequence length must cover its query chunk");
     if (seqs[r] < 0) return fail(-22, "oscar_decode_step_v1: negative sequence length");
@@ -144,13 +150,14 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
   uint8_t* host = ctx->host_ring + slot * kSlotBytes;
   uint8_t* dev = ctx->dev_ring + slot * kSlotBytes;
   // slot layout: qsl [B + 1] (clipped) | seqs [B] | groups | items
-  int ngroups = 0;
-  for (int r = 0; r < B; ++r) ngroups += clip(qsl[r + 1]) > clip(qsl[r]) ? (int)hk : 0;
+  // groups: (sub-)requests of 32 / G query tokens x kv heads
+  int64_t ngroups = 0;
+  for (int r = 0; r < B; ++r) ngroups += (clip(qsl[r + 1]) - clip(qsl[r]) + 32 / G - 1) / (32 / G) * hk;
   const int64_t o_seqs = align_up((int64_t)(B + 1) * 4, 16);
   const int64_t o_groups = align_up(o_seqs + (int64_t)B * 4, 16);
   const int64_t o_items = align_up(o_groups + (int64_t)ngroups * OSCAR_GROUP_INTS * 4, 16);
-  if (o_items + OSCAR_WORK_INTS * 4 > kSlotBytes)
-    return fail(-28, "oscar_decode_step_v1: %d requests exceed the metadata slot", B);
+  if (o_items + OSCAR_WORK_INTS * 4 > kSlotBytes) return OSCAR_STEP_NOT_DECODE;  // too many requests for a slot
+  const int max_groups = (int)ngroups;
   int32_t* h_qsl = (int32_t*)host;
   for (int r = 0; r <= B; ++r) h_qsl[r] = (int32_t)clip(qsl[r]);
   int32_t* h_seqs = (int32_t*)(host + o_seqs);
@@ -163,7 +170,8 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
   const int target = a.target_items > 0 ? a.target_items : ctx->cu_count;
   int rc = oscar_attn_plan_v1(h_qsl, h_seqs, B, has_new, (int32_t)hk, G, (int32_t)d, 8192, target,
                               window ? a.sink_tokens_eff : 0, window ? a.recent_tokens : 0, h_items, max_items,
-                              h_groups, ngroups, &plan);
+                              h_groups, max_groups, &plan);
+  if (rc == -28) return OSCAR_STEP_NOT_DECODE;  // a plan larger than a ring slot: the general path
   if (rc < 0) return rc;
   const StepLayout L(n, hq, hk, d, plan.num_items);
   if (a.workspace_bytes < L.total) {

@@ -339,7 +339,8 @@ def plan_decode(qsl: list, seqs: list, *, has_new: bool, num_kv_heads: int, grou
     sink, recent = (int(x) for x in window)
     # one call with room for any plan the target allows (at most 3 ranges per group,
     # at most 256 tiles per item); a second, exact call only if that was too small
-    ngroups = num_kv_heads * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+    sub = max(1, 32 // group)  # query tokens per sub-request (32 rows per kv head)
+    ngroups = num_kv_heads * sum(-(-(b - a) // sub) for a, b in zip(qsl, qsl[1:]) if b > a)
     guess = max(target_items, 1) + 3 * ngroups + sum(-(-s // 8192) for s in seqs) * num_kv_heads
     items = np.zeros(max(guess, 1) * WORK_INTS, np.int32)
     groups = np.zeros(max(ngroups, 1) * GROUP_INTS, np.int32)

@@ -95,7 +95,20 @@ def plan(lib, qsl, seqs, has_new=True, hk=1, group=6, d=256, chunk=8192, target=
 
 
 def item_tiles(it):
-    return it[2] + it[3] * np.arange(it[4])
+    return it[2] + (it[3] & 0xFFF) * np.arange(it[4])
+
+
+def sub_requests(qsl, seqs, has_new, group):
+    """The planner's (sub-)requests: (request, first query token, queries, keys, offset
+    in the chunk) for every cut of 32 // group query tokens of a non-empty request."""
+    sub = 32 // group
+    out = []
+    for r, (a0, b0, s) in enumerate(zip(qsl, qsl[1:], seqs)):
+        nq = b0 - a0
+        for a in range(0, nq, sub):
+            b = min(nq, a + sub)
+            out.append((r, a0 + a, b - a, max(0, s - (nq - b)), a if has_new else 0))
+    return out
 
 
 PLAN_CASES = [
@@ -105,6 +118,8 @@ PLAN_CASES = [
     ([0, 4, 6], [1025, 702], True, 2, 4),
     ([0] + list(range(1, 65)), [2048 + 37 * i for i in range(64)], False, 1, 6),
     ([0] + list(range(1, 65)), [1024 + 487 * i for i in range(64)], False, 1, 6),
+    ([0, 40, 47, 48], [3040, 507, 9000], True, 1, 6),           # chunks of 240 and 42 rows
+    ([0, 20, 37], [700, 4017], False, 2, 4),                    # cache-only, 80 and 68 rows
 ]
 
 
@@ -121,23 +136,25 @@ def check_plan(lib, qsl, seqs, has_new, hk, group, window, target, d):
     assert cnt > 0
     assert sorted(items[:, 5].tolist()) == list(range(cnt))          # partial slots: a permutation
     assert p.partial_bytes == cnt * 32 * (d + 1) * 4
-    ngroups = hk * sum(1 for a, b in zip(qsl, qsl[1:]) if b > a)
+    subs = {(r, qa): (nq, seq, off) for r, qa, nq, seq, off in sub_requests(qsl, seqs, has_new, group)}
+    ngroups = hk * len(subs)
     # within the target, unless the groups need more: an item holds at most 256 tiles
-    floor = hk * sum(max(1, -(-(-(-s // TILE)) // 256)) for a, b, s in zip(qsl, qsl[1:], seqs) if b > a)
+    floor = hk * sum(max(1, -(-(-(-seq // TILE)) // 256)) for nq, seq, off in subs.values())
     assert cnt <= max(target, floor)
     for it in items:
         req, kvh, nq, first, stride, count, part, qa, seq = (it[0], it[1] & 0xFFFF, it[1] >> 16, *it[2:8])
-        assert nq == qsl[req + 1] - qsl[req] and qa == qsl[req] and seq == seqs[req]
+        stride, off = stride & 0xFFF, stride >> 12
+        assert subs[(req, qa)] == (nq, seq, off)
         assert 0 <= kvh < hk and nq * group <= 32
         assert 0 <= first and stride >= 1 and (count > 0 or (first == 0 and stride == 1))
         assert count <= 8192 // TILE
         assert count == 0 or (first + stride * (count - 1)) * TILE < seq   # no tile past the end
     # per group: every tile of [0, ceil(seq / 32)) exactly once, slots contiguous
     for req, kvh, first_slot, nslots, qa, nq, z0, z1 in groups:
-        assert qa == qsl[req] and nq == qsl[req + 1] - qsl[req] and z0 == z1 == 0
-        rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh)]
+        assert subs[(req, qa)][0] == nq and z0 == z1 == 0
+        rows = items[(items[:, 0] == req) & ((items[:, 1] & 0xFFFF) == kvh) & (items[:, 6] == qa)]
         assert sorted(rows[:, 5].tolist()) == list(range(first_slot, first_slot + nslots))
-        cover = np.zeros((seqs[req] + TILE - 1) // TILE, np.int64)
+        cover = np.zeros((subs[(req, qa)][1] + TILE - 1) // TILE, np.int64)
         for it in rows:
             np.add.at(cover, item_tiles(it), 1)
         assert (cover == 1).all()
@@ -156,6 +173,7 @@ def test_plan_random_requests_cover_every_tile_once(lib, seed):
         has_new = bool(rng.integers(2))
         nreq = int(rng.integers(1, 40))
         lens = rng.integers(0 if not has_new else 1, 32 // group + 1, nreq)
+        lens[rng.random(nreq) < 0.15] *= 7                          # more than 32 rows: sub-requests
         lens[rng.random(nreq) < 0.1] = 0                            # empty requests
         if lens.sum() == 0:
             lens[0] = 1
@@ -236,14 +254,25 @@ def test_plan_launch_order_interleaves_groups(lib):
     assert (np.diff(pos) >= 0).all()
 
 
+def test_plan_cuts_long_chunks_into_sub_requests(lib):
+    # a continuation chunk of 12 tokens at 6 heads per KV head (72 rows): sub-requests of
+    # 5, 5 and 2 queries, each its own group; their key ranges end at their last query
+    cnt, items, groups, _ = plan(lib, [0, 12], [5012], has_new=True, group=6)
+    assert groups[:, 4].tolist() == [0, 5, 10] and groups[:, 5].tolist() == [5, 5, 2]
+    for qa, nq in ((0, 5), (5, 5), (10, 2)):
+        rows = items[items[:, 6] == qa]
+        assert (rows[:, 7] == 5000 + qa + nq).all() and ((rows[:, 3] >> 12) == qa).all()
+        assert ((rows[:, 1] >> 16) == nq).all()
+
+
 def test_plan_splits_long_history_across_items(lib):
     _, items, _, _ = plan(lib, [0, 4], [100003], target=256)
     assert len(items) > 64 and items[:, 4].max() * TILE <= 8192
 
 
 def test_plan_rejects_bad_requests(lib):
-    cnt, *_ = plan(lib, [0, 6], [100], group=6)             # 36 rows > 32
-    assert cnt == -22 and b"rows" in lib.oscar_last_error()
+    cnt, *_ = plan(lib, [0, 1], [100], group=33)            # 33 heads per KV head: no 32-row tile
+    assert cnt == -22 and b"query heads" in lib.oscar_last_error()
     cnt, *_ = plan(lib, [0, 4], [3], has_new=True)          # sequence shorter than its chunk
     assert cnt == -22
     cnt, *_ = plan(lib, [0, 1], [10], d=96)

@@ -71,10 +71,13 @@ def emulate(items, g):
         ext.access("items", idx * 8 * 4, 32, "item record")
         req, kvh, nq = it[0], it[1] & 0xFFFF, it[1] >> 16
         first, stride, count, part, qa, seq = it[2:8]
-        hist = seq - nq if g["has_new"] else seq
+        stride, off = stride & 0xFFF, stride >> 12
+        hist = seq - nq - off if g["has_new"] else seq
+        cur0 = qa - off
         nrows = nq * G
         # the kernel's rule: a record outside the plan's contract poisons its partial
-        if (req < 0 or req >= g["num_reqs"] or kvh >= hk or nq < 1 or nrows > 32 or hist < 0 or qa < 0
+        if (req < 0 or req >= g["num_reqs"] or kvh >= hk or nq < 1 or nrows > 32 or hist < 0 or off < 0
+                or cur0 < 0
                 or qa + nq > g["num_tokens"] or first < 0 or stride < 1 or count < 0 or count > MAX_TILES
                 or (count > 0 and (first + stride * (count - 1)) * TILE >= seq)):
             ext.access("part_lse", part * 32 * 4, 32 * 4, "poisoned lse")
@@ -110,7 +113,7 @@ def emulate(items, g):
         if g["has_new"]:
             pos = (t0[:, None] + m[:, 0][None, :]).ravel()
             cur = pos[(pos >= hist) & (pos < seq)]
-            ext.access("kv_new", ((qa + cur - hist) * g["kv_stride"] + kvh * D) * 2, D * 2, "current row")
+            ext.access("kv_new", ((cur0 + cur - hist) * g["kv_stride"] + kvh * D) * 2, D * 2, "current row")
         ext.access("part_o", part * 32 * D * 4, 32 * D * 4, "item partial")
         ext.access("part_lse", part * 32 * 4, 32 * 4, "item lse")
     return ext.bad
@@ -129,6 +132,7 @@ def test_decode_accesses_stay_in_their_buffers(lib, seed):
         legacy = bool(rng.integers(2))
         nreq = int(rng.integers(1, 24))
         lens = rng.integers(0 if not has_new else 1, 32 // group + 1, nreq)
+        lens[rng.random(nreq) < 0.2] *= 9                           # chunks cut into sub-requests
         if lens.sum() == 0:
             lens[0] = 1
         qsl = [0] + np.cumsum(lens).tolist()

@@ -81,6 +81,12 @@ DECODE_CASES = [
     ("pages_1536", [5000, 300], [4, 2], {"bs": 1536}),
     ("legacy_hk2", [700, 2000], [4, 1], {"legacy": True, "hk": 2, "group": 3}),
     ("hint_wide", [3000, 5000], [4, 1], {"hint": (512, 2048), "target": 24}),
+    # chunks of more than 32 rows per KV head: sub-requests of 5 (4 at group 8) query
+    # tokens, whose later sub-requests see the chunk's earlier keys as current rows
+    ("chunk_240_rows", [3000, 500], [40, 7], {}),
+    ("chunk_d128_hk2", [1500, 40], [20, 9], {"d": 128, "hk": 2, "group": 4}),
+    ("chunk_no_window", [2000], [33], {"window": False, "target": 16}),
+    ("cache_only_long", [2000, 100], [12, 20], {"fresh": False}),
 ]
 
 

@@ -41,8 +41,10 @@ def test_forward_steps_match_oracle(cuda, qdt, ulp):
     q_dtype = "bf16" if qdt == torch.bfloat16 else "f16"
     lens = [0, 0]
     # (new tokens of request 0, of request 1): fresh prefills, MTP + single-token
-    # decode, a continuation chunk (routed to the prefill) beside a decode
-    for step, (n0, n1) in enumerate([(300, 700), (4, 1), (200, 1)]):
+    # decode, continuation chunks of 1200 and 2400 rows (the split-K decode, as 32-row
+    # sub-requests) beside a decode and an MTP step (the continuation prefill through
+    # the forward: test_config5_batched_forward)
+    for step, (n0, n1) in enumerate([(300, 700), (4, 1), (200, 1), (400, 3)]):
         news = [n0, n1]
         slots, qsl, seqs = [], [0], []
         for r, n in enumerate(news):
