@@ -1,8 +1,9 @@
 // Streaming split-K paged attention over the packed INT2 history (gfx950).
 //
 // Replaces oscar_ascend/kernels/slab_attention.py:376-476 (slab_attention) for
-// requests whose rows (query tokens x heads per KV head) fit one 32-row MFMA tile:
-// decode, MTP verification (1 + 3 drafts x 6 heads = 24 rows) and cache-only decode.
+// cached requests: decode, MTP verification (1 + 3 drafts x 6 heads = 24 rows),
+// cache-only decode, and chunks of more rows (query tokens x heads per KV head) than
+// one 32-row MFMA tile holds, which the plan cuts into sub-requests of 32 rows.
 // Semantics follow streaming_attention.py:134-196: query i of a request with n_q
 // queries and length seq sees keys [0, seq - n_q + i + 1); history keys come from
 // the packed cache unless the staging owner tag of their seat equals the physical
