@@ -161,7 +161,8 @@ int oscar_rotate_v1(const oscar_rotate_args_v1* args, void* stream);
  * of their own, the history tiles between them to the others, each range
  * round-robin (item i of k: tiles first + i, first + i + k, ...), or the whole
  * group as one range where that takes fewer items, so that the most expensive
- * item is as cheap as target_items allows.  A request with more than 32 rows per
+ * item is as cheap as target_items allows, with at most 128 items in a group (one
+ * load round of the merge) where the 256-tile item limit allows.  A request with more than 32 rows per
  * kv head (n_q * group > 32; group <= 32) is planned as sub-requests of 32 / group
  * query tokens, each a group of its own: sub-request [a, b) of a request of n_q
  * queries and length seq has seq - n_q + b keys, its query i sees keys

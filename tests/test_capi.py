@@ -265,6 +265,17 @@ def test_plan_cuts_long_chunks_into_sub_requests(lib):
         assert ((rows[:, 1] >> 16) == nq).all()
 
 
+def test_plan_caps_items_per_group(lib):
+    # one long request: at most 128 items (one load round of the merge's 8 waves x 16)
+    # however large the target
+    for seq, target in ((24580, 256), (100003, 1024), (40000, 4096)):
+        cnt, items, groups, p = plan(lib, [0, 4], [seq], target=target)
+        assert cnt == groups[0, 3] and cnt <= 128 and p.max_group_items == cnt
+    # 8 requests of that length still take the whole target
+    cnt, *_ = plan(lib, [0] + [4 * i for i in range(1, 9)], [24580] * 8, target=256)
+    assert 200 < cnt <= 256
+
+
 def test_plan_splits_long_history_across_items(lib):
     _, items, _, _ = plan(lib, [0, 4], [100003], target=256)
     assert len(items) > 64 and items[:, 4].max() * TILE <= 8192
