@@ -79,10 +79,13 @@ def test_forward_steps_match_oracle(cuda, qdt, ulp):
     assert np.array_equal(caches[1].view(torch.uint8).cpu().numpy(), oracle_layer.v8)
 
 
-@pytest.mark.parametrize("mode", ["mtp_window", "cache_only", "fp16_mtp"])
+@pytest.mark.parametrize("mode", ["mtp_window", "cache_only", "fp16_mtp", "long_chunks", "long_chunks_fresh"])
 def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
     """forward() on decode-shaped batches takes oscar_decode_step_v1 (one native call);
-    the same batch through the general Python path (_run) and the oracle agree."""
+    the same batch through the general Python path (_run) and the oracle agree.
+    long_chunks: chunks of 240 and 72 rows per KV head (sub-requests of the plan);
+    long_chunks_fresh: the same beside a history-free request, which the native step
+    declines and the general path routes as a compact decode batch plus a prefill."""
     from oscar_amd import backend as B
     from oracle.attention import attention_ref
 
@@ -90,6 +93,10 @@ def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
     qdt = torch.float16 if mode == "fp16_mtp" else torch.bfloat16
     fresh = mode != "cache_only"
     prefixes, lengths = [3000, 129, 700, 24579], [4, 1, 3, 4]
+    if mode == "long_chunks":
+        lengths = [40, 1, 12, 4]
+    if mode == "long_chunks_fresh":
+        prefixes, lengths = [3000, 0, 700, 24579], [40, 300, 12, 4]
     c = cases.make_case(prefixes, lengths, fresh=fresh, seed=77)
     d, hq, hk = 256, 6, 1
     impl = OscarAttentionBackendImplFactory()
@@ -116,11 +123,14 @@ def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
     tv = None if c["v"] is None else torch.from_numpy(c["v"]).to(dev).to(qdt).view(N, -1)
     calls = {"reads": impl._oscar_stats["reads"]}
     out_native = torch.empty(N, hq * d, dtype=qdt, device=dev)
-    assert impl._native_step(layer, tq, tk, tv, caches, md, out_native)
+    native = impl._native_step(layer, tq, tk, tv, caches, md, out_native)
+    assert native == (mode != "long_chunks_fresh")
     out_general = torch.empty_like(out_native)
     impl._run(layer, tq, tk, tv, caches, md, out_general, write=True)
     torch.cuda.synchronize()
-    assert impl._oscar_stats["reads"] == calls["reads"] + 2
+    assert impl._oscar_stats["reads"] == calls["reads"] + 1 + native
+    if not native:
+        out_native = out_general
     q_dtype = "f16" if qdt == torch.float16 else "bf16"
     ref_o, _ = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"], c["seqs"],
                              c["scale"], c["stage"], q_dtype=q_dtype)
