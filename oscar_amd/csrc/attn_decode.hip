@@ -923,33 +923,26 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
   const int bq = blockIdx.y, b = bq >> 2, q = bq & 3;
   const int e = bq * 64 + lane;  // f32x4 index in the partial
   // a record that breaks oscar_attn_plan_v1's rules: rows outside the call are not
-  // written at all; a bad item range turns the group's rows into NaN
-  if (a < 0 || nq < 1 || nq * G > 32 || (int64_t)a + nq > A.num_tokens || kvh < 0 ||
-      kvh >= A.cache.num_kv_heads)
-    return;
+  // written at all; a bad item range turns the group's rows into NaN.  Branch-free up
+  // to the stores (such a record reads no item and the NaN comes in with the result):
+  // early exits here measured 0.25 us slower per merge at config 4a.
+  const bool rows_bad = a < 0 || nq < 1 || nq * G > 32 || (int64_t)a + nq > A.num_tokens || kvh < 0 ||
+                        kvh >= A.cache.num_kv_heads;
   const bool bad = i0 < 0 || ni < 0 || (int64_t)i0 + ni > A.num_items;
+  const int nitems = (bad || rows_bad) ? 0 : ni;
   const bool row_ok = n < nq * G;
-  if (bad) {
-    if (wave > 0 || !row_ok) return;
-    const int tok = a + n / G, head = kvh * G + n % G;
-    float* orow = A.out_rot + ((int64_t)tok * A.num_q_heads + head) * D;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) orow[pv_d<D>(b, out_tok(4 * q + j, gg))] = NAN;
-    if (bq == 0 && gg == 0) A.lse[(int64_t)tok * A.num_q_heads + head] = NAN;
-    return;
-  }
-  const f32x4* po = (const f32x4*)P.part_o + (int64_t)i0 * C::NV + e;
-  const float* pl = P.part_lse + (int64_t)i0 * 32 + n;
+  const f32x4* po = (const f32x4*)P.part_o + (int64_t)(nitems ? i0 : 0) * C::NV + e;
+  const float* pl = P.part_lse + (int64_t)(nitems ? i0 : 0) * 32 + n;
   float M = -INFINITY, L = 0.f;
-  bool nan = false;
+  bool nan = bad;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int i = wave; i < ni; i += W * kBatch) {
+  for (int i = wave; i < nitems; i += W * kBatch) {
     float l[kBatch];
     f32x4 x[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int it = i + u * W;
-      const bool in = it < ni;
+      const bool in = it < nitems;
       l[u] = in ? pl[(int64_t)it * 32] : -INFINITY;
       x[u] = (in && row_ok) ? po[(int64_t)it * C::NV] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -1004,6 +997,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
     }
   }
   M = Mt;
+  if (rows_bad) return;
   float lse = -INFINITY;
   if (nan) {
     acc = f32x4{NAN, NAN, NAN, NAN};

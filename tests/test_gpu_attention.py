@@ -192,6 +192,42 @@ def test_decode_nan_propagates_through_merge(cuda):
     assert err_o <= OUT_TOL and err_l <= LSE_TOL
 
 
+def test_decode_bad_plan_records_poison_only_their_rows(cuda):
+    """Records that break the planner's rules (a group whose item range runs past the
+    plan, an item whose key tiles run past its sequence) turn that group's rows into NaN
+    (output and LSE) instead of reading out of bounds; every other group is unaffected."""
+    import dataclasses
+    from oscar_amd import ops
+
+    c = cases.make_case([2000, 1500, 300, 700], [4, 2, 1, 3])
+    out, lse, plan = run_decode(c, target=48)
+    ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                     c["seqs"], c["scale"], c["stage"])
+    check(out, lse, ref_out, ref_lse, "good plan")
+    groups = plan.host_groups.reshape(-1, 8).copy()
+    items = plan.host_items.reshape(-1, 8).copy()
+    groups[1, 3] = plan.num_items + 5                      # group 1: item range past the plan
+    g2 = groups[2]
+    it = items[(items[:, 0] == g2[0]) & (items[:, 6] == g2[4])][0]
+    idx = int(np.nonzero((items == it).all(axis=1))[0][0])
+    items[idx, 2] = 10 ** 6                                 # group 2: one item's tiles past its sequence
+    bad = dataclasses.replace(plan, host_items=items.reshape(-1), host_groups=groups.reshape(-1))
+    bad.adopt(ops.upload(bad.host_parts(), torch.device("cuda")))
+    kc = torch.from_numpy(c["k8"]).view(torch.int8).cuda()
+    vc = torch.from_numpy(c["v8"]).view(torch.int8).cuda()
+    stage = tuple(torch.from_numpy(a).cuda() for a in c["stage"])
+    o2, l2 = ops.attention_decode(dev(c["q"]), dev(c["k"]), dev(c["v"]), kc, vc, torch.from_numpy(c["bt"]).cuda(),
+                                  bad, c["scale"], stage, head_dim=256)
+    torch.cuda.synchronize()
+    o2, l2 = o2.cpu().numpy(), l2.cpu().numpy()
+    rows = {r: np.arange(c["qsl"][r], c["qsl"][r + 1]) for r in range(4)}
+    for r in (1, 2):
+        assert np.isnan(l2[rows[r]]).all() and np.isnan(o2[rows[r]]).all(), f"request {r} not poisoned"
+    for r in (0, 3):
+        assert np.array_equal(np.isnan(l2[rows[r]]), np.zeros_like(l2[rows[r]], bool))
+        assert np.abs(o2[rows[r]] - ref_out[rows[r]]).max() <= OUT_TOL
+
+
 def test_decode_plan_covers_each_history_token_once(cuda):
     c = cases.make_case([24579] * 8, [4] * 8)
     from oscar_amd import ops
