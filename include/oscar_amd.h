@@ -268,6 +268,26 @@ typedef struct oscar_prefill_args_v1 {
 int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim);
 int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream);
 
+/* Workspace for oscar_attn_prefill_v1 with the balanced split of the key ranges: the
+ * history values (as v1, rounded up to 256 bytes) plus the FP32 partials of the query
+ * tiles (128 GQA rows each) whose key range is cut into chunks of about half a compute
+ * unit's share of the call's work; a merge launch combines them (FP32 LSE merge,
+ * slab_attention.py:341-356).  The reference runs one prefill per request with no such
+ * split (prefill.py:69-72, slab_attention.py:376-476): this only changes how the work
+ * is spread over the chip.  oscar_attn_prefill_v1 splits when workspace_bytes is at
+ * least this size (and the workspace 16-byte aligned), else runs one workgroup per query
+ * tile.  Returns -22 for invalid arguments. */
+int64_t oscar_prefill_workspace_bytes_v2(int64_t history, int64_t num_tokens, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t head_dim);
+
+/* The split plan oscar_attn_prefill_v1 uses for these sizes (no counterpart in the
+ * reference; for tests and callers sizing their own workspace): out[0..5] = chunks of the
+ * heaviest tile (0: no split), key tiles (32 keys) per chunk, query tiles, first query tile
+ * with two chunks, workgroups per KV head, partial slots per KV head; out[6 + c], c <=
+ * chunks = first workgroup of chunk class c.  Needs cap >= 6 + 33.  Returns 0 or -22. */
+int oscar_prefill_plan_v1(int64_t history, int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                          int32_t* out, int32_t cap);
+
 /* ---- native decode step ------------------------------------------------------
  * One call per decode-shaped forward of the impl (backend.py:249-393 for batches whose
  * requests all have history: decode, MTP verification, cache-only decode, and cached

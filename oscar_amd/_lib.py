@@ -113,6 +113,8 @@ SIGNATURES = {
     "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_attn_decode_static_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),
+    "oscar_prefill_workspace_bytes_v2": (i64, [i64, i64, i64, i64, i64]),
+    "oscar_prefill_plan_v1": (C.c_int, [i64, i64, i64, i64, C.POINTER(i32), i32]),
     "oscar_attn_prefill_v1": (C.c_int, [C.POINTER(PrefillArgs), vp]),
     "oscar_context_create_v1": (C.c_int, [i32, C.POINTER(vp)]),
     "oscar_context_destroy_v1": (C.c_int, [vp]),

@@ -69,6 +69,23 @@ __device__ __forceinline__ unsigned pv_bits(float v) {
 template <int QT> struct QVec { typedef bf16x8 type; typedef bf16x2 pair; typedef __bf16 elem; };
 template <> struct QVec<OSCAR_F16> { typedef f16x8 type; typedef f16x2 pair; typedef _Float16 elem; };
 
+// ---- balanced split of the key ranges (a workspace of oscar_prefill_workspace_bytes_v2)
+// Query tile qt (kRows GQA rows) sees key tiles [0, kt(qt)), kt growing with qt under
+// the causal mask.  One workgroup per tile leaves the chip unbalanced: the continuation
+// of 15360 + 9256 tokens is 441 tiles of 481..771 key tiles on 256 CUs (1.7 rounds), a
+// fresh 2048-token prefill 96 tiles (a third of the CUs).  The key range of a tile is
+// instead cut into chunks of U key tiles (c U .. (c + 1) U), U about the work of half a
+// CU, and every chunk is a workgroup ("unit"); a tile with more than one chunk writes
+// normalised partials + log2 LSEs, and prefill_merge_kernel combines them (FP32 LSE
+// merge).  Units are numbered chunk-major, heaviest tile first within a chunk index,
+// so the large units are dispatched first: the tiles that have a chunk c are the
+// suffix qt >= qmin[c] (kt is non-decreasing in qt), and unit u of chunk class c
+// (base[c] <= u < base[c + 1]) is tile ntq - 1 - (u - base[c]).
+constexpr int kMaxChunks = 32;
+constexpr int64_t kMinChunkTiles = 16;  // 512 keys: shorter chunks cost more in merge than they balance
+constexpr int64_t kSplitCUs = 256;      // MI355X compute units
+constexpr int64_t kUnitsPerCU = 2;
+
 struct PrefillParams {
   oscar_prefill_args_v1 a;
   oscar_staging_v1 st;
@@ -77,7 +94,63 @@ struct PrefillParams {
   int qtok;            // query tokens per workgroup
   uint16_t* hist_k;    // [history][Hk][D] bf16 history values (workspace)
   uint16_t* hist_v;
+  // the split plan (split == 0: one unit per query tile, the whole key range)
+  int split;
+  int chunks;          // chunks of the heaviest tile
+  int U;               // key tiles per chunk
+  int ntq;             // query tiles
+  int qmin1;           // first tile with two chunks (the split tiles are qt >= qmin1)
+  int base[kMaxChunks + 1];
+  float* part_o;       // [slot][Hk][kRows][D] normalised partial O of the split tiles' chunks
+  float* part_lse;     // [slot][Hk][kRows] log2-domain LSE of each partial
 };
+
+// key tiles seen by the last query of a tile ending at chunk token q1
+__host__ __device__ inline int64_t tile_keys(int64_t hist, int64_t q1) { return (hist + q1 + kKeys - 1) / kKeys; }
+
+struct SplitPlan {
+  int chunks = 0, U = 0, ntq = 0, units = 0, qmin1 = 0;
+  int base[kMaxChunks + 1] = {};
+  int64_t slots = 0;   // partial slots per KV head
+};
+
+SplitPlan plan_split(int64_t hist, int64_t n, int64_t qtok, int64_t hk) {
+  SplitPlan sp;
+  if (n <= 0) return sp;
+  const int64_t ntq = (n + qtok - 1) / qtok;
+  auto kt = [&](int64_t qt) { return tile_keys(hist, (qt + 1) * qtok < n ? (qt + 1) * qtok : n); };
+  int64_t work = 0;
+  for (int64_t qt = 0; qt < ntq; ++qt) work += kt(qt);
+  const int64_t kmax = kt(ntq - 1);
+  int64_t U = (work * hk + kSplitCUs * kUnitsPerCU - 1) / (kSplitCUs * kUnitsPerCU);
+  if (U < kMinChunkTiles) U = kMinChunkTiles;
+  if ((kmax + U - 1) / U > kMaxChunks) U = (kmax + kMaxChunks - 1) / kMaxChunks;
+  const int64_t chunks = (kmax + U - 1) / U;
+  if (chunks < 2 || ntq > (1 << 24) || U > (1 << 24)) return sp;
+  sp.chunks = (int)chunks;
+  sp.U = (int)U;
+  sp.ntq = (int)ntq;
+  // qmin[c]: first tile with kt > c U (kt non-decreasing in qt)
+  int64_t qt = 0, units = 0;
+  for (int c = 0; c < sp.chunks; ++c) {
+    while (qt < ntq && kt(qt) <= c * U) ++qt;
+    if (c == 1) sp.qmin1 = (int)qt;
+    sp.base[c] = (int)units;
+    units += ntq - qt;
+  }
+  sp.base[sp.chunks] = (int)units;
+  sp.units = (int)units;
+  sp.slots = units - sp.qmin1;  // every unit but the single-chunk tiles' (class 0, qt < qmin1)
+  return sp;
+}
+
+constexpr int64_t kWsAlign = 256;
+int64_t hist_bytes(int64_t history, int64_t hk, int64_t D) {
+  return history > 0 ? (2 * history * hk * D * (int64_t)sizeof(uint16_t) + kWsAlign - 1) / kWsAlign * kWsAlign : 0;
+}
+int64_t split_bytes(const SplitPlan& sp, int64_t hk, int64_t D) {
+  return sp.chunks < 2 ? 0 : sp.slots * hk * kRows * (D + 1) * (int64_t)sizeof(float);
+}
 
 // one wave per (history token, kv head): lane l holds elements E*l .. E*l+E-1
 template <int D, int QT>
@@ -150,13 +223,28 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   const int m = lane & 31, g = lane >> 5;
   const int G = P.group;
   const int ntiles_q = (int)((A.num_tokens + P.qtok - 1) / P.qtok);
-  const int qt = ntiles_q - 1 - (int)blockIdx.x;  // heaviest (latest) query tiles first
   const int kvh = blockIdx.y;
+  const int64_t hist = A.history;
+  const int64_t hk = A.num_kv_heads;
+  // this workgroup's unit: query tile qt over key tiles [kb, ke); slot >= 0: the tile
+  // is split and this unit writes a partial
+  int qt, kb = 0, slot = -1;
+  if (P.split) {
+    const int u = blockIdx.x;
+    int c = 0;
+#pragma unroll
+    for (int cc = 1; cc < kMaxChunks; ++cc)
+      if (cc < P.chunks && u >= P.base[cc]) c = cc;
+    const int idx = u - P.base[c];
+    qt = ntiles_q - 1 - idx;  // heaviest (latest) query tiles first within a chunk class
+    kb = c * P.U;
+    if (qt >= P.qmin1) slot = c == 0 ? idx : u - P.qmin1;
+  } else {
+    qt = ntiles_q - 1 - (int)blockIdx.x;  // heaviest (latest) query tiles first
+  }
   const int64_t q0 = (int64_t)qt * P.qtok;
   const int64_t q1 = (q0 + P.qtok < A.num_tokens) ? q0 + P.qtok : A.num_tokens;
-  const int64_t hist = A.history;
   const int64_t nkeys = hist + q1;  // keys visible to the last query of the tile
-  const int64_t hk = A.num_kv_heads;
 
   // double-buffered key tiles.  K rows are padded by 16 bytes (row-per-lane 16-byte
   // reads of 8 consecutive keys cover all banks), V rows by 32 bytes (the transpose
@@ -211,8 +299,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
     }
   };
 
-  const int ktiles = (int)((nkeys + kKeys - 1) / kKeys);
-  fetch(0);
+  const int kt_all = (int)tile_keys(hist, q1);
+  const int ke = (P.split && kb + P.U < kt_all) ? kb + P.U : kt_all;  // kb < kt_all (plan)
+  fetch(kb);
 
   // this lane's row
   const int n = wave * 32 + m;
@@ -233,16 +322,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) O[b][r] = 0.f;
 
-  stash(0);
-  if (ktiles > 1) fetch(1);
+  stash(kb & 1);
+  if (kb + 1 < ke) fetch(kb + 1);
   __syncthreads();
   // The tile loop does no VALU work on O (kept in AGPRs by the MFMAs): a tile whose
   // row max drifts more than kLazy above the reference leaves the loop, O and l are
   // rescaled once, and the loop resumes at that tile (its QK is recomputed).
-  int kt = 0;
+  int kt = kb;
   float m_move = -INFINITY;  // per row: the max that forced the exit
   while (true) {
-    for (; kt < ktiles; ++kt) {
+    for (; kt < ke; ++kt) {
       const int buf = kt & 1;
       const int64_t k0 = (int64_t)kt * kKeys;
       // ---- S^T = K Q^T; the operands of kQK K-steps are read from LDS together so
@@ -332,13 +421,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
       }
       // the prefetched tile kt+1 goes to the other buffer (last read before the previous
       // barrier), then tile kt+2 is prefetched; one barrier per tile
-      if (kt + 1 < ktiles) {
+      if (kt + 1 < ke) {
         stash(buf ^ 1);
-        if (kt + 2 < ktiles) fetch(kt + 2);
+        if (kt + 2 < ke) fetch(kt + 2);
       }
       __syncthreads();
     }
-    if (kt >= ktiles) break;
+    if (kt >= ke) break;
     // rare: rescale to the new reference and redo tile kt (its buffers are intact)
     const bool move = m_move > m_run + kLazy;
     const float f = move ? exp2f(m_run - m_move) : 1.f;
@@ -358,6 +447,20 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   if (!row_ok) return;
   // O back from the PV scale of bf16 V values (a power of two: exact)
   const float inv = (l_tot > 0.f) ? (QT == OSCAR_F16 ? 1.f : (float)(1 << kVShift)) / l_tot : 0.f;
+  if (slot >= 0) {
+    // a chunk of a split tile: normalised O and its log2-domain LSE (-inf: no key of
+    // the chunk visible to the row) for prefill_merge_kernel
+    const int64_t prow = ((int64_t)slot * hk + kvh) * kRows + n;
+    float* po = P.part_o + prow * D;
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4)
+        *(f32x4*)(po + 32 * b + 8 * (r >> 2) + 4 * g) =
+            f32x4{O[b][r] * inv, O[b][r + 1] * inv, O[b][r + 2] * inv, O[b][r + 3] * inv};
+    if (g == 0) P.part_lse[prow] = (l_tot > 0.f) ? m_run + log2f(l_tot) : -INFINITY;
+    return;
+  }
   const int64_t obase = qi * A.out_stride_token + (int64_t)head * D;
 #pragma unroll
   for (int b = 0; b < D / 32; ++b)
@@ -372,6 +475,62 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
     A.lse[qi * A.num_q_heads + head] = (l_tot > 0.f) ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
+// FP32 LSE merge of a split tile's chunk partials (slab_attention.py:341-356 applied
+// over the chunks): thread (row, 4 d values), D / 4 threads per row.  Writes what the
+// unsplit kernel writes for the row: the output (query dtype when there is no history,
+// else fp32 rotated) and the LSE.
+template <int D, int QT>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams P) {
+  constexpr int TPR = D / 4, RPW = 256 / TPR, WPT = kRows / RPW;
+  const oscar_prefill_args_v1& A = P.a;
+  const int s = blockIdx.x / WPT;  // split tile, heaviest first (its class-0 slot)
+  const int n = (blockIdx.x % WPT) * RPW + threadIdx.x / TPR;
+  const int dq = threadIdx.x % TPR;
+  const int kvh = blockIdx.y;
+  const int64_t hk = A.num_kv_heads;
+  const int G = P.group;
+  const int qt = P.ntq - 1 - s;
+  const int64_t q0 = (int64_t)qt * P.qtok;
+  const int64_t q1 = (q0 + P.qtok < A.num_tokens) ? q0 + P.qtok : A.num_tokens;
+  const int64_t qi = q0 + n / G;
+  if (n >= P.qtok * G || qi >= q1) return;
+  const int nch = (int)((tile_keys(A.history, q1) + P.U - 1) / P.U);
+  auto prow = [&](int c) {
+    const int64_t slot = c == 0 ? s : P.base[c] + s - P.qmin1;
+    return (slot * hk + kvh) * kRows + n;
+  };
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c)
+    if (c < nch) M = fmaxf(M, P.part_lse[prow(c)]);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c < nch) {
+        const int64_t r = prow(c);
+        const float lc = P.part_lse[r];
+        if (lc != -INFINITY) {
+          const float w = exp2f(lc - M);
+          L += w;
+          acc += ((const f32x4*)(P.part_o + r * D))[dq] * w;
+        }
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const int head = kvh * G + n % G;
+  const int64_t obase = qi * A.out_stride_token + (int64_t)head * D + 4 * dq;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (A.history == 0) ((uint16_t*)A.out)[obase + e] = (uint16_t)q_bits<QT>(acc[e] * inv);
+    else ((float*)A.out)[obase + e] = acc[e] * inv;
+  }
+  if (A.lse != nullptr && dq == 0)
+    A.lse[qi * A.num_q_heads + head] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
 }  // namespace
 
 }  // namespace oscar
@@ -381,6 +540,27 @@ using namespace oscar;
 extern "C" int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim) {
   if (history <= 0) return 0;
   return 2 * history * num_kv_heads * head_dim * (int64_t)sizeof(uint16_t);
+}
+
+extern "C" int64_t oscar_prefill_workspace_bytes_v2(int64_t history, int64_t num_tokens, int64_t num_q_heads,
+                                                     int64_t num_kv_heads, int64_t head_dim) {
+  if (history < 0 || num_tokens < 0 || num_kv_heads < 1 || num_q_heads < num_kv_heads ||
+      num_q_heads % num_kv_heads || (head_dim != 128 && head_dim != 256) || num_q_heads / num_kv_heads > kRows)
+    return -22;
+  const SplitPlan sp = plan_split(history, num_tokens, kRows / (num_q_heads / num_kv_heads), num_kv_heads);
+  return hist_bytes(history, num_kv_heads, head_dim) + split_bytes(sp, num_kv_heads, head_dim);
+}
+
+extern "C" int oscar_prefill_plan_v1(int64_t history, int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                                     int32_t* out, int32_t cap) {
+  if (!out || cap < 6 + kMaxChunks + 1 || history < 0 || num_tokens < 0 || num_kv_heads < 1 ||
+      num_q_heads < num_kv_heads || num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > kRows)
+    return -22;
+  const SplitPlan sp = plan_split(history, num_tokens, kRows / (num_q_heads / num_kv_heads), num_kv_heads);
+  const int64_t head[6] = {sp.chunks, sp.U, sp.ntq, sp.qmin1, sp.units, sp.slots};
+  for (int i = 0; i < 6; ++i) out[i] = (int32_t)head[i];
+  for (int c = 0; c <= kMaxChunks; ++c) out[6 + c] = sp.base[c];
+  return 0;
 }
 
 extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* stream) {
@@ -421,6 +601,20 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
     p.hist_k = (uint16_t*)a.workspace;
     p.hist_v = p.hist_k + a.history * a.num_kv_heads * D;
   }
+  // the balanced split when the workspace holds its partials (after the history values)
+  const SplitPlan sp = plan_split(a.history, a.num_tokens, p.qtok, a.num_kv_heads);
+  const int64_t hbytes = hist_bytes(a.history, a.num_kv_heads, D), sbytes = split_bytes(sp, a.num_kv_heads, D);
+  p.ntq = (int)((a.num_tokens + p.qtok - 1) / p.qtok);
+  if (sbytes > 0 && a.workspace != nullptr && (((uintptr_t)a.workspace) & 15) == 0 &&
+      a.workspace_bytes >= hbytes + sbytes) {
+    p.split = 1;
+    p.chunks = sp.chunks;
+    p.U = sp.U;
+    p.qmin1 = sp.qmin1;
+    for (int c = 0; c <= kMaxChunks; ++c) p.base[c] = sp.base[c];
+    p.part_o = (float*)((char*)a.workspace + hbytes);
+    p.part_lse = p.part_o + sp.slots * a.num_kv_heads * kRows * D;
+  }
   hipStream_t s = (hipStream_t)stream;
   if (a.history > 0) {
     const unsigned hb = (unsigned)((a.history * a.num_kv_heads + 3) / 4);
@@ -433,8 +627,7 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
     }
     OSCAR_CHECK_LAUNCH("history_bf16_kernel");
   }
-  const int ntq = (int)((a.num_tokens + p.qtok - 1) / p.qtok);
-  dim3 grid(ntq, (unsigned)a.num_kv_heads);
+  dim3 grid((unsigned)(p.split ? sp.units : p.ntq), (unsigned)a.num_kv_heads);
   if (a.q_dtype == OSCAR_F16) {
     if (D == 256) hipLaunchKernelGGL((prefill_kernel<256, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
     else hipLaunchKernelGGL((prefill_kernel<128, OSCAR_F16>), grid, dim3(kThreads), 0, s, p);
@@ -443,5 +636,16 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
     else hipLaunchKernelGGL((prefill_kernel<128, OSCAR_BF16>), grid, dim3(kThreads), 0, s, p);
   }
   OSCAR_CHECK_LAUNCH("prefill_kernel");
+  if (p.split) {
+    const dim3 mgrid((unsigned)((p.ntq - p.qmin1) * (kRows / (256 / (D / 4)))), (unsigned)a.num_kv_heads);
+    if (a.q_dtype == OSCAR_F16) {
+      if (D == 256) hipLaunchKernelGGL((prefill_merge_kernel<256, OSCAR_F16>), mgrid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((prefill_merge_kernel<128, OSCAR_F16>), mgrid, dim3(256), 0, s, p);
+    } else {
+      if (D == 256) hipLaunchKernelGGL((prefill_merge_kernel<256, OSCAR_BF16>), mgrid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((prefill_merge_kernel<128, OSCAR_BF16>), mgrid, dim3(256), 0, s, p);
+    }
+    OSCAR_CHECK_LAUNCH("prefill_merge_kernel");
+  }
   return 0;
 }

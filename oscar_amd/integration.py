@@ -83,7 +83,8 @@ def transient_reserve(impls, max_tokens: int, max_model_len: int = 0) -> int:
     (layers run one after another, so the worker needs one layer's worth): the store
     workspace, the step's rotated q/k/v/output, LSE and the item partials of the
     planner's upper bound of items, and the continuation prefill's bf16 history of up
-    to ``max_model_len`` tokens (the reference's streaming_reserve role,
+    to ``max_model_len`` tokens with the partials of its split over ``max_tokens`` query
+    tokens (the reference's streaming_reserve role,
     integration.py:36-62; its slab workspace knob bounds no buffer here)."""
     active = [impl for impl in impls if getattr(impl._oscar, "attention_mode", "streaming") == "streaming"]
     if not active:
@@ -99,7 +100,8 @@ def transient_reserve(impls, max_tokens: int, max_model_len: int = 0) -> int:
         items = (max(max_model_len, max_tokens) // 8192 + 1) * hk + max_tokens * hk
         step = lib.oscar_step_workspace_bytes_v1(max_tokens, hq, hk, d, items)
         store = lib.oscar_store_workspace_bytes_v1(max_tokens, hk, d)
-        prefill = lib.oscar_prefill_workspace_bytes_v1(max_model_len, hk, d) if max_model_len > 0 else 0
+        # history values plus the split prefill's partials (largest at the most tokens)
+        prefill = max(0, lib.oscar_prefill_workspace_bytes_v2(max(max_model_len, 0), max_tokens, hq, hk, d))
         best = max(best, step + store + prefill)
     return best
 

@@ -448,13 +448,15 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
 
 # ------------------------------------------------------------------------ prefill
 def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_cache=None,
-                      block_table_row=None, stage=None, out=None, lse=None):
+                      block_table_row=None, stage=None, out=None, lse=None, split=True):
     """Causal GQA prefill of one request.
 
     q/k/v are bf16 or fp16 (history values rounded q_dtype(fp16(x))).
     history == 0: original-domain fresh-only prefill, returns [n, Hq, D] in q's dtype.
     history > 0: rotated continuation over the packed history, returns fp32 out_rot
     (and fills lse [n, Hq] when given).
+    split: cut the query tiles' key ranges into balanced chunks (a larger workspace for
+    their partials and one merge launch); False runs one workgroup per query tile.
     """
     _require_cuda(q, k, v)
     if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -487,9 +489,15 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
     if lse is not None:
         a.lse = lse.data_ptr()
     lib = _lib.load()
-    if history > 0:
-        ws = DeviceScratch.get(q.device).prefill_workspace(
-            lib.oscar_prefill_workspace_bytes_v1(history, hk, head_dim))
+    # the history values plus the partials of the balanced split (0 for calls too small
+    # to split and without history)
+    need = lib.oscar_prefill_workspace_bytes_v2(history, n, hq, hk, head_dim)
+    if need < 0:
+        raise ValueError("OSCAR HIP prefill: unsupported sizes")
+    if not split:
+        need = lib.oscar_prefill_workspace_bytes_v1(history, hk, head_dim)
+    if need > 0:
+        ws = DeviceScratch.get(q.device).prefill_workspace(need)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.oscar_attn_prefill_v1(C.byref(a), C.c_void_p(_stream(q.device))), "oscar_attn_prefill_v1")
     return out

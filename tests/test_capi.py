@@ -34,7 +34,7 @@ def header_functions() -> set:
 
 def test_library_exports_every_header_symbol(lib):
     names = header_functions()
-    assert len(names) == 14, names
+    assert len(names) == 16, names
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES)
@@ -360,3 +360,80 @@ def test_static_decode_rejects_plans_beyond_its_scratch(lib):
                     max_group_items=_lib.DECODE_STATIC_MAX_ITEMS + 1)
     assert lib.oscar_attn_decode_static_v1(C.byref(a), None) == -22
     assert b"static scratch" in lib.oscar_last_error()
+
+
+# ---- the prefill's balanced split (oscar_prefill_plan_v1)
+PREFILL_SPLIT_CASES = [
+    (15360, 9256, 6, 1),   # config 5 continuation
+    (0, 2048, 6, 1),       # config 5 fresh-only prefill
+    (3000, 300, 6, 1), (129, 1024, 6, 1), (8193, 257, 6, 1),
+    (0, 21, 6, 1),         # one query tile: nothing to split
+    (0, 32768, 6, 1),      # long fresh prefill: the chunk count cap
+    (500, 5000, 8, 2), (1, 70000, 1, 1), (40000, 5, 6, 1),
+]
+
+
+def prefill_plan(lib, history, n, hq, hk):
+    out = (C.c_int32 * 64)()
+    assert lib.oscar_prefill_plan_v1(history, n, hq, hk, out, 64) == 0
+    chunks, U, ntq, qmin1, units, slots = list(out)[:6]
+    return chunks, U, ntq, qmin1, units, slots, list(out)[6:6 + 33]
+
+
+@pytest.mark.parametrize("history,n,hq,hk", PREFILL_SPLIT_CASES)
+def test_prefill_split_covers_every_key_tile_once(lib, history, n, hq, hk):
+    """The prefill kernel's unit decode (attn_prefill.hip: chunk class by base[], tile
+    ntq - 1 - idx, key tiles [c U, min((c + 1) U, kt)), slot) over the plan: every query
+    tile's key tiles [0, kt) are covered exactly once, the split tiles' partial slots are
+    distinct and dense, the merge finds each chunk's slot by its own formula, and the
+    workspace size is the history values plus one partial per slot."""
+    group = hq // hk
+    qtok = 128 // group
+    chunks, U, ntq, qmin1, units, slots, base = prefill_plan(lib, history, n, hq, hk)
+    assert ntq == -(-n // qtok) or chunks == 0
+    kt = [-(-(history + min((qt + 1) * qtok, n)) // 32) for qt in range(-(-n // qtok))]
+    hist_b = -(-2 * history * hk * 256 * 2 // 256) * 256 if history > 0 else 0
+    ws = lib.oscar_prefill_workspace_bytes_v2(history, n, hq, hk, 256)
+    if chunks < 2:
+        assert chunks == 0 and ws == hist_b
+        assert max(kt) <= max(16, -(-sum(kt) * hk // 512))  # the heaviest tile fits one chunk
+        return
+    assert U >= 16 and chunks == -(-kt[-1] // U) <= 32
+    cover = {qt: [] for qt in range(ntq)}
+    seen_slots = set()
+    for u in range(units):
+        c = max(cc for cc in range(chunks) if u >= base[cc])
+        idx = u - base[c]
+        qt = ntq - 1 - idx
+        kb, ke = c * U, min(c * U + U, kt[qt])
+        assert 0 <= qt < ntq and kb < ke
+        slot = (idx if c == 0 else u - qmin1) if qt >= qmin1 else -1
+        cover[qt].append((kb, ke, c, slot))
+        if slot >= 0:
+            assert slot not in seen_slots and 0 <= slot < slots
+            seen_slots.add(slot)
+            s = ntq - 1 - qt
+            assert slot == (s if c == 0 else base[c] + s - qmin1)  # prefill_merge_kernel's slot
+    assert len(seen_slots) == slots
+    for qt, ranges in cover.items():
+        ranges.sort()
+        assert ranges[0][0] == 0 and ranges[-1][1] == kt[qt]
+        assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+        split = len(ranges) > 1
+        assert split == (qt >= qmin1) == (kt[qt] > U)
+        assert all((r[3] >= 0) == split for r in ranges)
+    # units are dealt chunk-major, heaviest tile first: unit sizes never grow within a class
+    sizes = [min(U, kt[ntq - 1 - (u - base[c])] - c * U)
+             for c in range(chunks) for u in range(base[c], base[c + 1])]
+    assert sum(sizes) == sum(kt)
+    assert ws == hist_b + slots * hk * 128 * 257 * 4
+    assert ws >= (lib.oscar_prefill_workspace_bytes_v1(history, hk, 256) if history > 0 else 0)
+
+
+def test_prefill_split_sizes_reject_bad_arguments(lib):
+    out = (C.c_int32 * 64)()
+    assert lib.oscar_prefill_plan_v1(0, 100, 6, 1, out, 10) == -22
+    assert lib.oscar_prefill_plan_v1(0, 100, 5, 2, out, 64) == -22
+    assert lib.oscar_prefill_workspace_bytes_v2(-1, 100, 6, 1, 256) == -22
+    assert lib.oscar_prefill_workspace_bytes_v2(0, 100, 6, 1, 64) == -22
+    assert lib.oscar_prefill_workspace_bytes_v2(0, 0, 6, 1, 256) == 0

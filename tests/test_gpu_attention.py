@@ -250,7 +250,7 @@ def test_decode_plan_covers_each_history_token_once(cuda):
 def test_prefill_fresh_only_matches_sdpa(cuda):
     from oscar_amd import ops
 
-    for n, hq, hk in ((300, 6, 1), (129, 8, 2)):
+    for n, hq, hk in ((300, 6, 1), (129, 8, 2), (1100, 6, 1)):  # 1100: key ranges split in 3 chunks
         q = cases.bf16_normal((n, hq, 256), 71)
         k = cases.bf16_normal((n, hk, 256), 72)
         v = cases.bf16_normal((n, hk, 256), 73)
@@ -280,6 +280,47 @@ def test_prefill_continuation_matches_oracle(cuda, prefix, n, ramp):
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"])
     check(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, f"continuation {prefix}+{n}")
+
+
+@pytest.mark.parametrize("prefix,n", [(8193, 257), (0, 1100), (1025, 700)])
+def test_prefill_split_matches_unsplit_and_oracle(cuda, prefix, n):
+    """The balanced split (chunks of the query tiles' key ranges, partials merged by
+    prefill_merge_kernel) against one workgroup per query tile and the oracle."""
+    import ctypes as C
+    from oscar_amd import _lib, ops
+
+    out = (C.c_int32 * 64)()
+    assert _lib.load().oscar_prefill_plan_v1(prefix, n, 6, 1, out, 64) == 0 and out[0] >= 2
+    c = cases.make_case([prefix], [n], fresh=True, seed=prefix + n)
+    kw = dict(head_dim=256)
+    if prefix:
+        kw.update(history=prefix, k_cache=torch.from_numpy(c["k8"]).view(torch.int8).cuda(),
+                  v_cache=torch.from_numpy(c["v8"]).view(torch.int8).cuda(),
+                  block_table_row=torch.from_numpy(c["bt"][0]).cuda(),
+                  stage=tuple(torch.from_numpy(a).cuda() for a in c["stage"]))
+    res = {}
+    for split in (True, False):
+        lse = torch.empty(n, 6, dtype=torch.float32, device="cuda")
+        o = ops.attention_prefill(dev(c["q"]), dev(c["k"]), dev(c["v"]), c["scale"], lse=lse, split=split, **kw)
+        torch.cuda.synchronize()
+        res[split] = (o.float().cpu().numpy(), lse.cpu().numpy())
+    if prefix:
+        ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
+                                         c["seqs"], c["scale"], c["stage"])
+        for split in (True, False):
+            check(*res[split], ref_out, ref_lse, f"continuation {prefix}+{n} split={split}")
+        tol = 1e-3
+    else:
+        ref = causal_prefill_ref(c["q"], c["k"], c["v"], c["scale"])
+        for split in (True, False):
+            err = np.abs(res[split][0] - ref).max()
+            print(f"fresh {n} split={split}: max|dO|={err:.3e}", flush=True)
+            assert err <= OUT_TOL
+        tol = 2.0 ** -7 * max(1.0, float(np.abs(ref).max()))  # one bf16 ulp of the output
+    d_out = np.abs(res[True][0] - res[False][0]).max()
+    d_lse = np.abs(res[True][1] - res[False][1]).max()
+    print(f"split vs unsplit {prefix}+{n}: max|dO| {d_out:.3e}, max|dLSE| {d_lse:.3e}", flush=True)
+    assert d_out <= tol and d_lse <= 1e-4
 
 
 def test_prefill_fp16_queries(cuda):
