@@ -497,7 +497,9 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
     if not split:
         need = lib.oscar_prefill_workspace_bytes_v1(history, hk, head_dim)
     if need > 0:
+        # the size asked for, not the shared buffer's (which an earlier call may have
+        # grown past v1's size: the call would then split)
         ws = DeviceScratch.get(q.device).prefill_workspace(need)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
     _lib.check(lib.oscar_attn_prefill_v1(C.byref(a), C.c_void_p(_stream(q.device))), "oscar_attn_prefill_v1")
     return out

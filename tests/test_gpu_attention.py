@@ -282,17 +282,22 @@ def test_prefill_continuation_matches_oracle(cuda, prefix, n, ramp):
     check(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, f"continuation {prefix}+{n}")
 
 
-@pytest.mark.parametrize("prefix,n", [(8193, 257), (0, 1100), (1025, 700)])
-def test_prefill_split_matches_unsplit_and_oracle(cuda, prefix, n):
+@pytest.mark.parametrize("prefix,n,d,hk,group,qdt", [
+    (8193, 257, 256, 1, 6, "bf16"), (0, 1100, 256, 1, 6, "bf16"), (1025, 700, 256, 1, 6, "bf16"),
+    (2000, 600, 128, 2, 4, "bf16"), (0, 900, 128, 2, 4, "f16"), (3000, 200, 256, 1, 6, "f16")])
+def test_prefill_split_matches_unsplit_and_oracle(cuda, prefix, n, d, hk, group, qdt):
     """The balanced split (chunks of the query tiles' key ranges, partials merged by
-    prefill_merge_kernel) against one workgroup per query tile and the oracle."""
+    prefill_merge_kernel) against one workgroup per query tile and the oracle, at both
+    head dims, GQA 4 over two KV heads and fp16 queries."""
     import ctypes as C
     from oscar_amd import _lib, ops
 
+    hq = hk * group
     out = (C.c_int32 * 64)()
-    assert _lib.load().oscar_prefill_plan_v1(prefix, n, 6, 1, out, 64) == 0 and out[0] >= 2
-    c = cases.make_case([prefix], [n], fresh=True, seed=prefix + n)
-    kw = dict(head_dim=256)
+    assert _lib.load().oscar_prefill_plan_v1(prefix, n, hq, hk, out, 64) == 0 and out[0] >= 2
+    c = cases.make_case([prefix], [n], fresh=True, seed=prefix + n, hk=hk, group=group, d=d)
+    tdt = torch.float16 if qdt == "f16" else torch.bfloat16
+    kw = dict(head_dim=d)
     if prefix:
         kw.update(history=prefix, k_cache=torch.from_numpy(c["k8"]).view(torch.int8).cuda(),
                   v_cache=torch.from_numpy(c["v8"]).view(torch.int8).cuda(),
@@ -300,23 +305,25 @@ def test_prefill_split_matches_unsplit_and_oracle(cuda, prefix, n):
                   stage=tuple(torch.from_numpy(a).cuda() for a in c["stage"]))
     res = {}
     for split in (True, False):
-        lse = torch.empty(n, 6, dtype=torch.float32, device="cuda")
-        o = ops.attention_prefill(dev(c["q"]), dev(c["k"]), dev(c["v"]), c["scale"], lse=lse, split=split, **kw)
+        lse = torch.empty(n, hq, dtype=torch.float32, device="cuda")
+        o = ops.attention_prefill(dev(c["q"], tdt), dev(c["k"], tdt), dev(c["v"], tdt), c["scale"], lse=lse,
+                                  split=split, **kw)
         torch.cuda.synchronize()
         res[split] = (o.float().cpu().numpy(), lse.cpu().numpy())
     if prefix:
         ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
-                                         c["seqs"], c["scale"], c["stage"])
+                                         c["seqs"], c["scale"], c["stage"], q_dtype=qdt)
         for split in (True, False):
-            check(*res[split], ref_out, ref_lse, f"continuation {prefix}+{n} split={split}")
+            check(*res[split], ref_out, ref_lse, f"continuation {prefix}+{n} d={d} {qdt} split={split}")
         tol = 1e-3
     else:
-        ref = causal_prefill_ref(c["q"], c["k"], c["v"], c["scale"])
+        ref = causal_prefill_ref(c["q"], c["k"], c["v"], c["scale"], q_dtype=qdt)
         for split in (True, False):
             err = np.abs(res[split][0] - ref).max()
-            print(f"fresh {n} split={split}: max|dO|={err:.3e}", flush=True)
+            print(f"fresh {n} d={d} {qdt} split={split}: max|dO|={err:.3e}", flush=True)
             assert err <= OUT_TOL
-        tol = 2.0 ** -7 * max(1.0, float(np.abs(ref).max()))  # one bf16 ulp of the output
+        unit = 2.0 ** -10 if qdt == "f16" else 2.0 ** -7  # one output ulp of the largest value
+        tol = unit * max(1.0, float(np.abs(ref).max()))
     d_out = np.abs(res[True][0] - res[False][0]).max()
     d_lse = np.abs(res[True][1] - res[False][1]).max()
     print(f"split vs unsplit {prefix}+{n}: max|dO| {d_out:.3e}, max|dLSE| {d_lse:.3e}", flush=True)
