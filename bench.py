@@ -160,24 +160,26 @@ class Setup:
 
         c = CONFIG
         kc, vc, stage = self.layers[layer]
+        store = None
         if self.has_new:
-            ops.store(self.k_new, self.v_new, kc, vc, self.slots, head_dim=c["d"], rk=self.rk,
-                      rv=self.rv, stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
-                      seqs_dev=self.seq_dev, num_reqs=len(self.seqs),
-                      recent_tokens=c["recent_tokens"], sink_tokens_eff=self.sink_eff, query=self.q,
-                      query_rot=self.q_rot, key_rot=self.k_rot, value_rot=self.v_rot)
+            # the write and the decode in one call (oscar_decode_write_v1)
+            store = ops.store_args(self.k_new, self.v_new, kc, vc, self.slots, head_dim=c["d"], rk=self.rk,
+                                   rv=self.rv, stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
+                                   seqs_dev=self.seq_dev, num_reqs=len(self.seqs),
+                                   recent_tokens=c["recent_tokens"], sink_tokens_eff=self.sink_eff, query=self.q,
+                                   query_rot=self.q_rot, key_rot=self.k_rot, value_rot=self.v_rot)
         else:
             ops.rotate(self.q, self.rk, out=self.q_rot)
-        self.attention(layer)
+        self.attention(layer, store=store)
         ops.rotate(self.out_rot, self.rv, transpose=True, out_dtype=torch.bfloat16, out=self.out)
 
-    def attention(self, layer, phases=0):
+    def attention(self, layer, phases=0, store=None):
         from oscar_amd import ops
 
         kc, vc, stage = self.layers[layer]
         ops.attention_decode(self.q_rot, self.k_rot, self.v_rot, kc, vc, self.bt, self.plan,
                              self.scale, stage, head_dim=CONFIG["d"], out_rot=self.out_rot,
-                             lse=self.lse, phases=phases)
+                             lse=self.lse, phases=phases, store=store)
 
     def staged_counts(self):
         """Per-request count of history tokens whose owner tag selects the FP32 window."""

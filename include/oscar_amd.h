@@ -224,6 +224,19 @@ typedef struct oscar_attn_args_v1 {
 
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
 
+/* A step's store and split-K decode in one call: oscar_store_v1(store) then
+ * oscar_attn_decode_v1(attn) on `stream`, except that for a store of <= 64 tokens (and
+ * attn->phases == 0, a non-empty plan) the store's quantization, slot bytes, FP32 window
+ * copies and owner tags are written by extra workgroups of the decode's merge launch
+ * instead of the store's own launch, so the decode starts once the store's rotation has
+ * run.  From the rotation to the merge the seats the call writes carry a pending owner tag
+ * (-2, which matches no block): the decode sees the window as the store leaves it.  attn
+ * reads the store's rotated outputs (q = store->query_rot, k_new / v_new = key_rot /
+ * value_rot).  No counterpart in the reference, whose write (backend.py:249-333)
+ * completes before its read (:334-393); bytes, tags, window values and outputs are the
+ * same. */
+int oscar_decode_write_v1(const oscar_store_args_v1* store, const oscar_attn_args_v1* attn, void* stream);
+
 /* oscar_attn_decode_v1 that allocates nothing and takes no workspace: the item
  * partials live in a library-owned static device array of
  * OSCAR_DECODE_STATIC_MAX_ITEMS * 32 * 257 * 4 bytes (16.8 MB, held on every device

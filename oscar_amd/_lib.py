@@ -111,6 +111,7 @@ SIGNATURES = {
                                      i32, i32, i32, i32, C.POINTER(i32), i32, C.POINTER(i32), i32,
                                      C.POINTER(Plan)]),
     "oscar_attn_decode_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "oscar_decode_write_v1": (C.c_int, [C.POINTER(StoreArgs), C.POINTER(AttnArgs), vp]),
     "oscar_attn_decode_static_v1": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "oscar_prefill_workspace_bytes_v1": (i64, [i64, i64, i64]),
     "oscar_prefill_workspace_bytes_v2": (i64, [i64, i64, i64, i64, i64]),

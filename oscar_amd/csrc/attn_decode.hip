@@ -53,6 +53,7 @@
 #include <vector>
 
 #include "common.h"
+#include "store_quant.h"
 
 namespace oscar {
 
@@ -911,9 +912,30 @@ constexpr int kMergeWaves = 8;
 constexpr int kBatch = 16;  // items per load round of a wave
 
 template <int D>
-__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams P) {
+__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams P, StoreParams S) {
   using C = Cfg<D>;
   const oscar_attn_args_v1& A = P.a;
+  // Workgroups past the groups (launched only for a deferred store, S.deferred) finish
+  // that store: one wave per K / V vector quantizes the rotated vector the store's
+  // rotation launch left in S.y and writes its slot bytes, FP32 window copy and owner
+  // tag, as store_small_kernel's last slice workgroup does in the one-launch form.  It
+  // runs beside the merge: nothing here reads the cache or the window.
+  __shared__ float s_qrow[kMergeWaves][D];
+  __shared__ float s_qclip[kMergeWaves];
+  if ((int)blockIdx.x >= A.num_groups) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t hk = S.a.cache.num_kv_heads, nkv = S.a.num_tokens * hk;
+    const int64_t v = ((int64_t)(blockIdx.x - A.num_groups) * gridDim.y + blockIdx.y) * (blockDim.x >> 6) + wave;
+    if (!S.deferred || v >= 2 * nkv) return;
+    const int kind = v < nkv ? KIND_K : KIND_V;
+    const int64_t vw = kind == KIND_K ? v : v - nkv;
+    const int64_t t = vw / hk, h = vw % hk;
+    const DestLoads dl = dest_loads(S, t);
+    const f32x4 x4 = *(const f32x4*)(S.y + ((int64_t)kind * nkv + vw) * D + 4 * (lane < D / 4 ? lane : 0));
+    const Dest dest = dest_finish(S, kind, t, dl);
+    quant_vector<D>(S, kind, t, h, dest, x4, s_qrow[wave], &s_qclip[wave]);
+    return;
+  }
   // the group record carries everything the merge needs (no dependent loads)
   const int32_t* grp = A.groups + (int64_t)blockIdx.x * OSCAR_GROUP_INTS;
   const int kvh = grp[1], i0 = grp[2], ni = grp[3], a = grp[4], nq = grp[5];
@@ -1016,7 +1038,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
 }
 
 template <int D>
-int launch_decode(const AttnParams& p, hipStream_t s) {
+int launch_decode(const AttnParams& p, hipStream_t s, const StoreParams& sp) {
   if (p.a.phases != 2) {
     if (p.a.q_dtype == OSCAR_F16)
       hipLaunchKernelGGL((attn_main_kernel<D, OSCAR_F16>), dim3(p.a.num_items), dim3(kThreads), 0, s, p);
@@ -1031,7 +1053,12 @@ int launch_decode(const AttnParams& p, hipStream_t s) {
     const int per_group = p.a.max_group_items > 0 ? p.a.max_group_items : p.a.num_items;
     int waves = 1;
     while (waves < kMergeWaves && waves * kBatch < per_group) waves *= 2;
-    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(p.a.num_groups, Cfg<D>::NV / 64), dim3(waves * 64), 0, s, p);
+    // a deferred store's vectors: one per wave of the extra workgroups
+    constexpr int64_t gy = Cfg<D>::NV / 64;
+    const int64_t nvec = sp.deferred ? 2 * sp.a.num_tokens * sp.a.cache.num_kv_heads : 0;
+    const int64_t extra = (nvec + gy * waves - 1) / (gy * waves);
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3((unsigned)(p.a.num_groups + extra), (unsigned)gy), dim3(waves * 64), 0,
+                       s, p, sp);
     OSCAR_CHECK_LAUNCH("attn_merge_kernel");
   }
   return 0;
@@ -1292,11 +1319,16 @@ namespace {
 
 // Argument checks shared by both decode entry points; `name` prefixes the messages.
 // `partials` / `partial_bytes`: where the item partials go and how much room there is.
+// `store` (oscar_decode_write_v1): the store enqueued once the decode's arguments have
+// passed, deferred (its quantization in the merge launch) when it is a small call.
 int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials, int64_t partial_bytes,
-                   hipStream_t s) {
+                   hipStream_t s, const oscar_store_args_v1* store = nullptr) {
   const int64_t D = a.cache.head_dim;
   if (D != 128 && D != 256) return fail(-22, "%s: head_dim %lld unsupported", name, (long long)D);
-  if (a.num_items <= 0 || a.num_groups <= 0) return 0;
+  if (a.num_items <= 0 || a.num_groups <= 0) {
+    StoreParams sp{};
+    return store != nullptr ? store_launch(store, s, false, name, &sp) : 0;
+  }
   if (!a.q || !a.items || !a.groups || !partials || !a.out_rot || !a.lse || !a.block_table ||
       !a.query_start_loc || !a.seq_lens)
     return fail(-22, "%s: missing pointer", name);
@@ -1334,7 +1366,15 @@ int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials
   p.group = (int)(a.num_q_heads / a.cache.num_kv_heads);
   p.part_o = (float*)partials;
   p.part_lse = p.part_o + (int64_t)a.num_items * 32 * D;
-  return D == 256 ? launch_decode<256>(p, s) : launch_decode<128>(p, s);
+  StoreParams sp{};
+  if (store != nullptr) {
+    if (store->cache.head_dim != D)
+      return fail(-22, "%s: the store's head_dim %lld differs from the decode's", name,
+                  (long long)store->cache.head_dim);
+    const int rc = store_launch(store, s, a.phases == 0, name, &sp);
+    if (rc != 0) return rc;
+  }
+  return D == 256 ? launch_decode<256>(p, s, sp) : launch_decode<128>(p, s, sp);
 }
 
 // ---- the entry point that allocates nothing: item partials in a file-scope device
@@ -1376,6 +1416,13 @@ extern "C" int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream
   if (!args) return fail(-22, "oscar_attn_decode_v1: null args");
   return launch_checked(*args, "oscar_attn_decode_v1", args->workspace, args->workspace_bytes,
                         (hipStream_t)stream);
+}
+
+extern "C" int oscar_decode_write_v1(const oscar_store_args_v1* store, const oscar_attn_args_v1* attn,
+                                     void* stream) {
+  if (!store || !attn) return fail(-22, "oscar_decode_write_v1: null args");
+  return launch_checked(*attn, "oscar_decode_write_v1", attn->workspace, attn->workspace_bytes, (hipStream_t)stream,
+                        store);
 }
 
 extern "C" int oscar_attn_decode_static_v1(const oscar_attn_args_v1* args, void* stream) {

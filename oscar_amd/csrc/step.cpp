@@ -7,7 +7,8 @@
 // batch from the host metadata, build the split-K plan (oscar_attn_plan_v1) straight
 // into a pinned ring slot next to the request table, one host-to-device copy of the
 // slot, then the store (or the query rotation), the split-K decode + merge and the
-// inverse rotation, all through the public entry points, on the caller's stream.
+// inverse rotation, all through the public entry points, on the caller's stream (the
+// store and decode as oscar_decode_write_v1).
 #include <mutex>
 #include <vector>
 
@@ -191,9 +192,10 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
   void* v_rot = ws + L.v_rot;
   float* out_rot = (float*)(ws + L.out_rot);
   float* lse = (float*)(ws + L.lse);
-  // ---- write (or the query rotation alone)
+  // ---- write (enqueued with the decode below) or the query rotation alone
+  rc = 0;
+  oscar_store_args_v1 st{};
   if (has_new) {
-    oscar_store_args_v1 st{};
     st.key = a.key;
     st.value = a.value;
     st.kv_dtype = a.q_dtype;
@@ -224,7 +226,6 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
     st.workspace = a.store_workspace;
     st.workspace_bytes = a.store_workspace_bytes;
     st.arrivals = a.arrivals;
-    rc = oscar_store_v1(&st, stream);
   } else {
     oscar_rotate_args_v1 ro{};
     ro.x = a.query;
@@ -268,7 +269,9 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
     at.out_rot = out_rot;
     at.lse = lse;
     at.q_dtype = a.q_dtype;
-    rc = oscar_attn_decode_v1(&at, stream);
+    // with new tokens: the store and the decode in one call (a small store's
+    // quantization and slot / window writes ride in the decode's merge launch)
+    rc = has_new ? oscar_decode_write_v1(&st, &at, stream) : oscar_attn_decode_v1(&at, stream);
   }
   if (rc == 0) {
     oscar_rotate_args_v1 ro{};

@@ -25,249 +25,11 @@
 #include <atomic>
 
 #include "common.h"
+#include "store_quant.h"
 
 namespace oscar {
 
 namespace {
-
-enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
-
-typedef float __attribute__((ext_vector_type(2))) f32x2;
-
-// workgroups of the fused launch per kind at most (bounds the per-workgroup exact counts)
-constexpr int kMaxFusedGroups = 1024;
-
-struct StoreParams {
-  oscar_store_args_v1 a;
-  float* y;          // small calls: workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
-  int64_t capacity;  // num_blocks * block_size
-  int32_t* exact;    // large calls: [0] K total, [1] V total (written by the exact pass),
-                     // [2 + kind * kMaxFusedGroups + w] vectors workgroup w of the fused launch
-                     // left to the exact pass, then the lists [kind][nvec] (nvec = num_tokens *
-                     // num_kv_heads): workgroup w's entries start at its first vector
-  int32_t* flags;    // large calls: [num_tokens] bit 0 = position inside the window
-  u32x4* planes;     // large calls: R_k, R_v as fp16 MFMA B fragments [2][D/32][D/16][2][64]
-  int32_t* bexp;     // large calls: [2][D] power-of-two column scale of the planes
-  float* colnorm;    // large calls: [2][D] ||R_:d||
-  int32_t fused_kv_groups;  // large calls: fused workgroups per kind for K and for V
-};
-
-__device__ __forceinline__ int32_t* exact_counts(const StoreParams& p, int kind) {
-  return p.exact + 2 + kind * kMaxFusedGroups;
-}
-__device__ __forceinline__ int32_t* exact_list(const StoreParams& p, int kind, int64_t nvec) {
-  return p.exact + 2 + 2 * kMaxFusedGroups + kind * nvec;
-}
-
-__device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
-  // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
-  return (long long)((epoch << 24) | (token & 0xffffffll));
-}
-constexpr int64_t kMaxEpoch = (1ll << 39) - 1;
-
-__device__ __forceinline__ int64_t seat_of(int64_t slot, int64_t bs, int64_t rows) {
-  return ((slot / bs) % rows) * bs + slot % bs;
-}
-
-// 4 floats to dtype DT at element i (8 or 16 bytes, aligned)
-template <int DT>
-__device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
-  if constexpr (DT == OSCAR_F32) {
-    *(f32x4*)((float*)base + i) = f32x4{y[0], y[1], y[2], y[3]};
-  } else {
-    unsigned w[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const unsigned lo = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j]) : f32_to_f16_bits(y[2 * j]);
-      const unsigned hi = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j + 1]) : f32_to_f16_bits(y[2 * j + 1]);
-      w[j] = lo | (hi << 16);
-    }
-    *(u32x2*)((uint16_t*)base + i) = u32x2{w[0], w[1]};
-  }
-}
-
-// Sort-based clip threshold (backend.py:140-145): the idx-th smallest |x| of a
-// D-vector stored in LDS; ties are ordered by index so exactly one lane matches.
-template <int D>
-__device__ float clip_threshold(const float* row, int idx, volatile float* slot) {
-  const int lane = threadIdx.x & 63;
-  for (int i = lane; i < D; i += 64) {
-    float xi = fabsf(row[i]);
-    int rank = 0;
-    for (int j = 0; j < D; ++j) {
-      float xj = fabsf(row[j]);
-      rank += (xj < xi) || (xj == xi && j < i);
-    }
-    if (rank == idx) *slot = xi;
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  return *slot;
-}
-
-// Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
-// the last writer of each, and whether its position lies inside its request's sink /
-// recent window (backend.py:536-541: keep the FP32 copy, else drop the seat).
-struct Dest {
-  int64_t slot, seat;
-  int64_t koff, voff;  // fused kernel: byte offsets of the K and V slots in the caches
-  bool valid, slot_win, seat_win, keep;
-};
-
-// the window rule for token t of a request of length seq whose queries end at end
-__device__ __forceinline__ bool in_window(const oscar_store_args_v1& a, int64_t t, int64_t seq, int64_t end) {
-  const int64_t pos = seq - end + t;
-  return (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
-}
-
-// Destination of a small call's vector: winners of duplicate slots / seats by
-// scanning slot_mapping.  Computed by one wave, wave-uniform, in two steps so that
-// the loads go out early and their results are used late: dest_loads issues every
-// load (the token's slot, lane l's request-table entry and lane l's slot of the
-// call), dest_finish decides.  A call has at most kFusedTokens (64) tokens, so one
-// slot per lane covers it; requests past the first 64 are read in dest_finish.
-struct DestLoads {
-  int64_t slot;     // slot_mapping[t]
-  int64_t s2;       // slot_mapping[lane] (-1 past the call)
-  int64_t st, nx, sq;  // query_start_loc[lane], [lane + 1], seq_lens[lane]
-};
-
-__device__ __forceinline__ DestLoads dest_loads(const StoreParams& p, int64_t t) {
-  const oscar_store_args_v1& a = p.a;
-  const int lane = threadIdx.x & 63;
-  DestLoads l;
-  l.slot = a.slot_mapping[t];
-  l.s2 = lane < a.num_tokens ? a.slot_mapping[lane] : -1;
-  const bool in = lane < a.num_reqs && a.stage_mode == OSCAR_STAGE_WRITE;
-  l.st = in ? a.query_start_loc[lane] : a.num_tokens;
-  l.nx = in ? a.query_start_loc[lane + 1] : a.num_tokens;
-  l.sq = in ? a.seq_lens[lane] : 0;
-  return l;
-}
-
-__device__ Dest dest_finish(const StoreParams& p, int kind, int64_t t, const DestLoads& l) {
-  const oscar_store_args_v1& a = p.a;
-  const int lane = threadIdx.x & 63;
-  const int64_t bs = a.cache.block_size;
-  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
-  Dest d{};
-  const int64_t slot = l.slot;
-  // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
-  // length and query end come from the same loads (qsl is non-decreasing)
-  int64_t seq = 0, end = 0;
-  if (window) {
-    for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
-      const int r = c0 + lane;
-      const bool in = r < a.num_reqs;
-      int64_t st = l.st, nx = l.nx, sq = l.sq;
-      if (c0 > 0) {
-        st = in ? a.query_start_loc[r] : a.num_tokens;
-        nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
-        sq = in ? a.seq_lens[r] : 0;
-      }
-      const int64_t start = st < a.num_tokens ? st : a.num_tokens;
-      const uint64_t bal = __ballot(in && start <= t);
-      if (bal) {
-        const int last = 63 - __builtin_clzll(bal);
-        seq = __shfl(sq, last);
-        end = __shfl(nx, last);
-      }
-    }
-  }
-  d.slot = slot;
-  d.keep = window && in_window(a, t, seq, end);
-  d.valid = slot >= 0 && slot < p.capacity;
-  if (!d.valid) return d;
-  const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
-  d.seat = seat;
-  // last writer: no later valid token of the call has the same slot / seat
-  {
-    const int64_t t2 = lane, s2 = l.s2;
-    const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
-    const bool later_slot = later && s2 == slot;
-    const bool later_seat = window && later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
-    d.slot_win = !__any(later_slot);
-    d.seat_win = window && !__any(later_seat);
-    // standalone KV update: every written seat loses its window copy
-    if (a.stage_mode == OSCAR_STAGE_INVALIDATE && kind == KIND_K && lane == 0) a.staging.owner[seat] = -1;
-  }
-  return d;
-}
-
-// Quantize, pack and scatter one rotated vector (kind K or V of token t, kv head h,
-// destination d) held by one wave (lane b < D / 4: elements 4b..4b+3 in x4), with
-// the staging window and owner tag of its seat.
-template <int D>
-__device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t h, const Dest& d, f32x4 x4,
-                             float* row, float* clip_slot) {
-  constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
-  const oscar_store_args_v1& a = p.a;
-  const int64_t hk = a.cache.num_kv_heads;
-  const int lane = threadIdx.x & 63;
-  const bool active = lane < NL;
-  const int64_t bs = a.cache.block_size;
-  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
-  if (!d.valid) return;
-  const int64_t slot = d.slot, seat = d.seat;
-  const bool slot_win = d.slot_win, seat_win = d.seat_win;
-  const int64_t blk = slot / bs, off = slot % bs;
-  if (active) *(f32x4*)&row[4 * lane] = x4;
-
-  if (window && seat_win) {
-    const bool keep = d.keep;
-    if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
-    if (keep && active) {
-      float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) + (seat * hk + h) * D;
-      *(f32x4*)&dst[4 * lane] = x4;
-    }
-  }
-  if (!slot_win) return;
-
-  const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
-  float thr = INFINITY;
-  if (clip > 0.f) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    int idx = (int)(clip * (float)D);
-    if (idx > D - 1) idx = D - 1;
-    thr = clip_threshold<D>(row, idx, clip_slot);
-  }
-  // lane b handles byte b = elements 4b..4b+3
-  float x[4];
-  float vmin = INFINITY, vmax = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = active ? x4[j] : 0.f;
-    if (clip > 0.f) v = fminf(fmaxf(v, -thr), thr);
-    x[j] = v;
-    if (active) { vmin = fminf(vmin, v); vmax = fmaxf(vmax, v); }
-  }
-  vmin = wave_min(vmin);
-  vmax = wave_max(vmax);
-  float scale = __fdiv_rn(vmax - vmin, 3.0f);
-  if (!(scale > 0x1p-14f)) scale = 0x1p-14f;
-  const unsigned short scale_bits = f32_to_f16_bits(scale);
-  const unsigned short zero_bits = f32_to_f16_bits(vmin);
-  const float s16 = f16_bits_to_f32(scale_bits), z16 = f16_bits_to_f32(zero_bits);
-  uint8_t* kslot = a.cache.k + blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
-  uint8_t* vslot = a.cache.v + blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
-  if (active) {
-    unsigned byte = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float q = floorf(__fdiv_rn(x[j] - z16, s16) + 0.5f);
-      q = fminf(fmaxf(q, 0.f), 3.f);
-      byte |= (unsigned)((int)q & 3) << (2 * j);
-    }
-    uint8_t* dst = (kind == KIND_K) ? (kslot + 32) : vslot;
-    dst[lane] = (uint8_t)byte;
-  }
-  if (lane == 0) {
-    unsigned meta = (unsigned)scale_bits | ((unsigned)zero_bits << 16);
-    *(unsigned*)(kslot + (kind == KIND_K ? 0 : 4)) = meta;
-  }
-}
-
 
 // Calls of at most kFusedTokens tokens (decode and MTP steps): one launch of
 // workgroups (slice, vector group).  The vectors of a kind -- K and V rows (token, kv
@@ -351,7 +113,7 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
   // wave): out with the operands, used after the products
   const int64_t vw = v0 + wave, t = vw / hk, h = vw % hk;
   DestLoads dl{};
-  if (kv && wave < nv) dl = dest_loads(p, t);
+  if (kv && !p.deferred && wave < nv) dl = dest_loads(p, t);
   __syncthreads();
   double acc[kSmallVecs][2];
   if (R != nullptr) {
@@ -394,6 +156,16 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
     }
   }
   if (!kv) return;
+  if (p.deferred) {
+    // the seats of the call's valid tokens get the pending tag; the quantization
+    // writes their final tags (every such seat has a last writer among the tokens)
+    if (kind == KIND_K && blockIdx.x == 0 && tid < nv && a.stage_mode != OSCAR_STAGE_NONE) {
+      const int64_t slot = a.slot_mapping[(v0 + tid) / hk];
+      if (slot >= 0 && slot < p.capacity)
+        a.staging.owner[seat_of(slot, a.cache.block_size, a.staging.rows)] = kPendingTag;
+    }
+    return;
+  }
   Dest dest{};
   if (wave < nv) dest = dest_finish(p, kind, t, dl);
   // the slice is written (stores complete before the barrier): count it in; the last
@@ -1373,30 +1145,31 @@ static int current_cu_count() {
   return cu;
 }
 
-extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
-  if (args == nullptr) return fail(-22, "oscar_store_v1: null args");
+int oscar::store_launch(const oscar_store_args_v1* args, void* stream, bool defer, const char* fn, StoreParams* out) {
+  *out = StoreParams{};
+  if (args == nullptr) return fail(-22, "%s: null args", fn);
   const oscar_store_args_v1& a = *args;
-  if (a.num_tokens < 0) return fail(-22, "oscar_store_v1: negative num_tokens");
+  if (a.num_tokens < 0) return fail(-22, "%s: negative num_tokens", fn);
   if (a.num_tokens == 0) return 0;
   const int64_t D = a.cache.head_dim;
   if (D != 64 && D != 128 && D != 256)
-    return fail(-22, "oscar_store_v1: head_dim %lld unsupported (64/128/256)", (long long)D);
+    return fail(-22, "%s: head_dim %lld unsupported (64/128/256)", fn, (long long)D);
   if (a.key == nullptr || a.value == nullptr || a.slot_mapping == nullptr)
-    return fail(-22, "oscar_store_v1: key/value/slot_mapping required");
+    return fail(-22, "%s: key/value/slot_mapping required", fn);
   if (a.kv_dtype != OSCAR_BF16 && a.kv_dtype != OSCAR_F16 && a.kv_dtype != OSCAR_F32)
-    return fail(-22, "oscar_store_v1: bad kv_dtype %d", a.kv_dtype);
+    return fail(-22, "%s: bad kv_dtype %d", fn, a.kv_dtype);
   if (a.cache.k == nullptr || a.cache.v == nullptr || a.cache.block_size <= 0 ||
       a.cache.num_blocks <= 0 || a.cache.num_kv_heads <= 0)
-    return fail(-22, "oscar_store_v1: invalid cache geometry");
+    return fail(-22, "%s: invalid cache geometry", fn);
   if (a.cache.k_stride[2] < 32 + D / 4 || a.cache.v_stride[2] < D / 4)
-    return fail(-22, "oscar_store_v1: slot stride too small for the packed layout");
+    return fail(-22, "%s: slot stride too small for the packed layout", fn);
   for (int i = 0; i < 3; ++i)
     if ((a.cache.k_stride[i] & 3) || (a.cache.v_stride[i] & 3))
-      return fail(-22, "oscar_store_v1: cache strides must be multiples of 4 bytes");
+      return fail(-22, "%s: cache strides must be multiples of 4 bytes", fn);
   if ((((uintptr_t)a.cache.k) & 3) || (((uintptr_t)a.cache.v) & 3))
-    return fail(-22, "oscar_store_v1: cache base must be 4-byte aligned");
+    return fail(-22, "%s: cache base must be 4-byte aligned", fn);
   if (a.key_stride_token < a.cache.num_kv_heads * D || a.value_stride_token < a.cache.num_kv_heads * D)
-    return fail(-22, "oscar_store_v1: key/value row stride smaller than heads*D");
+    return fail(-22, "%s: key/value row stride smaller than heads*D", fn);
   // inputs are read 8 elements (16 or 32 bytes) at a time, outputs written 4 at a time
   const int esz = a.kv_dtype == OSCAR_F32 ? 4 : 2;
   auto misaligned = [&](const void* ptr, int64_t stride) {
@@ -1404,37 +1177,37 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
   };
   if (misaligned(a.key, a.key_stride_token) || misaligned(a.value, a.value_stride_token) ||
       (a.query_rot != nullptr && misaligned(a.query, a.query_stride_token)))
-    return fail(-22, "oscar_store_v1: key/value/query rows must be 16-byte aligned");
+    return fail(-22, "%s: key/value/query rows must be 16-byte aligned", fn);
   if ((a.key_rot && (((uintptr_t)a.key_rot) & 15)) || (a.value_rot && (((uintptr_t)a.value_rot) & 15)) ||
       (a.query_rot && (((uintptr_t)a.query_rot) & 15)))
-    return fail(-22, "oscar_store_v1: rotated outputs must be 16-byte aligned");
+    return fail(-22, "%s: rotated outputs must be 16-byte aligned", fn);
   if ((a.rk && (((uintptr_t)a.rk) & 15)) || (a.rv && (((uintptr_t)a.rv) & 15)))
-    return fail(-22, "oscar_store_v1: rotations must be 16-byte aligned");
+    return fail(-22, "%s: rotations must be 16-byte aligned", fn);
   if (a.slot_claims == nullptr || a.epoch_counter == nullptr)
-    return fail(-22, "oscar_store_v1: slot_claims scratch and the device epoch counter are required");
-  if (a.num_tokens >= (1ll << 24)) return fail(-22, "oscar_store_v1: more than 2^24 tokens per call");
+    return fail(-22, "%s: slot_claims scratch and the device epoch counter are required", fn);
+  if (a.num_tokens >= (1ll << 24)) return fail(-22, "%s: more than 2^24 tokens per call", fn);
   if (a.stage_mode != OSCAR_STAGE_NONE) {
     if (a.staging.owner == nullptr || a.staging.rows <= 0)
-      return fail(-22, "oscar_store_v1: staging arena required for stage_mode %d", a.stage_mode);
+      return fail(-22, "%s: staging arena required for stage_mode %d", fn, a.stage_mode);
     if (a.stage_mode == OSCAR_STAGE_WRITE &&
         (a.seat_claims == nullptr || a.staging.stage_k == nullptr || a.staging.stage_v == nullptr ||
          a.query_start_loc == nullptr || a.seq_lens == nullptr || a.num_reqs <= 0))
-      return fail(-22, "oscar_store_v1: window write needs seat_claims, arena and request metadata");
+      return fail(-22, "%s: window write needs seat_claims, arena and request metadata", fn);
     if (a.stage_mode == OSCAR_STAGE_WRITE &&
         ((((uintptr_t)a.staging.stage_k) & 15) || (((uintptr_t)a.staging.stage_v) & 15)))
-      return fail(-22, "oscar_store_v1: staging arena must be 16-byte aligned");
+      return fail(-22, "%s: staging arena must be 16-byte aligned", fn);
   }
   if (a.query_rot != nullptr &&
       (a.query == nullptr || a.num_q_heads <= 0 || a.query_stride_token < a.num_q_heads * D))
-    return fail(-22, "oscar_store_v1: query_rot requires query, num_q_heads and a valid stride");
+    return fail(-22, "%s: query_rot requires query, num_q_heads and a valid stride", fn);
   const int64_t need = oscar_store_workspace_bytes_v1(a.num_tokens, a.cache.num_kv_heads, D);
   if (a.workspace == nullptr || a.workspace_bytes < need || (((uintptr_t)a.workspace) & 15))
-    return fail(-22, "oscar_store_v1: 16-byte aligned workspace of %lld bytes required", (long long)need);
+    return fail(-22, "%s: 16-byte aligned workspace of %lld bytes required", fn, (long long)need);
   if (a.num_tokens <= kFusedTokens && (a.arrivals == nullptr || (((uintptr_t)a.arrivals) & 3)))
-    return fail(-22, "oscar_store_v1: calls of <= %lld tokens need the arrivals counters", (long long)kFusedTokens);
+    return fail(-22, "%s: calls of <= %lld tokens need the arrivals counters", fn, (long long)kFusedTokens);
   if (2 * a.num_tokens * a.cache.num_kv_heads >= (1ll << 31) ||
       (a.query_rot != nullptr && a.num_tokens * a.num_q_heads >= (1ll << 31)))
-    return fail(-22, "oscar_store_v1: num_tokens x heads too large for one call");
+    return fail(-22, "%s: num_tokens x heads too large for one call", fn);
   StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size};
   uint8_t* ws = (uint8_t*)a.workspace;
   p.exact = (int32_t*)ws;
@@ -1444,7 +1217,14 @@ extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
   p.colnorm = (float*)(p.bexp + 2 * D);
   const int cu = a.num_tokens <= kFusedTokens ? 0 : current_cu_count();
   hipStream_t s = (hipStream_t)stream;
+  p.deferred = defer && a.num_tokens <= kFusedTokens;
+  *out = p;
   if (D == 256) return launch_store<256>(p, cu, s);
   if (D == 128) return launch_store<128>(p, cu, s);
   return launch_store<64>(p, cu, s);
+}
+
+extern "C" int oscar_store_v1(const oscar_store_args_v1* args, void* stream) {
+  StoreParams p;
+  return store_launch(args, stream, false, "oscar_store_v1", &p);
 }

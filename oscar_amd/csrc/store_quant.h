@@ -1,0 +1,267 @@
+// Device code of the INT2 quantizer shared by the store launches (store.hip) and the
+// decode's merge launch, which finishes deferred small stores (oscar_decode_write_v1):
+// the store parameters, destinations (last writers, window rule), the sort clip and
+// quant_vector (namespace oscar; inline and template definitions, identical in every
+// translation unit that includes it).
+#pragma once
+
+#include "common.h"
+
+namespace oscar {
+
+enum Kind { KIND_K = 0, KIND_V = 1, KIND_Q = 2 };
+
+typedef float __attribute__((ext_vector_type(2))) f32x2;
+
+// workgroups of the fused launch per kind at most (bounds the per-workgroup exact counts)
+constexpr int kMaxFusedGroups = 1024;
+
+struct StoreParams {
+  oscar_store_args_v1 a;
+  float* y;          // small calls: workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
+  int64_t capacity;  // num_blocks * block_size
+  int32_t* exact;    // large calls: [0] K total, [1] V total (written by the exact pass),
+                     // [2 + kind * kMaxFusedGroups + w] vectors workgroup w of the fused launch
+                     // left to the exact pass, then the lists [kind][nvec] (nvec = num_tokens *
+                     // num_kv_heads): workgroup w's entries start at its first vector
+  int32_t* flags;    // large calls: [num_tokens] bit 0 = position inside the window
+  u32x4* planes;     // large calls: R_k, R_v as fp16 MFMA B fragments [2][D/32][D/16][2][64]
+  int32_t* bexp;     // large calls: [2][D] power-of-two column scale of the planes
+  float* colnorm;    // large calls: [2][D] ||R_:d||
+  int32_t fused_kv_groups;  // large calls: fused workgroups per kind for K and for V
+  int32_t deferred;  // small calls of oscar_decode_write_v1: store_small_kernel rotates only
+                     // (read-path copies, rotated K / V in y, pending tags); the merge launch
+                     // of the decode quantizes (quant_deferred)
+};
+
+// Owner tag of a seat that a deferred small call rewrites, from its rotation launch to
+// its quantization: it matches no block, so a reader in between (the decode of
+// oscar_decode_write_v1) treats the seat as the call leaves it -- rewritten or
+// invalidated, the old token's FP32 copy is gone either way.
+constexpr int64_t kPendingTag = -2;
+
+__device__ __forceinline__ int32_t* exact_counts(const StoreParams& p, int kind) {
+  return p.exact + 2 + kind * kMaxFusedGroups;
+}
+__device__ __forceinline__ int32_t* exact_list(const StoreParams& p, int kind, int64_t nvec) {
+  return p.exact + 2 + 2 * kMaxFusedGroups + kind * nvec;
+}
+
+__device__ __forceinline__ long long claim_value(int64_t epoch, int64_t token) {
+  // 39-bit epoch above a 24-bit token index: 5e11 calls before the counter saturates
+  return (long long)((epoch << 24) | (token & 0xffffffll));
+}
+constexpr int64_t kMaxEpoch = (1ll << 39) - 1;
+
+__device__ __forceinline__ int64_t seat_of(int64_t slot, int64_t bs, int64_t rows) {
+  return ((slot / bs) % rows) * bs + slot % bs;
+}
+
+// 4 floats to dtype DT at element i (8 or 16 bytes, aligned)
+template <int DT>
+__device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
+  if constexpr (DT == OSCAR_F32) {
+    *(f32x4*)((float*)base + i) = f32x4{y[0], y[1], y[2], y[3]};
+  } else {
+    unsigned w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const unsigned lo = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j]) : f32_to_f16_bits(y[2 * j]);
+      const unsigned hi = DT == OSCAR_BF16 ? f32_to_bf16_bits(y[2 * j + 1]) : f32_to_f16_bits(y[2 * j + 1]);
+      w[j] = lo | (hi << 16);
+    }
+    *(u32x2*)((uint16_t*)base + i) = u32x2{w[0], w[1]};
+  }
+}
+
+// Sort-based clip threshold (backend.py:140-145): the idx-th smallest |x| of a
+// D-vector stored in LDS; ties are ordered by index so exactly one lane matches.
+template <int D>
+__device__ float clip_threshold(const float* row, int idx, volatile float* slot) {
+  const int lane = threadIdx.x & 63;
+  for (int i = lane; i < D; i += 64) {
+    float xi = fabsf(row[i]);
+    int rank = 0;
+    for (int j = 0; j < D; ++j) {
+      float xj = fabsf(row[j]);
+      rank += (xj < xi) || (xj == xi && j < i);
+    }
+    if (rank == idx) *slot = xi;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  return *slot;
+}
+
+// Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
+// the last writer of each, and whether its position lies inside its request's sink /
+// recent window (backend.py:536-541: keep the FP32 copy, else drop the seat).
+struct Dest {
+  int64_t slot, seat;
+  int64_t koff, voff;  // fused kernel: byte offsets of the K and V slots in the caches
+  bool valid, slot_win, seat_win, keep;
+};
+
+// the window rule for token t of a request of length seq whose queries end at end
+__device__ __forceinline__ bool in_window(const oscar_store_args_v1& a, int64_t t, int64_t seq, int64_t end) {
+  const int64_t pos = seq - end + t;
+  return (pos >= seq - a.recent_tokens) || (pos < a.sink_tokens_eff);
+}
+
+// Destination of a small call's vector: winners of duplicate slots / seats by
+// scanning slot_mapping.  Computed by one wave, wave-uniform, in two steps so that
+// the loads go out early and their results are used late: dest_loads issues every
+// load (the token's slot, lane l's request-table entry and lane l's slot of the
+// call), dest_finish decides.  A call has at most kFusedTokens (64) tokens, so one
+// slot per lane covers it; requests past the first 64 are read in dest_finish.
+struct DestLoads {
+  int64_t slot;     // slot_mapping[t]
+  int64_t s2;       // slot_mapping[lane] (-1 past the call)
+  int64_t st, nx, sq;  // query_start_loc[lane], [lane + 1], seq_lens[lane]
+};
+
+__device__ __forceinline__ DestLoads dest_loads(const StoreParams& p, int64_t t) {
+  const oscar_store_args_v1& a = p.a;
+  const int lane = threadIdx.x & 63;
+  DestLoads l;
+  l.slot = a.slot_mapping[t];
+  l.s2 = lane < a.num_tokens ? a.slot_mapping[lane] : -1;
+  const bool in = lane < a.num_reqs && a.stage_mode == OSCAR_STAGE_WRITE;
+  l.st = in ? a.query_start_loc[lane] : a.num_tokens;
+  l.nx = in ? a.query_start_loc[lane + 1] : a.num_tokens;
+  l.sq = in ? a.seq_lens[lane] : 0;
+  return l;
+}
+
+__device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, const DestLoads& l) {
+  const oscar_store_args_v1& a = p.a;
+  const int lane = threadIdx.x & 63;
+  const int64_t bs = a.cache.block_size;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  Dest d{};
+  const int64_t slot = l.slot;
+  // request of token t: the last r < num_reqs with min(qsl[r], num_tokens) <= t; its
+  // length and query end come from the same loads (qsl is non-decreasing)
+  int64_t seq = 0, end = 0;
+  if (window) {
+    for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
+      const int r = c0 + lane;
+      const bool in = r < a.num_reqs;
+      int64_t st = l.st, nx = l.nx, sq = l.sq;
+      if (c0 > 0) {
+        st = in ? a.query_start_loc[r] : a.num_tokens;
+        nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
+        sq = in ? a.seq_lens[r] : 0;
+      }
+      const int64_t start = st < a.num_tokens ? st : a.num_tokens;
+      const uint64_t bal = __ballot(in && start <= t);
+      if (bal) {
+        const int last = 63 - __builtin_clzll(bal);
+        seq = __shfl(sq, last);
+        end = __shfl(nx, last);
+      }
+    }
+  }
+  d.slot = slot;
+  d.keep = window && in_window(a, t, seq, end);
+  d.valid = slot >= 0 && slot < p.capacity;
+  if (!d.valid) return d;
+  const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
+  d.seat = seat;
+  // last writer: no later valid token of the call has the same slot / seat
+  {
+    const int64_t t2 = lane, s2 = l.s2;
+    const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
+    const bool later_slot = later && s2 == slot;
+    const bool later_seat = window && later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
+    d.slot_win = !__any(later_slot);
+    d.seat_win = window && !__any(later_seat);
+    // standalone KV update: every written seat loses its window copy
+    if (a.stage_mode == OSCAR_STAGE_INVALIDATE && kind == KIND_K && lane == 0) a.staging.owner[seat] = -1;
+  }
+  return d;
+}
+
+// Quantize, pack and scatter one rotated vector (kind K or V of token t, kv head h,
+// destination d) held by one wave (lane b < D / 4: elements 4b..4b+3 in x4), with
+// the staging window and owner tag of its seat.
+template <int D>
+__device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t h, const Dest& d, f32x4 x4,
+                             float* row, float* clip_slot) {
+  constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
+  const oscar_store_args_v1& a = p.a;
+  const int64_t hk = a.cache.num_kv_heads;
+  const int lane = threadIdx.x & 63;
+  const bool active = lane < NL;
+  const int64_t bs = a.cache.block_size;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  if (!d.valid) return;
+  const int64_t slot = d.slot, seat = d.seat;
+  const bool slot_win = d.slot_win, seat_win = d.seat_win;
+  const int64_t blk = slot / bs, off = slot % bs;
+  if (active) *(f32x4*)&row[4 * lane] = x4;
+
+  if (window && seat_win) {
+    const bool keep = d.keep;
+    if (kind == KIND_K && lane == 0) a.staging.owner[seat] = keep ? blk : -1;
+    if (keep && active) {
+      float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) + (seat * hk + h) * D;
+      *(f32x4*)&dst[4 * lane] = x4;
+    }
+  }
+  if (!slot_win) return;
+
+  const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
+  float thr = INFINITY;
+  if (clip > 0.f) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    int idx = (int)(clip * (float)D);
+    if (idx > D - 1) idx = D - 1;
+    thr = clip_threshold<D>(row, idx, clip_slot);
+  }
+  // lane b handles byte b = elements 4b..4b+3
+  float x[4];
+  float vmin = INFINITY, vmax = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = active ? x4[j] : 0.f;
+    if (clip > 0.f) v = fminf(fmaxf(v, -thr), thr);
+    x[j] = v;
+    if (active) { vmin = fminf(vmin, v); vmax = fmaxf(vmax, v); }
+  }
+  vmin = wave_min(vmin);
+  vmax = wave_max(vmax);
+  float scale = __fdiv_rn(vmax - vmin, 3.0f);
+  if (!(scale > 0x1p-14f)) scale = 0x1p-14f;
+  const unsigned short scale_bits = f32_to_f16_bits(scale);
+  const unsigned short zero_bits = f32_to_f16_bits(vmin);
+  const float s16 = f16_bits_to_f32(scale_bits), z16 = f16_bits_to_f32(zero_bits);
+  uint8_t* kslot = a.cache.k + blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
+  uint8_t* vslot = a.cache.v + blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
+  if (active) {
+    unsigned byte = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float q = floorf(__fdiv_rn(x[j] - z16, s16) + 0.5f);
+      q = fminf(fmaxf(q, 0.f), 3.f);
+      byte |= (unsigned)((int)q & 3) << (2 * j);
+    }
+    uint8_t* dst = (kind == KIND_K) ? (kslot + 32) : vslot;
+    dst[lane] = (uint8_t)byte;
+  }
+  if (lane == 0) {
+    unsigned meta = (unsigned)scale_bits | ((unsigned)zero_bits << 16);
+    *(unsigned*)(kslot + (kind == KIND_K ? 0 : 4)) = meta;
+  }
+}
+
+// Store launch shared by oscar_store_v1 and oscar_decode_write_v1 (store.hip): checks
+// the arguments (messages prefixed by fn), then launches the store on stream; with
+// defer and a call of at most 64 tokens only the rotation (store_small_kernel with
+// p.deferred = 1: read-path copies, rotated K / V in p.y, pending tags), the
+// quantization being left to quant_deferred in the decode's merge launch.  *out
+// receives the parameters; returns 0, or the negative error.
+int store_launch(const oscar_store_args_v1* args, void* stream, bool defer, const char* fn, StoreParams* out);
+
+}  // namespace oscar

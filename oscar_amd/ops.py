@@ -201,20 +201,30 @@ def decode_step(ctx: DeviceContext, args: "_lib.StepArgs", stream: int) -> int:
 
 
 # ------------------------------------------------------------------------ store
-def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=None,
-          k_clip=0.0, v_clip=0.0, stage=None, stage_mode=STAGE_NONE, qsl_dev=None,
-          seqs_dev=None, num_reqs=0, recent_tokens=0, sink_tokens_eff=0, query=None,
-          query_rot=None, key_rot=None, value_rot=None):
+def store(key, value, k_cache, v_cache, slot_mapping, **kw):
     """Rotate + clip + INT2 quantize + scatter (+ staging window) in one C call.
 
     key/value [N, Hk, D] (bf16/fp16/fp32), slot_mapping [N] int64 (negative = skip).
     rk/rv fp32 [D, D] or None for identity.  Optional query [N, Hq, D] and
-    *_rot outputs receive the unclipped rotated values in the input dtype.
+    *_rot outputs receive the unclipped rotated values in the input dtype.  Keyword
+    arguments as store_args.
     """
+    args = store_args(key, value, k_cache, v_cache, slot_mapping, **kw)
+    if args is not None:
+        _lib.check(_lib.load().oscar_store_v1(C.byref(args[0]), C.c_void_p(_stream(key.device))), "oscar_store_v1")
+
+
+def store_args(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=None,
+               k_clip=0.0, v_clip=0.0, stage=None, stage_mode=STAGE_NONE, qsl_dev=None,
+               seqs_dev=None, num_reqs=0, recent_tokens=0, sink_tokens_eff=0, query=None,
+               query_rot=None, key_rot=None, value_rot=None):
+    """The C arguments of a store (None for an empty call) and the tensors they point
+    into, for oscar_store_v1 (store) or oscar_decode_write_v1 (attention_decode's
+    `store`)."""
     _require_cuda(key, value, k_cache, v_cache, slot_mapping)
     n = slot_mapping.shape[0]
     if n == 0:
-        return
+        return None
     lib = _lib.load()
     dev = key.device
     hk = k_cache.shape[2]
@@ -267,7 +277,7 @@ def store(key, value, k_cache, v_cache, slot_mapping, *, head_dim, rk=None, rv=N
     ws = scratch.store_workspace(need)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.arrivals = scratch.store_arrivals(hk).data_ptr()
-    _lib.check(lib.oscar_store_v1(C.byref(a), C.c_void_p(_stream(dev))), "oscar_store_v1")
+    return a, (key, value, slot_mapping, query, st, ws)
 
 
 # ------------------------------------------------------------------------ rotate
@@ -387,13 +397,18 @@ def _check_table(table: torch.Tensor, plan: DecodePlan, block_size: int) -> None
 
 
 def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: DecodePlan, scale,
-                     stage=None, *, head_dim, out_rot=None, lse=None, phases=0, static_scratch=False):
+                     stage=None, *, head_dim, out_rot=None, lse=None, phases=0, static_scratch=False,
+                     store=None):
     """Rotated-domain attention over INT2 history (+ current chunk): (out_rot fp32, lse fp32).
 
     q (and k_new / v_new) are bf16 or fp16; history values are rounded q_dtype(fp16(x)).
     static_scratch: call oscar_attn_decode_static_v1 (item partials in the library's
-    static device array, no workspace)."""
+    static device array, no workspace).  store: store_args(...) of the step's write, whose
+    rotated outputs are q / k_new / v_new: one oscar_decode_write_v1 call runs the store
+    and the decode (a small store's quantization then rides in the merge launch)."""
     _require_cuda(q, k_cache, v_cache, block_table)
+    if store is not None and static_scratch:
+        raise ValueError("store= goes with the workspace decode only")
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("OSCAR HIP attention requires bf16 or fp16 queries")
     n, hq, _ = q.shape
@@ -403,6 +418,8 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     if lse is None:
         lse = torch.full((n, hq), -math.inf, dtype=torch.float32, device=dev)
     if plan.num_items == 0 or n == 0:
+        if store is not None:
+            _lib.check(_lib.load().oscar_store_v1(C.byref(store[0]), C.c_void_p(_stream(dev))), "oscar_store_v1")
         return out_rot, lse
     if q.stride(2) != 1 or q.stride(1) != head_dim:
         q = q.contiguous()
@@ -441,6 +458,10 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
     a.phases = int(phases)
     a.q_dtype = _DTYPES[q.dtype]
     lib = _lib.load()
+    if store is not None:
+        _lib.check(lib.oscar_decode_write_v1(C.byref(store[0]), C.byref(a), C.c_void_p(_stream(dev))),
+                   "oscar_decode_write_v1")
+        return out_rot, lse
     entry = "oscar_attn_decode_static_v1" if static_scratch else "oscar_attn_decode_v1"
     _lib.check(getattr(lib, entry)(C.byref(a), C.c_void_p(_stream(dev))), entry)
     return out_rot, lse

@@ -34,7 +34,7 @@ def header_functions() -> set:
 
 def test_library_exports_every_header_symbol(lib):
     names = header_functions()
-    assert len(names) == 16, names
+    assert len(names) == 17, names
     for name in names:
         assert hasattr(lib, name), name
     assert names == set(_lib.SIGNATURES)
@@ -308,6 +308,7 @@ def test_entry_points_reject_null_and_unsupported_args_without_touching_the_gpu(
     assert lib.oscar_rotate_v1(None, None) == -22
     assert lib.oscar_attn_decode_v1(None, None) == -22
     assert lib.oscar_attn_decode_static_v1(None, None) == -22
+    assert lib.oscar_decode_write_v1(None, None, None) == -22
     assert lib.oscar_attn_prefill_v1(None, None) == -22
     r = _lib.RotateArgs(rows=4, head_dim=96, x=1, r=1, out=1)
     assert lib.oscar_rotate_v1(C.byref(r), None) == -22 and b"head_dim" in lib.oscar_last_error()

@@ -371,3 +371,72 @@ def test_rotate_matches_fp32_reference(cuda):
         ref = x.astype(np.float64) @ (r.T if transpose else r).astype(np.float64)
         err = np.abs(got - ref).max()
         assert err < 1e-4, err
+
+
+def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda):
+    """oscar_decode_write_v1 (store + decode in one call, the small store's quantization
+    in the merge launch): request 1's new tokens are written onto the window seats of
+    request 0's last four history tokens (an 8-row arena), whose keys dominate request
+    0's scores (key ramp).  The decode must see those seats as the store leaves them --
+    the old tokens back on their INT2 codes -- and the window, tags and bytes must end
+    as the oracle's."""
+    import copy
+    import math
+    from oscar_amd import ops
+    from oscar_amd._lib import STAGE_WRITE
+    from oracle.store import Staging, store_ref
+
+    d, bs, prefixes = 256, 128, [3000, 700]
+    c = cases.make_case(prefixes, [4, 4], fresh=True, seed=93, key_ramp=4.0)
+    bt = c["bt"]
+    st = Staging(bs, 1, d, 128, 256, 1024)  # 8 rows: blocks share rows
+    sk0, sv0, own0 = c["stage"]
+    staged = [(int(b), col, r0) for r0 in range(own0.shape[0]) for col in range(bs) if (b := own0[r0, col]) >= 0]
+    p = np.arange(prefixes[0] - 4, prefixes[0])
+    last = {(int(bt[0, q // bs]), int(q % bs)) for q in p}
+    for b, col, r0 in sorted(staged, key=lambda x: (x[0], x[1]) in last):  # request 0's last tokens win
+        st.owner[b % st.rows, col] = b
+        st.stage_k[b % st.rows, col], st.stage_v[b % st.rows, col] = sk0[r0, col], sv0[r0, col]
+    used = set(bt[0, :math.ceil(c["seqs"][0] / bs)].tolist()) | set(bt[1, :math.ceil(c["seqs"][1] / bs)].tolist())
+    blk0 = int(bt[0, p[0] // bs])
+    target = next(b for b in range(c["k8"].shape[0]) if b not in used and b % st.rows == blk0 % st.rows)
+    pos0 = np.arange(prefixes[0], prefixes[0] + 4)
+    slots = np.concatenate([bt[0, pos0 // bs].astype(np.int64) * bs + pos0 % bs,
+                            target * bs + (p % bs).astype(np.int64)])
+    # the oracle: the window after the store (identity rotations), then the attention
+    post = copy.deepcopy(st)
+    post.write(c["k"], c["v"], slots, c["qsl"], c["seqs"])
+    assert all(post.owner[blk0 % st.rows, q % bs] == target for q in p)
+    ref_o, ref_l = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
+                                 post.arrays())
+    pre_o, _ = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
+                             st.arrays())
+    gap = np.abs(ref_o - pre_o).max()
+    print(f"window before vs after the store: max|dO| {gap:.3e}", flush=True)
+    assert gap > 5 * OUT_TOL  # the case tells the two windows apart
+    kc = torch.from_numpy(c["k8"].copy()).view(torch.int8).cuda()
+    vc = torch.from_numpy(c["v8"].copy()).view(torch.int8).cuda()
+    sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
+    n, hq = c["q"].shape[:2]
+    q_rot = torch.empty(n, hq, d, dtype=torch.bfloat16, device="cuda")
+    k_rot = torch.empty(n, 1, d, dtype=torch.bfloat16, device="cuda")
+    v_rot = torch.empty_like(k_rot)
+    plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=1, group=6, head_dim=d,
+                           device=torch.device("cuda"), window=(st.sink_eff, 256))
+    store = ops.store_args(dev(c["k"]), dev(c["v"]), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+                           stage=(sk, sv, own), stage_mode=STAGE_WRITE,
+                           qsl_dev=torch.tensor(c["qsl"], dtype=torch.int32, device="cuda"),
+                           seqs_dev=torch.tensor(c["seqs"], dtype=torch.int32, device="cuda"), num_reqs=2,
+                           recent_tokens=256, sink_tokens_eff=st.sink_eff, query=dev(c["q"]), query_rot=q_rot,
+                           key_rot=k_rot, value_rot=v_rot)
+    out, lse = ops.attention_decode(q_rot, k_rot, v_rot, kc, vc, torch.from_numpy(bt).cuda(), plan, c["scale"],
+                                    (sk, sv, own), head_dim=d, store=store)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), lse.cpu().numpy(), ref_o, ref_l, "decode_write over rewritten seats")
+    k8, v8 = c["k8"].copy(), c["v8"].copy()
+    store_ref(c["k"], c["v"], k8, v8, slots)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
+    assert np.array_equal(own.cpu().numpy(), post.owner)
+    assert np.array_equal(sk.cpu().numpy(), post.stage_k)
+    assert np.array_equal(sv.cpu().numpy(), post.stage_v)
