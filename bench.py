@@ -37,7 +37,8 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "attn_main_8x24k_mtp_traffic.txt"
 LAYERS = 16
 CONFIG = dict(requests=8, history=24576, q_len=4, hq=6, hk=1, d=256, block_size=128,
-              sink_tokens=64, recent_tokens=256, staging_tokens=8192)
+              sink_tokens=64, recent_tokens=256, staging_tokens=8192,
+              k_clip=0.0, v_clip=0.0)  # sort-clip ratios of the step's write (--clip: the serve defaults)
 
 
 def log(msg):
@@ -164,7 +165,7 @@ class Setup:
         if self.has_new:
             # the write and the decode in one call (oscar_decode_write_v1)
             store = ops.store_args(self.k_new, self.v_new, kc, vc, self.slots, head_dim=c["d"], rk=self.rk,
-                                   rv=self.rv, stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
+                                   rv=self.rv, k_clip=c["k_clip"], v_clip=c["v_clip"], stage=stage, stage_mode=STAGE_WRITE, qsl_dev=self.qsl_dev,
                                    seqs_dev=self.seq_dev, num_reqs=len(self.seqs),
                                    recent_tokens=c["recent_tokens"], sink_tokens_eff=self.sink_eff, query=self.q,
                                    query_rot=self.q_rot, key_rot=self.k_rot, value_rot=self.v_rot)
@@ -308,7 +309,7 @@ def config_decode(dev, name, histories, q_len, has_new, layers, steps, warmup):
             "data": "synthetic",
             "config": {"workload": name, "requests": len(histories), "history_total": sum(histories),
                        "q_len": q_len, "has_new": has_new, "layers_cycled": layers,
-                       "staged_total": sum(staged)},
+                       "staged_total": sum(staged), "clip": [CONFIG["k_clip"], CONFIG["v_clip"]]},
             "roofline": {"bound": "hbm", "kernel": "attn_main_kernel<256>", "achieved": achieved,
                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                          "algorithmic_bytes": b_main, "kernel_us": med_ms * 1e3, "traffic": None}}
@@ -662,6 +663,9 @@ def main(argv=None):
     ap.add_argument("--config", default="4a", choices=["4a", "2", "3", "4b", "5"],
                     help="4a (default, the headline metric); 2 store; 3 single-request MTP; "
                          "4b 64 cache-only decodes; 5 continuation prefill")
+    ap.add_argument("--clip", action="store_true",
+                    help="the step's write with the serve defaults' sort clip (K 0.96, V 0.92; "
+                         "delivery/serve_oscar.sh:32-33) instead of the library default (off)")
     ap.add_argument("--profile-main", action="store_true",
                     help="only run attn_main over the layer caches plus a calibration copy "
                          "(the workload of the rocprofv3 --pmc passes)")
@@ -669,6 +673,8 @@ def main(argv=None):
                     help="FETCH_CSV WRITE_CSV [RDREQ_CSV]: turn the counter-collection CSVs into "
                          + str(TRAFFIC_FILE))
     args = ap.parse_args(argv)
+    if args.clip:
+        CONFIG.update(k_clip=0.96, v_clip=0.92)
     if args.pmc_summary:
         if len(args.pmc_summary) not in (2, 3):
             ap.error("--pmc-summary takes FETCH_CSV WRITE_CSV [RDREQ_CSV]")
@@ -751,7 +757,8 @@ def main(argv=None):
                                "16 layer caches cycled",
                    "requests": c["requests"], "history": c["history"], "q_len": c["q_len"],
                    "hq": c["hq"], "hk": c["hk"], "head_dim": c["d"], "block_size": c["block_size"],
-                   "layers_cycled": LAYERS, "staged_per_request": staged},
+                   "layers_cycled": LAYERS, "staged_per_request": staged,
+                   "clip": [c["k_clip"], c["v_clip"]]},
         "roofline": {"bound": "hbm", "kernel": "attn_main_kernel<256>", "achieved": achieved,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "algorithmic_bytes": b_main, "kernel_us": med_ms * 1e3,

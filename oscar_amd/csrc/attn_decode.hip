@@ -920,8 +920,6 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
   // rotation launch left in S.y and writes its slot bytes, FP32 window copy and owner
   // tag, as store_small_kernel's last slice workgroup does in the one-launch form.  It
   // runs beside the merge: nothing here reads the cache or the window.
-  __shared__ float s_qrow[kMergeWaves][D];
-  __shared__ float s_qclip[kMergeWaves];
   if ((int)blockIdx.x >= A.num_groups) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t hk = S.a.cache.num_kv_heads, nkv = S.a.num_tokens * hk;
@@ -933,7 +931,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
     const DestLoads dl = dest_loads(S, t);
     const f32x4 x4 = *(const f32x4*)(S.y + ((int64_t)kind * nkv + vw) * D + 4 * (lane < D / 4 ? lane : 0));
     const Dest dest = dest_finish(S, kind, t, dl);
-    quant_vector<D>(S, kind, t, h, dest, x4, s_qrow[wave], &s_qclip[wave]);
+    quant_vector<D>(S, kind, t, h, dest, x4);
     return;
   }
   // the group record carries everything the merge needs (no dependent loads)

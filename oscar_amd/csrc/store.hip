@@ -88,8 +88,6 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
 
   __shared__ __attribute__((aligned(16))) double s_x[kSmallVecs][D];
   __shared__ double s_red[kSmallParts][kSmallVecs * kSmallCols];
-  __shared__ float s_row[kSmallVecs][D];
-  __shared__ float s_clip[kSmallVecs];
   __shared__ int s_last;
   // this thread's rows kp * RPT + i of the slice's columns c0 + 2 cp, + 1: issued
   // first, used after the barrier
@@ -182,7 +180,7 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
   f32x4 x4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) x4[j] = __hip_atomic_load(yv + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  quant_vector<D>(p, kind, t, h, dest, x4, s_row[wave], &s_clip[wave]);
+  quant_vector<D>(p, kind, t, h, dest, x4);
 }
 
 
@@ -935,10 +933,9 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   // the slices' partial sums: [slice][vector][column pair half][quad], one double2 each
   // (consecutive quads in consecutive 16-byte words)
   __shared__ __attribute__((aligned(16))) double2 s_part[S][G][2][NQ];
-  // y, then the quantizer's scratch row of the same vector (its wave reads y first)
+  // y of the group's vectors, rounded to fp32
   __shared__ __attribute__((aligned(16))) float s_y[G][D];
   __shared__ int32_t s_id[G];
-  __shared__ float s_clip[G];
   __shared__ Dest s_dst[G];
   for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
     // ---- the group's entries: each list position g0 .. g0 + G - 1 below count lies in
@@ -1046,7 +1043,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       const int32_t id = s_id[v];
       if (id < 0) continue;
       const f32x4 y4 = *(const f32x4*)&s_y[v][4 * (lane < D / 4 ? lane : 0)];
-      quant_vector<D>(p, kind, id / hk, id % hk, s_dst[v], y4, s_y[v], &s_clip[v]);
+      quant_vector<D>(p, kind, id / hk, id % hk, s_dst[v], y4);
     }
     __syncthreads();  // s_id, s_xd, s_part, s_y, s_dst are rewritten by the next group
     load_rows(0, ra);  // the next group's first rows (ra holds this group's last batch)

@@ -74,23 +74,26 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
   }
 }
 
-// Sort-based clip threshold (backend.py:140-145): the idx-th smallest |x| of a
-// D-vector stored in LDS; ties are ordered by index so exactly one lane matches.
+// Sort-clip threshold (backend.py:140-145): the idx-th smallest |x| (0-based) of a
+// D-vector held by one wave, lane l < D / 4 holding elements 4l .. 4l + 3 in x4.
+// Selected bit by bit from the top on the magnitude bits (the order of |x|; NaN above
+// inf, as a sort puts it last): the answer is the largest v with count(|x| < v) <= idx,
+// each count four ballots of the wave.
 template <int D>
-__device__ float clip_threshold(const float* row, int idx, volatile float* slot) {
-  const int lane = threadIdx.x & 63;
-  for (int i = lane; i < D; i += 64) {
-    float xi = fabsf(row[i]);
-    int rank = 0;
-    for (int j = 0; j < D; ++j) {
-      float xj = fabsf(row[j]);
-      rank += (xj < xi) || (xj == xi && j < i);
-    }
-    if (rank == idx) *slot = xi;
+__device__ float wave_kth_abs(f32x4 x4, int idx) {
+  const bool active = (int)(threadIdx.x & 63) < D / 4;
+  uint32_t u[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) u[j] = active ? (__float_as_uint(x4[j]) & 0x7fffffffu) : 0xffffffffu;
+  uint32_t v = 0;
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t cand = v | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot(u[j] < cand));
+    if (cnt <= idx) v = cand;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  return *slot;
+  return __uint_as_float(v);
 }
 
 // Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
@@ -186,8 +189,7 @@ __device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, co
 // destination d) held by one wave (lane b < D / 4: elements 4b..4b+3 in x4), with
 // the staging window and owner tag of its seat.
 template <int D>
-__device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t h, const Dest& d, f32x4 x4,
-                             float* row, float* clip_slot) {
+__device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t h, const Dest& d, f32x4 x4) {
   constexpr int NL = D / 4;  // lanes holding 4 elements (one packed byte) each
   const oscar_store_args_v1& a = p.a;
   const int64_t hk = a.cache.num_kv_heads;
@@ -199,7 +201,6 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
   const int64_t slot = d.slot, seat = d.seat;
   const bool slot_win = d.slot_win, seat_win = d.seat_win;
   const int64_t blk = slot / bs, off = slot % bs;
-  if (active) *(f32x4*)&row[4 * lane] = x4;
 
   if (window && seat_win) {
     const bool keep = d.keep;
@@ -214,11 +215,9 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
   const float clip = kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio;
   float thr = INFINITY;
   if (clip > 0.f) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
     int idx = (int)(clip * (float)D);
     if (idx > D - 1) idx = D - 1;
-    thr = clip_threshold<D>(row, idx, clip_slot);
+    thr = wave_kth_abs<D>(x4, idx);
   }
   // lane b handles byte b = elements 4b..4b+3
   float x[4];
