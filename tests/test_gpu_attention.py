@@ -373,7 +373,8 @@ def test_rotate_matches_fp32_reference(cuda):
         assert err < 1e-4, err
 
 
-def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda):
+@pytest.mark.parametrize("d,hk,group", [(256, 1, 6), (128, 2, 4)])
+def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group):
     """oscar_decode_write_v1 (store + decode in one call, the small store's quantization
     in the merge launch): request 1's new tokens are written onto the window seats of
     request 0's last four history tokens (an 8-row arena), whose keys dominate request
@@ -386,27 +387,34 @@ def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda):
     from oscar_amd._lib import STAGE_WRITE
     from oracle.store import Staging, store_ref
 
-    d, bs, prefixes = 256, 128, [3000, 700]
-    c = cases.make_case(prefixes, [4, 4], fresh=True, seed=93, key_ramp=4.0)
+    bs, prefixes = 128, [3000, 700]
+    c = cases.make_case(prefixes, [4, 4], fresh=True, seed=93, key_ramp=4.0, hk=hk, group=group, d=d)
     bt = c["bt"]
-    st = Staging(bs, 1, d, 128, 256, 1024)  # 8 rows: blocks share rows
+    st = Staging(bs, hk, d, 128, 256, 1024)  # 8 rows: blocks share rows
     sk0, sv0, own0 = c["stage"]
-    staged = [(int(b), col, r0) for r0 in range(own0.shape[0]) for col in range(bs) if (b := own0[r0, col]) >= 0]
-    p = np.arange(prefixes[0] - 4, prefixes[0])
+    # request 0's four staged window tokens with the largest scores (over its query rows)
+    # are the ones request 1's new tokens will evict
+    win = np.arange(prefixes[0] - 256, prefixes[0])
+    q0 = c["q"][c["qsl"][0]:c["qsl"][1]].reshape(-1, hk, group, d)
+    kw = np.stack([sk0[int(bt[0, q // bs]) % own0.shape[0], q % bs] for q in win])  # [256, hk, d]
+    score = np.max(np.stack([(q0[:, h] @ kw[:, h].T).max(axis=(0, 1)) for h in range(hk)]), axis=0)
+    p = np.sort(win[np.argsort(score)[-4:]])
     last = {(int(bt[0, q // bs]), int(q % bs)) for q in p}
-    for b, col, r0 in sorted(staged, key=lambda x: (x[0], x[1]) in last):  # request 0's last tokens win
+    staged = [(int(b), col, r0) for r0 in range(own0.shape[0]) for col in range(bs) if (b := own0[r0, col]) >= 0]
+    for b, col, r0 in sorted(staged, key=lambda x: (x[0], x[1]) in last):  # the chosen tokens win
         st.owner[b % st.rows, col] = b
         st.stage_k[b % st.rows, col], st.stage_v[b % st.rows, col] = sk0[r0, col], sv0[r0, col]
     used = set(bt[0, :math.ceil(c["seqs"][0] / bs)].tolist()) | set(bt[1, :math.ceil(c["seqs"][1] / bs)].tolist())
-    blk0 = int(bt[0, p[0] // bs])
-    target = next(b for b in range(c["k8"].shape[0]) if b not in used and b % st.rows == blk0 % st.rows)
+    free = [b for b in range(c["k8"].shape[0]) if b not in used]
+    blk = [int(bt[0, q // bs]) for q in p]
+    target = [next(b for b in free if b % st.rows == x % st.rows) for x in blk]
     pos0 = np.arange(prefixes[0], prefixes[0] + 4)
     slots = np.concatenate([bt[0, pos0 // bs].astype(np.int64) * bs + pos0 % bs,
-                            target * bs + (p % bs).astype(np.int64)])
+                            np.array(target, np.int64) * bs + (p % bs).astype(np.int64)])
     # the oracle: the window after the store (identity rotations), then the attention
     post = copy.deepcopy(st)
     post.write(c["k"], c["v"], slots, c["qsl"], c["seqs"])
-    assert all(post.owner[blk0 % st.rows, q % bs] == target for q in p)
+    assert all(post.owner[b % st.rows, q % bs] == t for b, q, t in zip(blk, p, target))
     ref_o, ref_l = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
                                  post.arrays())
     pre_o, _ = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
@@ -419,9 +427,9 @@ def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda):
     sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
     n, hq = c["q"].shape[:2]
     q_rot = torch.empty(n, hq, d, dtype=torch.bfloat16, device="cuda")
-    k_rot = torch.empty(n, 1, d, dtype=torch.bfloat16, device="cuda")
+    k_rot = torch.empty(n, hk, d, dtype=torch.bfloat16, device="cuda")
     v_rot = torch.empty_like(k_rot)
-    plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=1, group=6, head_dim=d,
+    plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=hk, group=group, head_dim=d,
                            device=torch.device("cuda"), window=(st.sink_eff, 256))
     store = ops.store_args(dev(c["k"]), dev(c["v"]), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
                            stage=(sk, sv, own), stage_mode=STAGE_WRITE,
