@@ -74,12 +74,14 @@ class Setup:
 
         c = CONFIG
         histories = histories or [c["history"]] * c["requests"]
-        n = q_len or c["q_len"]
         B = len(histories)
+        # new tokens (or cache-only queries) per request: one count, or one per request
+        ns = [int(x) for x in q_len] if isinstance(q_len, (list, tuple)) else [q_len or c["q_len"]] * B
+        n, total = ns[0], sum(ns)
         hq, hk, d, bs = c["hq"], c["hk"], c["d"], c["block_size"]
         self.dev, self.n, self.has_new, self.histories = dev, n, has_new, list(histories)
         gen = torch.Generator(device=dev).manual_seed(seed)
-        span = [L + (n if has_new else 0) for L in histories]
+        span = [L + (nr if has_new else 0) for L, nr in zip(histories, ns)]
         pages = [math.ceil(x / bs) for x in span]
         self.nb = sum(pages)
         perm = torch.randperm(self.nb, generator=gen, device=dev).to(torch.int32)
@@ -127,18 +129,18 @@ class Setup:
         torch.cuda.synchronize()
         # step inputs: n new tokens per request at positions L..L+n-1 (or, cache-only,
         # n queries over the cached history)
-        self.q = torch.randn(B * n, hq, d, generator=gen, device=dev).bfloat16()
-        self.qsl = [i * n for i in range(B + 1)]
+        self.q = torch.randn(total, hq, d, generator=gen, device=dev).bfloat16()
+        self.qsl = [0] + np.cumsum(ns).tolist()
         self.q_rot = torch.empty_like(self.q)
         if has_new:
-            self.k_new = outlier_kv(B * n, hk, d, gen, dev)
-            self.v_new = outlier_kv(B * n, hk, d, gen, dev)
+            self.k_new = outlier_kv(total, hk, d, gen, dev)
+            self.v_new = outlier_kv(total, hk, d, gen, dev)
             sl = []
-            for r, L in enumerate(histories):
-                npos = torch.arange(L, L + n, device=dev)
+            for r, (L, nr) in enumerate(zip(histories, ns)):
+                npos = torch.arange(L, L + nr, device=dev)
                 sl.append(self.bt[r, npos // bs].long() * bs + npos % bs)
             self.slots = torch.cat(sl).contiguous()
-            self.seqs = [L + n for L in histories]
+            self.seqs = [L + nr for L, nr in zip(histories, ns)]
             self.k_rot = torch.empty_like(self.k_new)
             self.v_rot = torch.empty_like(self.v_new)
         else:
@@ -146,11 +148,11 @@ class Setup:
             self.seqs = list(histories)
         self.qsl_dev = torch.tensor(self.qsl, dtype=torch.int32, device=dev)
         self.seq_dev = torch.tensor(self.seqs, dtype=torch.int32, device=dev)
-        self.out_rot = torch.zeros(B * n, hq, d, dtype=torch.float32, device=dev)
-        self.lse = torch.zeros(B * n, hq, dtype=torch.float32, device=dev)
-        self.out = torch.empty(B * n, hq, d, dtype=torch.bfloat16, device=dev)
+        self.out_rot = torch.zeros(total, hq, d, dtype=torch.float32, device=dev)
+        self.lse = torch.zeros(total, hq, dtype=torch.float32, device=dev)
+        self.out = torch.empty(total, hq, d, dtype=torch.bfloat16, device=dev)
         self.plan = None
-        if n * (hq // hk) <= 32:  # decode-shaped: the split-K plan of the benchmarked step
+        if len(set(ns)) == 1 and n * (hq // hk) <= 32:  # decode-shaped: the split-K plan of the step
             self.plan = ops.plan_decode(self.qsl, self.seqs, has_new=has_new, num_kv_heads=hk,
                                         group=hq // hk, head_dim=d, device=dev,
                                         window=(self.sink_eff, c["recent_tokens"]))
@@ -480,21 +482,24 @@ def compare_calls_ms(fn, repeats=6):
     return {"first_call_ms": first, "median_ms": float(np.median(warm)), "samples_ms": warm}
 
 
-# tools/benchmark_streaming.py:16-20: (name, requests, prefix, query tokens)
-FORWARD_CASES = (("mtp", 1, 24579, 4), ("concurrent", 8, 24579, 4), ("prefill", 1, 15360, 9256))
+# tools/benchmark_streaming.py:16-20: (name, histories, query tokens per request), plus the
+# config-5 batch in one call (the continuation, 16 decodes over 8192 tokens, a 2048-token
+# history-free prefill)
+FORWARD_CASES = (("mtp", [24579], 4), ("concurrent", [24579] * 8, 4), ("prefill", [15360], 9256),
+                 ("config5_batched", [15360] + [8192] * 16 + [0], [9256] + [1] * 16 + [2048]))
 
 
 def forward_timings(dev):
     """impl.forward per call at the reference's three bench cases (its scope: one layer's
     full forward incl. write, window and rotations), host-timed around device syncs."""
     res = {}
-    for name, batch, prefix, count in FORWARD_CASES:
-        setup = Setup(dev, [prefix] * batch, count, True, layers=1, seed=20261210)
+    for name, histories, count in FORWARD_CASES:
+        setup = Setup(dev, histories, count, True, layers=1, seed=20261210)
         call = forward_call(setup)
         res[name] = compare_calls_ms(call)
         # back to back as a serving loop calls it (no synchronisation between calls):
         # the per-call rate once host work and device work overlap
-        reps = 50 if name != "prefill" else 5
+        reps = 50 if name in ("mtp", "concurrent") else 5
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(reps):
