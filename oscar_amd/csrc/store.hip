@@ -10,7 +10,10 @@
 //
 //   calls of <= kFusedTokens tokens (decode / MTP steps): store_small_kernel, one
 //   launch of (32-column slice, group of 8 vectors) workgroups; y in fp64 (exact
-//   products, one rounding), winners by scanning the call's slot_mapping.
+//   products, one rounding), winners by scanning the call's slot_mapping.  Under
+//   oscar_decode_write_v1 the launch stops after the rotation (deferred: pending owner
+//   tags on the seats it rewrites) and the decode's merge launch quantizes
+//   (store_quant.h).
 //
 //   larger calls: store_prep_kernel (last-writer claims, window flags, fp16 planes of R),
 //   store_fused_kernel (MFMA rotation into LDS, then per vector: read-path copy,
