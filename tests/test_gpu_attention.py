@@ -373,8 +373,9 @@ def test_rotate_matches_fp32_reference(cuda):
         assert err < 1e-4, err
 
 
-@pytest.mark.parametrize("d,hk,group", [(256, 1, 6), (128, 2, 4)])
-def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group):
+@pytest.mark.parametrize("d,hk,group,mode", [(256, 1, 6, "write"), (128, 2, 4, "write"), (256, 1, 6, "write_clip"),
+                                             (128, 2, 4, "invalidate")])
+def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group, mode):
     """oscar_decode_write_v1 (store + decode in one call, the small store's quantization
     in the merge launch): request 1's new tokens are written onto the window seats of
     request 0's last four history tokens (an 8-row arena), whose keys dominate request
@@ -384,8 +385,8 @@ def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group)
     import copy
     import math
     from oscar_amd import ops
-    from oscar_amd._lib import STAGE_WRITE
-    from oracle.store import Staging, store_ref
+    from oscar_amd._lib import STAGE_INVALIDATE, STAGE_WRITE
+    from oracle.store import Staging, clip, store_ref
 
     bs, prefixes = 128, [3000, 700]
     c = cases.make_case(prefixes, [4, 4], fresh=True, seed=93, key_ramp=4.0, hk=hk, group=group, d=d)
@@ -413,8 +414,12 @@ def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group)
                             np.array(target, np.int64) * bs + (p % bs).astype(np.int64)])
     # the oracle: the window after the store (identity rotations), then the attention
     post = copy.deepcopy(st)
-    post.write(c["k"], c["v"], slots, c["qsl"], c["seqs"])
-    assert all(post.owner[b % st.rows, q % bs] == t for b, q, t in zip(blk, p, target))
+    if mode == "invalidate":  # a standalone KV update: the rewritten seats lose their copies
+        post.invalidate(slots)
+        assert all(post.owner[b % st.rows, q % bs] == -1 for b, q in zip(blk, p))
+    else:
+        post.write(c["k"], c["v"], slots, c["qsl"], c["seqs"])
+        assert all(post.owner[b % st.rows, q % bs] == t for b, q, t in zip(blk, p, target))
     ref_o, ref_l = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
                                  post.arrays())
     pre_o, _ = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], bt, c["qsl"], c["seqs"], c["scale"],
@@ -431,18 +436,23 @@ def test_decode_write_sees_the_window_as_the_store_leaves_it(cuda, d, hk, group)
     v_rot = torch.empty_like(k_rot)
     plan = ops.plan_decode(c["qsl"], c["seqs"], has_new=True, num_kv_heads=hk, group=group, head_dim=d,
                            device=torch.device("cuda"), window=(st.sink_eff, 256))
+    clips = (0.96, 0.92) if mode == "write_clip" else (0.0, 0.0)
+    win_kw = dict(stage_mode=STAGE_INVALIDATE) if mode == "invalidate" else dict(
+        stage_mode=STAGE_WRITE, qsl_dev=torch.tensor(c["qsl"], dtype=torch.int32, device="cuda"),
+        seqs_dev=torch.tensor(c["seqs"], dtype=torch.int32, device="cuda"), num_reqs=2, recent_tokens=256,
+        sink_tokens_eff=st.sink_eff)
     store = ops.store_args(dev(c["k"]), dev(c["v"]), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
-                           stage=(sk, sv, own), stage_mode=STAGE_WRITE,
-                           qsl_dev=torch.tensor(c["qsl"], dtype=torch.int32, device="cuda"),
-                           seqs_dev=torch.tensor(c["seqs"], dtype=torch.int32, device="cuda"), num_reqs=2,
-                           recent_tokens=256, sink_tokens_eff=st.sink_eff, query=dev(c["q"]), query_rot=q_rot,
-                           key_rot=k_rot, value_rot=v_rot)
+                           k_clip=clips[0], v_clip=clips[1], stage=(sk, sv, own), query=dev(c["q"]),
+                           query_rot=q_rot, key_rot=k_rot, value_rot=v_rot, **win_kw)
     out, lse = ops.attention_decode(q_rot, k_rot, v_rot, kc, vc, torch.from_numpy(bt).cuda(), plan, c["scale"],
                                     (sk, sv, own), head_dim=d, store=store)
     torch.cuda.synchronize()
-    check(out.cpu().numpy(), lse.cpu().numpy(), ref_o, ref_l, "decode_write over rewritten seats")
+    check(out.cpu().numpy(), lse.cpu().numpy(), ref_o, ref_l, f"decode_write over rewritten seats ({mode})")
     k8, v8 = c["k8"].copy(), c["v8"].copy()
-    store_ref(c["k"], c["v"], k8, v8, slots)
+    if clips[0]:
+        store_ref(clip(c["k"], clips[0]), clip(c["v"], clips[1]), k8, v8, slots)
+    else:
+        store_ref(c["k"], c["v"], k8, v8, slots)
     assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
     assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
     assert np.array_equal(own.cpu().numpy(), post.owner)
