@@ -350,9 +350,9 @@ def config_store(dev, reps=20, layers=4):
 
     def call(r):
         kc, vc, stage = caches[r % layers]
-        ops.store(k, v, kc, vc, sl, head_dim=d, rk=rk, rv=rv, stage=stage, stage_mode=STAGE_WRITE,
-                  qsl_dev=qsl, seqs_dev=seqs, num_reqs=1, recent_tokens=c["recent_tokens"],
-                  sink_tokens_eff=sink_eff)
+        ops.store(k, v, kc, vc, sl, head_dim=d, rk=rk, rv=rv, k_clip=c["k_clip"], v_clip=c["v_clip"],
+                  stage=stage, stage_mode=STAGE_WRITE, qsl_dev=qsl, seqs_dev=seqs, num_reqs=1,
+                  recent_tokens=c["recent_tokens"], sink_tokens_eff=sink_eff)
 
     ms = event_ms(call, reps)
     valid = slots >= 0
@@ -375,6 +375,7 @@ def config_store(dev, reps=20, layers=4):
             "dtype": "bf16 in, f16-MFMA rotation certified against the exact fp32 rotation, int2 out",
             "data": "synthetic",
             "config": {"workload": "config 2: 15360 tokens, 5% -1 slots, 2% rewrites, window write",
+                       "clip": [c["k_clip"], c["v_clip"]],
                        "unique_slots": uniq, "kept_window_seats": kept},
             "roofline": {"bound": "hbm", "kernel": "store_prep_kernel + store_fused_kernel + store_exact_kernel",
                          "achieved": b_alg / t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
