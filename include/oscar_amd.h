@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define OSCAR_ABI_VERSION 2
+#define OSCAR_ABI_VERSION 3
 
 /* element types of dense inputs/outputs */
 enum oscar_dtype { OSCAR_F32 = 0, OSCAR_F16 = 1, OSCAR_BF16 = 2 };
@@ -220,6 +220,15 @@ typedef struct oscar_attn_args_v1 {
                                    2 = merge only (the workspace holds the pass) */
   int32_t q_dtype;              /* OSCAR_BF16 or OSCAR_F16: q, k_new, v_new; history values
                                    are rounded q_dtype(fp16(x)) as the reference does */
+  /* block_table geometry [rows, cols] (streaming_attention.py:48-53): rows >= num_reqs and
+   * cols >= 1 are checked on the host (-22, "Missing request block-table rows").  The
+   * lengths are device data here, so coverage (ceil(history / block_size) <= cols) is
+   * checked by the kernel: an item whose history needs a column past cols reads no
+   * table entry and turns its group's rows into NaN.  The entry points that hold host
+   * lengths (oscar_decode_step_v1, oscar_attn_prefill_v1) reject such a table on the
+   * host with "Block table cannot cover the history". */
+  int64_t block_table_rows;
+  int64_t block_table_cols;
 } oscar_attn_args_v1;
 
 int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
@@ -233,8 +242,13 @@ int oscar_attn_decode_v1(const oscar_attn_args_v1* args, void* stream);
  * (-2, which matches no block): the decode sees the window as the store leaves it.  attn
  * reads the store's rotated outputs (q = store->query_rot, k_new / v_new = key_rot /
  * value_rot).  No counterpart in the reference, whose write (backend.py:249-333)
- * completes before its read (:334-393); bytes, tags, window values and outputs are the
- * same. */
+ * completes before its read (:334-393).  Bytes, tags, window values and outputs are the
+ * same as oscar_store_v1 then oscar_attn_decode_v1 provided that no valid slot of the
+ * store lies inside the history the decode reads (a slot of a page in a request's block
+ * table below its history length): the deferred quantization lands after the split-K
+ * pass has read the old codes.  vLLM's block allocator gives this (a step writes only
+ * the slots of its new tokens, past every history); a caller that rewrites history
+ * slots in the same step calls oscar_store_v1 and oscar_attn_decode_v1 instead. */
 int oscar_decode_write_v1(const oscar_store_args_v1* store, const oscar_attn_args_v1* attn, void* stream);
 
 /* oscar_attn_decode_v1 that allocates nothing and takes no workspace: the item
@@ -276,6 +290,9 @@ typedef struct oscar_prefill_args_v1 {
   int64_t workspace_bytes;
   int32_t q_dtype;              /* OSCAR_BF16 or OSCAR_F16: q, k, v (history values are
                                    rounded q_dtype(fp16(x)) as the reference does) */
+  /* entries of block_table_row: ceil(history / block_size) > block_table_cols is
+   * rejected (-22, "Block table cannot cover the history", streaming_attention.py:48-53) */
+  int64_t block_table_cols;
 } oscar_prefill_args_v1;
 
 int64_t oscar_prefill_workspace_bytes_v1(int64_t history, int64_t num_kv_heads, int64_t head_dim);
@@ -316,7 +333,11 @@ int oscar_prefill_plan_v1(int64_t history, int64_t num_tokens, int64_t num_q_hea
  *
  * The context holds a ring of pinned host and device metadata slots, reused once the
  * event recorded after the slot's last reader has completed; one per device, created
- * once (it allocates), used from any thread. */
+ * once (it allocates), used from any thread.  The step is eager-only: it builds the plan
+ * on the host at every call, copies it from a ring slot that a later call rewrites, and
+ * may wait on a ring event, so it must not be captured into a HIP graph (it returns -22
+ * while `stream` is capturing).  Graph capture works with oscar_store_v1 and with
+ * oscar_attn_decode_v1 / oscar_decode_write_v1 over a plan uploaded beforehand. */
 typedef struct oscar_context_v1 oscar_context_v1;
 int oscar_context_create_v1(int32_t device, oscar_context_v1** ctx);
 int oscar_context_destroy_v1(oscar_context_v1* ctx);
@@ -361,6 +382,12 @@ typedef struct oscar_step_args_v1 {
   void* workspace;
   int64_t workspace_bytes;
   int64_t workspace_needed;     /* out: bytes this call needed (set when it returns -28) */
+  /* block_table geometry [rows, cols], checked on the host before anything is enqueued
+   * (streaming_attention.py:48-53): rows < num_reqs -> -22 "Missing request block-table
+   * rows"; a request with queries whose history (seq - its query count with key / value,
+   * else seq) needs more than cols pages -> -22 "Block table cannot cover the history" */
+  int64_t block_table_rows;
+  int64_t block_table_cols;
 } oscar_step_args_v1;
 
 int64_t oscar_step_workspace_bytes_v1(int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,

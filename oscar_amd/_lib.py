@@ -15,7 +15,7 @@ OSCAR_F32, OSCAR_F16, OSCAR_BF16 = 0, 1, 2
 STAGE_NONE, STAGE_INVALIDATE, STAGE_WRITE = 0, 1, 2
 WORK_INTS = 8
 GROUP_INTS = 8
-ABI_VERSION = 2
+ABI_VERSION = 3
 DECODE_STATIC_MAX_ITEMS = 512
 
 vp = C.c_void_p
@@ -69,6 +69,7 @@ class AttnArgs(C.Structure):
         ("items", vp), ("num_items", i32), ("groups", vp), ("num_groups", i32),
         ("workspace", vp), ("workspace_bytes", i64), ("max_group_items", i32),
         ("out_rot", vp), ("lse", vp), ("phases", i32), ("q_dtype", i32),
+        ("block_table_rows", i64), ("block_table_cols", i64),
     ]
 
 
@@ -79,7 +80,7 @@ class PrefillArgs(C.Structure):
         ("history", i64), ("cache", Cache), ("block_table_row", vp),
         ("staging", C.POINTER(Staging)), ("scale", f32), ("out", vp),
         ("out_stride_token", i64), ("lse", vp), ("workspace", vp), ("workspace_bytes", i64),
-        ("q_dtype", i32),
+        ("q_dtype", i32), ("block_table_cols", i64),
     ]
 
 
@@ -95,6 +96,7 @@ class StepArgs(C.Structure):
         ("slot_claims", vp), ("seat_claims", vp), ("epoch_counter", vp),
         ("store_workspace", vp), ("store_workspace_bytes", i64), ("arrivals", vp),
         ("workspace", vp), ("workspace_bytes", i64), ("workspace_needed", i64),
+        ("block_table_rows", i64), ("block_table_cols", i64),
     ]
 
 
@@ -150,7 +152,14 @@ def load() -> C.CDLL:
     return lib
 
 
+EINVAL = -22
+
+
 def check(status: int, what: str) -> None:
+    """Raise for a nonzero status: ValueError for rejected arguments (-22, where the
+    reference's own checks raise ValueError, e.g. streaming_attention.py:32-65),
+    RuntimeError for anything else (launch or allocation failures)."""
     if status != 0:
         msg = load().oscar_last_error().decode(errors="replace")
-        raise RuntimeError(f"{what} failed ({status}): {msg}")
+        cls = ValueError if status == EINVAL else RuntimeError
+        raise cls(f"{what} failed ({status}): {msg}")

@@ -338,6 +338,8 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         has_new = key is not None
         if has_new and self._oscar.window_enabled:
             self._ensure_staging(layer, kv_cache)
+        stream = torch.cuda.current_stream(query.device).cuda_stream
+        scratch = ops.DeviceScratch.get(query.device, stream)
         a = self._step_args(layer, query.device, query.dtype)
         if a is None:
             return False
@@ -354,7 +356,7 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             window = self._stage(layer) is not None
             a.stage_mode = STAGE_WRITE if window else (
                 STAGE_INVALIDATE if getattr(layer, "_oscar_stage_ready", False) else STAGE_NONE)
-            ws = ops.DeviceScratch.get(query.device).store_workspace(
+            ws = scratch.store_workspace(
                 _lib.load().oscar_store_workspace_bytes_v1(n, hk, d))
             a.store_workspace, a.store_workspace_bytes = ws.data_ptr(), ws.numel()
         else:
@@ -362,13 +364,16 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         table = _block_tables(md)
         if table.dtype != torch.int32 or table.stride(-1) != 1 or table.device != query.device:
             table = table.to(device=query.device, dtype=torch.int32).contiguous()
+        if table.ndim != 2:
+            raise ValueError("Missing request block-table rows")
         a.block_table, a.block_table_stride = table.data_ptr(), table.stride(0)
+        a.block_table_rows, a.block_table_cols = table.shape
         a.host_query_start_loc, a.host_seq_lens = _address(qsl), _address(seqs)
         a.num_reqs = len(qsl) - 1
         ctx = ops.DeviceContext.get(query.device)
-        ws = ctx.step_workspace(0)  # shared by every layer of the device: current buffer
+        ws = scratch.step_workspace(0)  # shared by every layer: the stream's current buffer
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        rc = ops.decode_step(ctx, a, torch.cuda.current_stream(query.device).cuda_stream)
+        rc = ops.decode_step(ctx, a, stream, scratch)
         if rc != 0:
             return False
         if n < query.shape[0]:

@@ -9,6 +9,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -33,14 +34,18 @@ def build(verbose: bool = False) -> Path:
     """Compile each source to an object in oscar_amd/_build/, then link the .so."""
     out_dir = HERE / "_build"
     out_dir.mkdir(exist_ok=True)
-    objs = []
+    cmds, objs = [], []
     for src in sources():
         obj = out_dir / (src.stem + ".o")
         cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
             cmd[1:1] = ["-x", "hip"]
-        _run(cmd, verbose)
+        cmds.append(cmd)
         objs.append(str(obj))
+    # the sources compile independently: at most one compiler process per source
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)

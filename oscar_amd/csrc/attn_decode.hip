@@ -269,12 +269,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   const int bs = (int)A.cache.block_size;  // a multiple of 32
   const int64_t hk = A.cache.num_kv_heads;
   if (part < 0 || part >= A.num_items) return;
-  // an item that breaks oscar_attn_plan_v1's rules poisons its partial (NaN LSE, so
-  // the merged rows are NaN) instead of reading out of bounds
+  // an item that breaks oscar_attn_plan_v1's rules, or whose history needs a block-table
+  // column past block_table_cols, poisons its partial (NaN LSE, so the merged rows are
+  // NaN) instead of reading out of bounds
   if (req < 0 || req >= A.num_reqs || kvh >= hk || nq < 1 || nrows > 32 || hist < 0 || off < 0 ||
       cur0 < 0 || qa + nq > A.num_tokens || first < 0 || stride < 1 || count < 0 ||
       count > kMaxItemTokens / kTile ||
-      (count > 0 && (first + (int64_t)stride * (count - 1)) * kTile >= seq)) {
+      (count > 0 && (first + (int64_t)stride * (count - 1)) * kTile >= seq) ||
+      (hist > 0 && (hist - 1) / bs >= A.block_table_cols)) {
     if (tid < 32) P.part_lse[(int64_t)part * 32 + tid] = NAN;
     return;
   }
@@ -336,8 +338,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   }
   __builtin_amdgcn_sched_barrier(0);  // keep round 1 ahead of round 2
   if (lane < my) {
-    // ids outside the cache are clamped (the host validates tables; this keeps a
-    // bad table from faulting)
+    // ids outside the cache are clamped (a table entry may hold any value; this keeps
+    // a bad one from faulting)
     wblk = (wblk < 0 || wblk >= A.cache.num_blocks) ? 0 : wblk;
     wseat = P.has_stage ? (int)((unsigned)wblk % st_rows) * bs : 0;
   }
@@ -1315,23 +1317,20 @@ extern "C" int oscar_attn_plan_v1(const int32_t* qsl, const int32_t* seqs, int32
 
 namespace {
 
-// Argument checks shared by both decode entry points; `name` prefixes the messages.
-// `partials` / `partial_bytes`: where the item partials go and how much room there is.
-// `store` (oscar_decode_write_v1): the store enqueued once the decode's arguments have
-// passed, deferred (its quantization in the merge launch) when it is a small call.
-int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials, int64_t partial_bytes,
-                   hipStream_t s, const oscar_store_args_v1* store = nullptr) {
+// Argument checks of a non-empty plan that do not depend on where the item partials
+// go; `name` prefixes the messages.
+int check_args(const oscar_attn_args_v1& a, const char* name) {
   const int64_t D = a.cache.head_dim;
   if (D != 128 && D != 256) return fail(-22, "%s: head_dim %lld unsupported", name, (long long)D);
-  if (a.num_items <= 0 || a.num_groups <= 0) {
-    StoreParams sp{};
-    return store != nullptr ? store_launch(store, s, false, name, &sp) : 0;
-  }
-  if (!a.q || !a.items || !a.groups || !partials || !a.out_rot || !a.lse || !a.block_table ||
-      !a.query_start_loc || !a.seq_lens)
+  if (!a.q || !a.items || !a.groups || !a.out_rot || !a.lse || !a.block_table || !a.query_start_loc ||
+      !a.seq_lens)
     return fail(-22, "%s: missing pointer", name);
   if ((a.k_new == nullptr) != (a.v_new == nullptr))
     return fail(-22, "%s: both new K and V must be supplied together", name);
+  // streaming_attention.py:48-50; the coverage of each history (:51-53) is checked by the
+  // kernel, which holds the lengths
+  if (a.block_table_rows < a.num_reqs || a.block_table_cols < 1 || a.block_table_stride < a.block_table_cols)
+    return fail(-22, "%s: Missing request block-table rows", name);
   if (a.phases < 0 || a.phases > 2) return fail(-22, "%s: phases must be 0, 1 or 2", name);
   if (a.q_dtype != OSCAR_BF16 && a.q_dtype != OSCAR_F16)
     return fail(-22, "%s: q_dtype must be OSCAR_BF16 or OSCAR_F16", name);
@@ -1351,12 +1350,29 @@ int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials
   if (a.staging && (a.staging->rows < 1 || a.staging->rows * a.cache.block_size >= (1ll << 31) ||
                     (((uintptr_t)a.staging->stage_k) & 15) || (((uintptr_t)a.staging->stage_v) & 15)))
     return fail(-22, "%s: staging arena rows out of range or unaligned", name);
+  if (a.max_group_items < 0 || a.max_group_items > a.num_items)
+    return fail(-22, "%s: max_group_items out of range", name);
+  return 0;
+}
+
+// The decode entry points after their own checks.  `partials` / `partial_bytes`: where
+// the item partials go and how much room there is.  `store` (oscar_decode_write_v1): the
+// store enqueued once the decode's arguments have passed, deferred (its quantization in
+// the merge launch) when it is a small call.
+int launch_checked(const oscar_attn_args_v1& a, const char* name, void* partials, int64_t partial_bytes,
+                   hipStream_t s, const oscar_store_args_v1* store = nullptr) {
+  const int64_t D = a.cache.head_dim;
+  if (D != 128 && D != 256) return fail(-22, "%s: head_dim %lld unsupported", name, (long long)D);
+  if (a.num_items <= 0 || a.num_groups <= 0) {
+    StoreParams sp{};
+    return store != nullptr ? store_launch(store, s, false, name, &sp) : 0;
+  }
+  if (const int rc = check_args(a, name)) return rc;
+  if (!partials) return fail(-22, "%s: missing workspace", name);
   const int64_t need = (int64_t)a.num_items * 32 * (D + 1) * (int64_t)sizeof(float);
   if (partial_bytes < need)
     return fail(-22, "%s: workspace of %lld bytes < %lld for %d items", name, (long long)partial_bytes,
                 (long long)need, a.num_items);
-  if (a.max_group_items < 0 || a.max_group_items > a.num_items)
-    return fail(-22, "%s: max_group_items out of range", name);
   AttnParams p{};
   p.a = a;
   p.has_stage = a.staging != nullptr;
@@ -1429,6 +1445,7 @@ extern "C" int oscar_attn_decode_static_v1(const oscar_attn_args_v1* args, void*
     return fail(-22, "oscar_attn_decode_static_v1: %d items exceed the static scratch (at most %d)",
                 args->num_items, OSCAR_DECODE_STATIC_MAX_ITEMS);
   if (args->num_items <= 0 || args->num_groups <= 0) return 0;
+  if (const int rc = check_args(*args, "oscar_attn_decode_static_v1")) return rc;
   void* partials = nullptr;
   const int rc = static_partials((hipStream_t)stream, &partials);
   if (rc != 0) return rc;

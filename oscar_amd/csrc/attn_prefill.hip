@@ -577,8 +577,12 @@ extern "C" int oscar_attn_prefill_v1(const oscar_prefill_args_v1* args, void* st
   const int G = (int)(a.num_q_heads / a.num_kv_heads);
   if (G > kRows) return fail(-22, "oscar_attn_prefill_v1: more than %d query heads per KV head", kRows);
   if (a.history < 0) return fail(-22, "oscar_attn_prefill_v1: negative history");
-  if (a.history > 0 && (!a.cache.k || !a.cache.v || !a.block_table_row || a.cache.head_dim != D))
+  if (a.history > 0 && (!a.cache.k || !a.cache.v || !a.block_table_row || a.cache.head_dim != D ||
+                        a.cache.block_size < 1))
     return fail(-22, "oscar_attn_prefill_v1: history needs the cache and the block-table row");
+  // streaming_attention.py:51-53
+  if (a.history > 0 && (a.history + a.cache.block_size - 1) / a.cache.block_size > a.block_table_cols)
+    return fail(-22, "oscar_attn_prefill_v1: Block table cannot cover the history");
   // q/k/v rows and the history workspace are read as 16-byte vectors
   if ((((uintptr_t)a.q) & 15) || (((uintptr_t)a.k) & 15) || (((uintptr_t)a.v) & 15) ||
       ((a.q_stride_token * 2) & 15) || ((a.kv_stride_token * 2) & 15))

@@ -125,24 +125,45 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
   if (has_new && !a.slot_mapping) return fail(-22, "oscar_decode_step_v1: slot_mapping required with new K/V");
   const int G = (int)(hq / hk);
   if (G > 32) return OSCAR_STEP_NOT_DECODE;  // no 32-row tile holds one token's heads
+  const int64_t bs = a.cache.block_size;
+  if (bs < 1) return fail(-22, "oscar_decode_step_v1: invalid cache geometry");
+  // streaming_attention.py:48-65: table rows for every request, a staging arena of at
+  // least one row
+  if (a.block_table_rows < B || a.block_table_cols < 1)
+    return fail(-22, "Missing request block-table rows");
+  if (a.staging != nullptr && a.staging->rows < 1) return fail(-22, "Invalid streaming staging geometry");
   // ---- classify: every request decode-shaped, the requests tile [0, n)
   const int32_t* qsl = a.host_query_start_loc;
   const int32_t* seqs = a.host_seq_lens;
   auto clip = [&](int64_t x) { return x < n ? x : n; };
-  if (qsl[0] != 0 || clip(qsl[B]) != n) return OSCAR_STEP_NOT_DECODE;
   for (int r = 0; r < B; ++r) {
     const int64_t q0 = clip(qsl[r]), q1 = clip(qsl[r + 1]);
     if (q1 < q0) return fail(-22, "oscar_decode_step_v1: query_start_loc must be non-decreasing");
+    if (seqs[r] < 0) return fail(-22, "oscar_decode_step_v1: negative sequence length");
     const int64_t nq = q1 - q0;
+    if (nq == 0) continue;
+    if (has_new && seqs[r] < nq) return fail(-22, "oscar_decode_step_v1: sequence length must cover its query chunk");
+    // the pages of the history this request reads through the table
+    const int64_t hist = has_new ? seqs[r] - nq : seqs[r];
+    if ((hist + bs - 1) / bs > a.block_table_cols) return fail(-22, "Block table cannot cover the history");
+  }
+  if (qsl[0] != 0 || clip(qsl[B]) != n) return OSCAR_STEP_NOT_DECODE;
+  for (int r = 0; r < B; ++r) {
+    const int64_t nq = clip(qsl[r + 1]) - clip(qsl[r]);
     if (nq == 0) continue;
     // chunks of more than 32 rows per KV head run as sub-requests, up to kMaxSplitRows
     if (has_new && nq * G > kMaxSplitRows) return OSCAR_STEP_NOT_DECODE;
     if (has_new && seqs[r] == nq) return OSCAR_STEP_NOT_DECODE;  // history-free: prefill
-    if (has_new && seqs[r] < nq) return fail(-22, "oscar_decode_step_v1: sequence length must cover its query chunk");
-    if (seqs[r] < 0) return fail(-22, "oscar_decode_step_v1: negative sequence length");
   }
-  // ---- ring slot (wait only if the slot's previous call has not finished reading it)
   hipStream_t s = (hipStream_t)stream;
+  // the plan is built on the host at every call and copied from a ring slot that later
+  // calls rewrite: a captured copy would replay stale metadata
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess)
+    return fail(-5, "oscar_decode_step_v1: cannot query the stream's capture status");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(-22, "oscar_decode_step_v1: eager only (the stream is capturing a graph)");
+  // ---- ring slot (wait only if the slot's previous call has not finished reading it)
   std::unique_lock<std::mutex> lock(ctx->mu);
   const int slot = ctx->next;
   ctx->next = (ctx->next + 1) % kRingSlots;
@@ -254,6 +275,8 @@ extern "C" int oscar_decode_step_v1(oscar_context_v1* ctx, oscar_step_args_v1* a
     at.cache = a.cache;
     at.block_table = a.block_table;
     at.block_table_stride = a.block_table_stride;
+    at.block_table_rows = a.block_table_rows;
+    at.block_table_cols = a.block_table_cols;
     at.query_start_loc = d_qsl;
     at.seq_lens = d_seqs;
     at.num_reqs = B;

@@ -100,12 +100,17 @@ def upload(parts, device) -> list:
 
 
 class DeviceScratch:
-    """Per-device scratch: last-writer claim tables and growable workspaces."""
+    """Scratch of one (device, stream): last-writer claim tables, the claim epoch, the
+    small store's arrival counters and the growable workspaces of the store, the decode,
+    the prefill and the native step.  Work enqueued on different streams gets different
+    scratch, so concurrent calls never share these buffers (each is allocated while its
+    stream is current, so torch's allocator orders its reuse on that stream)."""
 
     _by_device: dict = {}
 
     def __init__(self, device: torch.device):
         self.device = device
+        self.step_ws = torch.empty(0, dtype=torch.uint8, device=device)
         # claim epoch lives on the device so that captured graphs replay with fresh epochs
         self.epoch_counter = torch.zeros(2, dtype=torch.int64, device=device)
         self.slot_claims = torch.zeros(0, dtype=torch.int64, device=device)
@@ -116,10 +121,15 @@ class DeviceScratch:
         self.prefill_ws = torch.empty(0, dtype=torch.uint8, device=device)
 
     @classmethod
-    def get(cls, device: torch.device) -> "DeviceScratch":
-        key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    def get(cls, device: torch.device, stream: int | None = None) -> "DeviceScratch":
+        """The scratch of `device` for `stream` (a raw HIP stream handle; default: the
+        device's current stream, the one the caller's work goes to)."""
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        if stream is None:
+            stream = torch.cuda.current_stream(index).cuda_stream
+        key = (index, stream)
         if key not in cls._by_device:
-            cls._by_device[key] = cls(torch.device("cuda", key[1]))
+            cls._by_device[key] = cls(torch.device("cuda", index))
         return cls._by_device[key]
 
     def claims(self, slots: int, seats: int):
@@ -156,10 +166,19 @@ class DeviceScratch:
             self.attn_ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self.attn_ws
 
+    def step_workspace(self, nbytes: int) -> torch.Tensor:
+        """The native decode step's workspace (rotated q / k / v, out_rot, LSE, item
+        partials)."""
+        if self.step_ws.numel() < nbytes:
+            self.step_ws = torch.empty(max(nbytes, 4 << 20), dtype=torch.uint8, device=self.device)
+        return self.step_ws
+
 
 class DeviceContext:
     """The library's native context for one device (pinned + device metadata ring of the
-    decode step), created once per device and destroyed with the process."""
+    decode step, safe to share between streams: a ring slot is reused once the event
+    recorded after its last reader has completed), created once per device and
+    destroyed with the process."""
 
     _by_device: dict = {}
 
@@ -169,7 +188,6 @@ class DeviceContext:
         _lib.check(lib.oscar_context_create_v1(index, C.byref(ptr)), "oscar_context_create_v1")
         self.ptr = ptr
         self.index = index
-        self.step_ws = None
 
     @classmethod
     def get(cls, device: torch.device) -> "DeviceContext":
@@ -179,20 +197,14 @@ class DeviceContext:
             ctx = cls._by_device[index] = cls(index)
         return ctx
 
-    def step_workspace(self, nbytes: int) -> torch.Tensor:
-        if self.step_ws is None or self.step_ws.numel() < nbytes:
-            self.step_ws = torch.empty(max(nbytes, 4 << 20), dtype=torch.uint8,
-                                       device=torch.device("cuda", self.index))
-        return self.step_ws
 
-
-def decode_step(ctx: DeviceContext, args: "_lib.StepArgs", stream: int) -> int:
-    """oscar_decode_step_v1; grows the step workspace and retries once when it is too
-    small.  Returns 0, or STEP_NOT_DECODE when the batch needs the general path."""
+def decode_step(ctx: DeviceContext, args: "_lib.StepArgs", stream: int, scratch: DeviceScratch) -> int:
+    """oscar_decode_step_v1; grows the stream's step workspace and retries once when it
+    is too small.  Returns 0, or STEP_NOT_DECODE when the batch needs the general path."""
     lib = _lib.load()
     rc = lib.oscar_decode_step_v1(ctx.ptr, C.byref(args), C.c_void_p(stream))
     if rc == -28 and args.workspace_needed > args.workspace_bytes:
-        ws = ctx.step_workspace(args.workspace_needed)
+        ws = scratch.step_workspace(args.workspace_needed)
         args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
         rc = lib.oscar_decode_step_v1(ctx.ptr, C.byref(args), C.c_void_p(stream))
     if rc < 0:
@@ -444,6 +456,7 @@ def attention_decode(q, k_new, v_new, k_cache, v_cache, block_table, plan: Decod
         a.k_new, a.v_new, a.kv_new_stride_token = k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0)
     a.cache = cache_struct(k_cache, v_cache, head_dim)
     a.block_table, a.block_table_stride = table.data_ptr(), table.stride(0)
+    a.block_table_rows, a.block_table_cols = table.shape
     a.query_start_loc, a.seq_lens, a.num_reqs = plan.qsl.data_ptr(), plan.seqs.data_ptr(), plan.seqs.numel()
     if st is not None:
         a.staging = C.pointer(st)
@@ -499,7 +512,7 @@ def attention_prefill(q, k, v, scale, *, head_dim, history=0, k_cache=None, v_ca
         if math.ceil(history / k_cache.shape[1]) > row.numel():
             raise ValueError("Block table cannot cover the history")
         keep.append(row)
-        a.block_table_row = row.data_ptr()
+        a.block_table_row, a.block_table_cols = row.data_ptr(), row.numel()
         st = staging_struct(stage, k_cache, head_dim)
         if st is not None:
             keep.append(st)

@@ -342,9 +342,101 @@ def decode_args(**kw):
         a.cache.k_stride[i] = a.cache.v_stride[i] = st
     a.workspace_bytes = 4 * 32 * 257 * 4
     a.max_group_items = 4
+    a.block_table_rows, a.block_table_cols = 1, 16
     for k, v in kw.items():
         setattr(a, k, v)
     return a
+
+
+def test_decode_rejects_a_table_with_missing_rows_or_columns(lib):
+    """streaming_attention.py:48-50: the table needs a row per request and at least one
+    column (its stride at least its width); checked before anything is launched."""
+    for kw in (dict(block_table_rows=0), dict(block_table_cols=0), dict(block_table_cols=17),
+               dict(num_reqs=2, block_table_rows=1)):
+        a = decode_args(**kw)
+        for entry in ("oscar_attn_decode_v1", "oscar_attn_decode_static_v1"):
+            assert getattr(lib, entry)(C.byref(a), None) == -22, (kw, entry)
+            assert b"Missing request block-table rows" in lib.oscar_last_error()
+        assert lib.oscar_decode_write_v1(C.byref(_lib.StoreArgs(num_tokens=0)), C.byref(a), None) == -22
+
+
+def test_table_coverage_check_matches_the_reference_rule():
+    """The decode kernel's per-item guard `hist > 0 && (hist - 1) / bs >= cols` (an item
+    that fails it reads no table entry and poisons its rows) is the reference's
+    `ceil(prefix / bs) > cols` (streaming_attention.py:51-53) for every history length."""
+    for bs in (32, 128, 1536):
+        for cols in range(0, 6):
+            for hist in range(0, 7 * bs + 2):
+                assert (hist > 0 and (hist - 1) // bs >= cols) == (-(-hist // bs) > cols)
+
+
+def prefill_args(**kw):
+    """Continuation prefill arguments that pass every host check up to the table
+    coverage (placeholder device addresses; nothing is launched)."""
+    a = _lib.PrefillArgs(q=0x10000, q_stride_token=1536, k=0x20000, v=0x30000, kv_stride_token=256,
+                         num_tokens=8, num_q_heads=6, num_kv_heads=1, head_dim=256, history=1000,
+                         block_table_row=0x40000, scale=0.0625, out=0x50000, out_stride_token=1536,
+                         workspace=0x100000, workspace_bytes=1 << 30, q_dtype=_lib.OSCAR_BF16)
+    a.cache.k, a.cache.v = 0x100000, 0x200000
+    a.cache.num_blocks, a.cache.block_size, a.cache.num_kv_heads, a.cache.head_dim = 8, 128, 1, 256
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_prefill_rejects_a_table_row_that_cannot_cover_the_history(lib):
+    for history, cols in ((1000, 7), (129, 1), (1, 0)):
+        a = prefill_args(history=history, block_table_cols=cols)
+        assert lib.oscar_attn_prefill_v1(C.byref(a), None) == -22
+        assert b"Block table cannot cover the history" in lib.oscar_last_error()
+
+
+def step_args(qsl, seqs, has_new=True, rows=None, cols=16, staging_rows=None):
+    """Native-step arguments with host metadata; device fields are placeholders.  The
+    calls below are rejected by the host checks before the context or the stream is
+    touched."""
+    a = _lib.StepArgs(query=0x10000, num_tokens=qsl[-1], num_q_heads=6, q_dtype=_lib.OSCAR_BF16,
+                      block_table=0x20000, block_table_stride=cols, rk=0x30000, rv=0x40000,
+                      output=0x50000, workspace=0x60000, workspace_bytes=1 << 20)
+    if has_new:
+        a.key, a.value, a.kv_stride_token, a.slot_mapping = 0x70000, 0x80000, 256, 0x90000
+    a.cache.k, a.cache.v = 0x100000, 0x200000
+    a.cache.num_blocks, a.cache.block_size, a.cache.num_kv_heads, a.cache.head_dim = 64, 128, 1, 256
+    keep = [(C.c_int32 * len(qsl))(*qsl), (C.c_int32 * len(seqs))(*seqs)]
+    a.host_query_start_loc = C.cast(keep[0], C.c_void_p)
+    a.host_seq_lens = C.cast(keep[1], C.c_void_p)
+    a.num_reqs = len(seqs)
+    a.block_table_rows = len(seqs) if rows is None else rows
+    a.block_table_cols = cols
+    if staging_rows is not None:
+        st = _lib.Staging(stage_k=0xA0000, stage_v=0xB0000, owner=0xC0000, rows=staging_rows)
+        keep.append(st)
+        a.staging = C.pointer(st)
+    return a, keep
+
+
+def test_native_step_rejects_what_the_reference_rejects(lib):
+    """oscar_decode_step_v1 raises where streaming_attention.py:48-65 raises: a missing
+    table row, a history whose pages outnumber the table's columns (the history is
+    seq minus the chunk with new K/V, seq without), an empty staging arena."""
+    ctx = (C.c_uint8 * 4096)()  # never dereferenced: every call below fails its host checks
+    cases = [
+        (dict(qsl=[0, 4, 8], seqs=[1000, 1000], rows=1), b"Missing request block-table rows"),
+        (dict(qsl=[0, 4, 8], seqs=[1000, 1000], cols=0), b"Missing request block-table rows"),
+        # 2052 - 4 = 2048 history tokens fill exactly 16 pages; 2053 - 4 needs 17
+        (dict(qsl=[0, 4, 8], seqs=[2052, 2053]), b"Block table cannot cover the history"),
+        (dict(qsl=[0, 1, 2], seqs=[2048, 2049], has_new=False), b"Block table cannot cover the history"),
+        (dict(qsl=[0, 4], seqs=[1000], staging_rows=0), b"Invalid streaming staging geometry"),
+    ]
+    for kw, msg in cases:
+        a, keep = step_args(**kw)
+        assert lib.oscar_decode_step_v1(C.cast(ctx, C.c_void_p), C.byref(a), None) == -22, kw
+        assert msg in lib.oscar_last_error(), (kw, lib.oscar_last_error())
+    # a request without queries in this batch reads nothing, whatever its length
+    a, keep = step_args(qsl=[0, 4, 4], seqs=[1000, 99999], rows=2)
+    a.block_table_rows = 1
+    assert lib.oscar_decode_step_v1(C.cast(ctx, C.c_void_p), C.byref(a), None) == -22
+    assert b"Missing request block-table rows" in lib.oscar_last_error()
 
 
 def test_decode_rejects_a_workspace_smaller_than_the_plan_needs(lib):

@@ -194,3 +194,59 @@ def test_native_step_reads_host_metadata_in_the_accessor_order():
     assert list(qsl) == [0, 4, 5] and seqs.dtype == torch.int32 and seqs.tolist() == [9, 8]
     # device-only metadata: the native step is skipped (reading it would synchronise)
     assert host_metadata_arrays(NS(query_start_loc=torch.tensor([0, 1]), seq_lens=torch.tensor([3]))) is None
+
+
+def _plan(qsl, seqs, has_new):
+    import numpy as np
+
+    from oscar_amd.ops import DecodePlan
+
+    return DecodePlan(np.zeros(0, np.int32), np.zeros(0, np.int32), list(qsl), list(seqs), has_new,
+                      0, 0, 0, 0)
+
+
+def test_general_path_table_check_raises_like_the_reference():
+    """ops._check_table restates streaming_attention.py:48-53: a row per request, and
+    ceil(history / block_size) columns where the history is seq minus the chunk when
+    new K/V come with the queries (seq alone otherwise); requests without queries in
+    the batch read nothing."""
+    from oscar_amd.ops import _check_table
+
+    table = torch.zeros(2, 16, dtype=torch.int32)
+    _check_table(table, _plan([0, 4, 8], [2052, 2052], True), 128)      # 2048 = 16 pages
+    _check_table(table, _plan([0, 4, 4], [2052, 99999], True), 128)     # second request idle
+    _check_table(table, _plan([0, 1, 2], [2048, 1], False), 128)
+    with pytest.raises(ValueError, match="Block table cannot cover the history"):
+        _check_table(table, _plan([0, 4, 8], [2052, 2053], True), 128)
+    with pytest.raises(ValueError, match="Block table cannot cover the history"):
+        _check_table(table, _plan([0, 1, 2], [2049, 1], False), 128)
+    with pytest.raises(ValueError, match="Missing request block-table rows"):
+        _check_table(table[:1], _plan([0, 4, 8], [100, 100], True), 128)
+    with pytest.raises(ValueError, match="Missing request block-table rows"):
+        _check_table(table[0], _plan([0, 4], [100], True), 128)
+
+
+def test_staging_struct_checks_the_arena_against_the_cache():
+    """ops.staging_struct restates streaming_attention.py:55-65: owner [rows, bs], values
+    [rows, bs, Hk, D] fp32, rows >= 1, all contiguous."""
+    from oscar_amd.ops import staging_struct
+
+    kc = torch.zeros(8, 32, 2, 64, dtype=torch.int8)
+    good = (torch.zeros(4, 32, 2, 64), torch.zeros(4, 32, 2, 64), torch.full((4, 32), -1, dtype=torch.int64))
+    assert staging_struct(good, kc, 64).rows == 4
+    assert staging_struct(None, kc, 64) is None
+    bad = {
+        "rows": (torch.zeros(0, 32, 2, 64), torch.zeros(0, 32, 2, 64), torch.zeros(0, 32, dtype=torch.int64)),
+        "block size": (torch.zeros(4, 16, 2, 64), torch.zeros(4, 16, 2, 64), torch.zeros(4, 16, dtype=torch.int64)),
+        "heads": (torch.zeros(4, 32, 1, 64), torch.zeros(4, 32, 1, 64), good[2]),
+        "head_dim": (torch.zeros(4, 32, 2, 32), good[1], good[2]),
+        "owner rows": (good[0], good[1], torch.zeros(3, 32, dtype=torch.int64)),
+        "v shape": (good[0], torch.zeros(4, 32, 2, 65), good[2]),
+    }
+    for what, stage in bad.items():
+        with pytest.raises(ValueError, match="Invalid streaming staging geometry"):
+            staging_struct(stage, kc, 64)
+    with pytest.raises(ValueError, match="contiguous"):
+        staging_struct((good[0].transpose(0, 1), good[1], good[2]), kc, 64)
+    with pytest.raises(ValueError, match="fp32"):
+        staging_struct((good[0].half(), good[1], good[2]), kc, 64)

@@ -68,7 +68,7 @@ def test_arena_rows_and_layer_bytes():
     assert integ.arena_rows(cfg, 128) == 0 + (2 + 1) + 2     # sink pages 0, recent 2 + 1, 2 spare
     assert integ.arena_rows(cfg, 32) == 2 + (8 + 1) + 2
     cfg = OscarConfig()
-    per_seat = 2 * 1 * 256 * 4 + 16
+    per_seat = 2 * 1 * 256 * 4 + 8  # fp32 K and V values, int64 owner tag
     assert integ.layer_fixed_bytes(cfg, 1, 256, 128) == 2 * 256 * 256 * 4 + 64 * 128 * per_seat
     cfg.sink_tokens = cfg.recent_tokens = 0  # window off
     assert integ.layer_fixed_bytes(cfg, 1, 256, 128) == 2 * 256 * 256 * 4
@@ -183,6 +183,34 @@ def test_mtp_shadow_pool_replaces_an_int8_pool_once():
     other.forward(None, None, None, None, bf16, None)
     assert seen[-1] is bf16  # a bf16 pool goes through unchanged
     assert not is_shadow_impl(Native())
+    assert not hasattr(impl, "do_kv_cache_update")  # only where the native class has it
+
+
+def test_mtp_shadow_pool_keeps_a_stacked_pool_stacked_and_covers_kv_updates():
+    """A stacked [2, ...] int8 pool gets a stacked bf16 twin (a native impl may unbind
+    it), and do_kv_cache_update writes the draft's K/V into the twin, never the pool."""
+    class Native:
+        def forward(self, layer, query, key, value, kv_cache, attn_metadata, *args, **kwargs):
+            return kv_cache
+
+        def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
+            k_cache, v_cache = kv_cache.unbind(0)
+            k_cache.view(-1, *key.shape[1:])[slot_mapping] = key
+            v_cache.view(-1, *value.shape[1:])[slot_mapping] = value
+
+    impl = Native()
+    install_shadow(impl)
+    pool = torch.zeros(2, 3, 4, 1, 8, dtype=torch.int8)
+    twin = impl.forward(None, None, None, None, pool, None)
+    assert isinstance(twin, torch.Tensor) and twin.shape == pool.shape and twin.dtype == torch.bfloat16
+    key = torch.full((2, 1, 8), 1.5, dtype=torch.bfloat16)
+    impl.do_kv_cache_update(None, key, -key, pool, torch.tensor([1, 6]))
+    assert not pool.any()  # the int8 pool is untouched
+    flat = twin.view(2, -1, 1, 8)
+    assert (flat[0, [1, 6]] == 1.5).all() and (flat[1, [1, 6]] == -1.5).all() and flat[0, 0].eq(0).all()
+    assert impl.forward(None, None, None, None, pool, None) is twin  # allocated once
+    with pytest.raises(ValueError):
+        impl.forward(None, None, None, None, torch.zeros(3, 4, 1, 8, dtype=torch.int8), None)
 
 
 def test_plugin_surgery_routes_full_layers_to_oscar_and_drafts_to_the_shadow(monkeypatch):
