@@ -74,22 +74,31 @@ def attention_ref(q, k_new, v_new, k8, v8, bt, qsl, seqs, scale, stage=None, *,
         else:
             keys, vals = k_hist, v_hist
         keys64, vals64 = keys.astype(np.float64), vals.astype(np.float64)
-        for i in range(n_q):
-            visible = seq - n_q + i + 1
-            if visible <= 0 or (wanted is not None and a + i not in wanted):
-                continue
-            for h in range(hq):
-                kv = h // group
-                s = keys64[:visible, kv] @ q[a + i, h].astype(np.float64) * scale
-                m = np.max(s)
-                if np.isnan(m):
-                    out[a + i, h] = np.nan
-                    lse[a + i, h] = np.nan
-                    continue
-                p = np.exp(s - m)
-                tot = p.sum()
-                out[a + i, h] = (p @ vals64[:visible, kv]) / tot
-                lse[a + i, h] = m + np.log(tot)
+        # query i sees the first seq - n_q + i + 1 keys; rows are evaluated in blocks,
+        # each head group of a KV head at once: S = Q K^T over the block's longest
+        # visible prefix, keys past a row's own prefix masked to -inf
+        idx = [i for i in range(n_q) if seq - n_q + i + 1 > 0 and (wanted is None or a + i in wanted)]
+        for c0 in range(0, len(idx), 128):
+            blk = np.asarray(idx[c0:c0 + 128], np.int64)
+            visible = seq - n_q + blk + 1
+            vmax = int(visible.max())
+            hidden = np.arange(vmax)[None, :] >= visible[:, None]
+            for kv in range(hk):
+                heads = slice(kv * group, (kv + 1) * group)
+                qb = q[a + blk, heads].astype(np.float64)                  # [rows, group, D]
+                s = (qb.reshape(-1, qb.shape[-1]) @ keys64[:vmax, kv].T).reshape(len(blk), group, vmax) * scale
+                s[np.broadcast_to(hidden[:, None, :], s.shape)] = -np.inf
+                m = s.max(-1, keepdims=True)
+                with np.errstate(invalid="ignore"):
+                    p = np.exp(s - m)
+                tot = p.sum(-1, keepdims=True)
+                o = (p.reshape(-1, vmax) @ vals64[:vmax, kv]).reshape(len(blk), group, -1) / tot
+                lse_b = (m + np.log(tot))[..., 0]
+                bad = np.isnan(m[..., 0])
+                o[bad] = np.nan
+                lse_b[bad] = np.nan
+                out[a + blk, heads] = o
+                lse[a + blk, heads] = lse_b
     return out, lse
 
 

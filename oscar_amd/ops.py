@@ -169,7 +169,7 @@ class DeviceScratch:
     def step_workspace(self, nbytes: int) -> torch.Tensor:
         """The native decode step's workspace (rotated q / k / v, out_rot, LSE, item
         partials)."""
-        if self.step_ws.numel() < nbytes:
+        if self.step_ws.numel() < max(nbytes, 1):  # never hand out an empty buffer
             self.step_ws = torch.empty(max(nbytes, 4 << 20), dtype=torch.uint8, device=self.device)
         return self.step_ws
 

@@ -278,13 +278,18 @@ def test_config1_store_then_decode_through_forward(cuda):
 
 
 # ---------------------------------------------------------------- config 5
-def continuation_rows(history, n, extra=48, seed=20261205):
+def continuation_rows(history, n, extra=48, seed=20261205, group=6):
     """First and last rows, both sides of every 8192-key boundary the chunk crosses,
-    and a seeded sample through the chunk."""
+    one query token in every 128-row GQA query tile of the prefill (128 // group tokens
+    each; the token's place in its tile moves from tile to tile), so every tile and
+    every chunk of the balanced split, with its merge slot, is compared; and a seeded
+    sample through the chunk."""
     rows = {0, 1, n - 2, n - 1}
     for key in range(8192, history + n + 1, 8192):
         i = key - history - 1  # query i sees keys [0, history + i + 1)
         rows.update(r for r in (i - 1, i, i + 1) if 0 <= r < n)
+    per_tile = 128 // group
+    rows.update(min(n - 1, t * per_tile + (t * 8) % per_tile) for t in range(-(-n // per_tile)))
     rows.update(np.random.default_rng(seed).choice(n, extra, replace=False).tolist())
     return sorted(rows)
 
@@ -305,6 +310,7 @@ def test_config5_continuation_at_full_size(cuda):
                                 stage=stage, lse=lse)
     torch.cuda.synchronize()
     rows = continuation_rows(history, n)
+    assert {r // (128 // 6) for r in rows} == set(range(-(-n // (128 // 6))))  # every query tile
     ref_o, ref_l = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                  c["seqs"], c["scale"], c["stage"], rows=rows)
     check_attention(out.cpu().numpy(), lse.cpu().numpy(), ref_o, ref_l,
