@@ -230,20 +230,49 @@ __device__ __forceinline__ bool row_all(bool pred) {
   return ((m >> (threadIdx.x & 48)) & 0xffffull) == 0xffffull;
 }
 
+__device__ __forceinline__ uint32_t row_or(uint32_t x) {
+  x |= (uint32_t)dpp_row_i<kDppXor1>((int)x);
+  x |= (uint32_t)dpp_row_i<kDppXor2>((int)x);
+  x |= (uint32_t)dpp_row_i<kDppHalfMirror>((int)x);
+  return x | (uint32_t)dpp_row_i<kDppMirror>((int)x);
+}
+
 // idx-th smallest |y| of the row's D values (the sort-clip threshold, backend.py:140-145),
-// bit by bit from the top: the answer is the largest value v with count(|y| < v) <= idx
+// bit by bit from the top: the answer is the largest value v with count(|y| < v) <= idx.
+// A row's candidate interval [v, v + 2^w) holds the elements of ranks c_lo .. c_hi - 1;
+// a row whose interval holds exactly one element stops there and takes that element
+// (an OR over the row; every other element contributes 0) instead of its remaining
+// bits.  The loop runs while any row of the wave holds two or more (ties run to bit 0).
 template <int E>
 __device__ float row_kth_abs(const float* y, int idx) {
   uint32_t u[E];
 #pragma unroll
   for (int j = 0; j < E; ++j) u[j] = __float_as_uint(y[j]) & 0x7fffffffu;  // order of |y| (finite)
   uint32_t v = 0;
-  for (int bit = 30; bit >= 0; --bit) {
+  int c_lo = 0, c_hi = 16 * E, w = 31;
+  for (int bit = 30; bit >= 0 && __any(c_hi - c_lo > 1); --bit) {
     const uint32_t cand = v | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) cnt += u[j] < cand;
-    if (row_sum(cnt) <= idx) v = cand;
+    cnt = row_sum(cnt);
+    if (c_hi - c_lo > 1) {  // a settled row keeps its interval
+      if (cnt <= idx) {
+        v = cand;
+        c_lo = cnt;
+      } else {
+        c_hi = cnt;
+      }
+      w = bit;
+    }
+  }
+  if (c_hi - c_lo == 1) {
+    const uint64_t end = (uint64_t)v + (1ull << w);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j)
+      if (u[j] >= v && (uint64_t)u[j] < end) m |= u[j];
+    v = row_or(m);
   }
   return __uint_as_float(v);
 }
@@ -380,7 +409,6 @@ constexpr int kFusedThreads = 512;  // 8 waves
 constexpr int kChainSteps = 4;      // K-steps per accumulation chain
 constexpr int kExactThreads = 512;
 constexpr int kExactGroup = 8;      // vectors per exact-pass group
-constexpr int kExactBuffer = 512;   // exact-pass vectors a fused workgroup gathers in LDS
 constexpr int kReqLds = 2048;       // request tables of up to this many entries go to LDS
 
 // power-of-two exponent s with m * 2^s in [2^14, 2^15) (m > 0 finite); 0 otherwise
@@ -865,8 +893,9 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
 // x_k R_kc in fp64 for the group's vectors, the four columns c = 4 quad .. 4 quad + 3
 // and the D / S rows k of its slice (each product of an input element with an fp32
 // entry is exact in fp64); R's rows come straight from global memory in batches of RB,
-// x_k of the group from LDS (one broadcast address per wave).  The slices' partial sums
-// are added in slice order, then rounded once to fp32.
+// the next two batches in flight during a batch's products (each batch costs one L2
+// round trip), x_k of the group from LDS (one broadcast address per wave).  The slices' partial sums are added in slice order, then
+// rounded once to fp32.
 template <int D, int XT>
 __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams p) {
   constexpr int G = kExactGroup;             // vectors per group
@@ -891,7 +920,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const int cq = tid % NQ, sl = tid / NQ;    // column quad, row slice
   const int k0 = sl * RS;
-  auto load_rows = [&](int kb, f32x4* r) {   // R[k][4 cq ..], k = k0 + kb + j
+  auto load_rows = [&](int kb, f32x4* r) {   // R[k][4 cq ..], k = k0 + kb + j (identity for NULL)
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int k = k0 + kb + j, o = k - 4 * cq;
@@ -899,8 +928,6 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       else r[j] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
     }
   };
-  f32x4 ra[RB];
-  load_rows(0, ra);  // the first rows of R are in flight during the scan
 
   // ---- the fused workgroups' counts: this thread's PT consecutive workgroups w and the
   // exclusive prefix pre[w] of all counts before them (a wave scan, then the waves)
@@ -941,6 +968,11 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   __shared__ int32_t s_id[G];
   __shared__ Dest s_dst[G];
   for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
+    // R's batches 0 (ra) and 1 (rb1), independent of the group: in flight during the
+    // list reads and the staging; batch b + 2 is issued when batch b's products start
+    f32x4 ra[RB], rb1[RB];
+    load_rows(0, ra);
+    if (RB < RS) load_rows(RB, rb1);
     // ---- the group's entries: each list position g0 .. g0 + G - 1 below count lies in
     // exactly one workgroup's segment; the thread owning that workgroup fills it
     {
@@ -981,11 +1013,10 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     double acc[G][4];
 #pragma unroll
     for (int v = 0; v < G; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0;
-    // batches of RB rows: the next batch's rows in flight during this one's products
 #pragma unroll 1
     for (int kb = 0; kb < RS; kb += RB) {
       f32x4 rn[RB];
-      if (kb + RB < RS) load_rows(kb + RB, rn);
+      if (kb + 2 * RB < RS) load_rows(kb + 2 * RB, rn);
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
         const int k = k0 + kb + j;
@@ -1003,9 +1034,10 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
           acc[v + 1][3] = fma(xv.y, r3, acc[v + 1][3]);
         }
       }
-      if (kb + RB < RS) {
 #pragma unroll
-        for (int j = 0; j < RB; ++j) ra[j] = rn[j];
+      for (int j = 0; j < RB; ++j) {
+        ra[j] = rb1[j];
+        rb1[j] = rn[j];
       }
     }
 #pragma unroll
@@ -1049,7 +1081,6 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       quant_vector<D>(p, kind, id / hk, id % hk, s_dst[v], y4);
     }
     __syncthreads();  // s_id, s_xd, s_part, s_y, s_dst are rewritten by the next group
-    load_rows(0, ra);  // the next group's first rows (ra holds this group's last batch)
   }
 }
 

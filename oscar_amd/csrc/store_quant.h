@@ -78,7 +78,10 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
 // D-vector held by one wave, lane l < D / 4 holding elements 4l .. 4l + 3 in x4.
 // Selected bit by bit from the top on the magnitude bits (the order of |x|; NaN above
 // inf, as a sort puts it last): the answer is the largest v with count(|x| < v) <= idx,
-// each count four ballots of the wave.
+// each count four ballots of the wave.  The candidate interval [v, v + 2^(b+1)) holds
+// the elements of ranks c_lo .. c_hi - 1; once it holds exactly one (c_hi - c_lo == 1)
+// that element is the answer, found by a wave minimum over the interval instead of the
+// remaining bits (ties keep the interval at two or more elements and run to bit 0).
 template <int D>
 __device__ float wave_kth_abs(f32x4 x4, int idx) {
   const bool active = (int)(threadIdx.x & 63) < D / 4;
@@ -86,12 +89,31 @@ __device__ float wave_kth_abs(f32x4 x4, int idx) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) u[j] = active ? (__float_as_uint(x4[j]) & 0x7fffffffu) : 0xffffffffu;
   uint32_t v = 0;
-  for (int bit = 30; bit >= 0; --bit) {
+  int c_lo = 0, c_hi = D, bit = 30;
+  for (; bit >= 0 && c_hi - c_lo > 1; --bit) {  // wave-uniform: one vector per wave
     const uint32_t cand = v | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot(u[j] < cand));
-    if (cnt <= idx) v = cand;
+    if (cnt <= idx) {
+      v = cand;
+      c_lo = cnt;
+    } else {
+      c_hi = cnt;
+    }
+  }
+  if (c_hi - c_lo == 1) {
+    // the one element in [v, v + 2^(bit + 1)) (bit + 1 <= 31: the span fits 64 bits),
+    // gathered by an OR over the wave (every other element contributes 0; its bits are
+    // kept exactly, NaN payloads included)
+    const uint64_t end = (uint64_t)v + (2ull << bit);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (u[j] >= v && (uint64_t)u[j] < end) m |= u[j];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o);
+    v = m;
   }
   return __uint_as_float(v);
 }
