@@ -251,8 +251,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   // reads of 4 consecutive keys x 32 bytes cover all banks)
   __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKeys][D + 8];
   __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKeys][D + 16];
-  // each wave's Q^T operands (K-step j, lane l), read at each use
-  __shared__ __attribute__((aligned(16))) u32x4 s_q[kWaves][D / 16][64];
 
   // fill mapping: pass i, thread -> key i * KPP + tid / CPR, 16-byte column tid % CPR,
   // so that a wave reads (and stores to LDS) whole contiguous key rows
@@ -309,9 +307,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
   const bool row_ok = (n < P.qtok * G) && (qi < q1);
   const int head = kvh * G + n % G;
   const uint16_t* qrow = (const uint16_t*)A.q + (row_ok ? qi : 0) * A.q_stride_token + (int64_t)head * D;
+  // the wave's Q^T operands (K-step j) in registers for the whole key range: each
+  // tile's QK then reads only K from LDS
+  QV qreg[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j)
-    s_q[wave][j][lane] = row_ok ? *(const u32x4*)(qrow + 16 * j + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    qreg[j] = __builtin_bit_cast(QV, row_ok ? *(const u32x4*)(qrow + 16 * j + 8 * g) : u32x4{0u, 0u, 0u, 0u});
   const float c = A.scale * kLog2e;
   const int64_t limit = hist + qi + 1;  // keys [0, limit) visible to this row
 
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
 #pragma unroll
         for (int j = 0; j < kQK; ++j) {
           ka[j] = *(const QV*)&s_k[buf][m][16 * (j0 + j) + 8 * g];
-          qa[j] = __builtin_bit_cast(QV, s_q[wave][j0 + j][lane]);
+          qa[j] = qreg[j0 + j];
         }
 #pragma unroll
         for (int j = 0; j < kQK; ++j) {
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillParams P) {
           else S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], S, 0, 0, 0);
         }
         // keep the group's LDS reads ahead of its MFMAs (one latency per group)
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQK, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kQK, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, kQK, 0);
       }
       const bool full = (k0 + kKeys <= hist + q0 + 1);  // visible to every row of the tile
