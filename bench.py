@@ -455,6 +455,12 @@ def forward_call(setup, layer_idx=0):
     layer._oscar_stage_ready = impl._oscar_stage_ready = True
     impl.stage_block = c["block_size"]
     impl.sink_eff = setup.sink_eff
+    # what cache initialization does in serving (integration.initialize_layers): the
+    # stream's scratch and the transient workspaces at the sizes the batch limits give
+    from oscar_amd import integration
+
+    integration.reserve_device_scratch([impl], [(kc, vc)], max_tokens=setup.q.shape[0],
+                                       max_len=max(setup.seqs), max_seqs=len(setup.seqs))
     md = _Meta()
     md.num_actual_tokens = setup.q.shape[0]
     md.slot_mapping = setup.slots

@@ -164,6 +164,15 @@ class _Batch:
         as it is."""
         return not self.fresh and not self.long
 
+    def span(self, members):
+        """(i0, i1, a, b) when requests i0 <= i < i1 are the members and empty requests and
+        their query rows are [a, b); None when another request's rows lie in between."""
+        lo, hi = min(members), max(members)
+        inside = set(members)
+        if any(j not in inside and self.qsl[j + 1] > self.qsl[j] for j in range(lo, hi + 1)):
+            return None
+        return lo, hi + 1, self.qsl[lo], self.qsl[hi + 1]
+
     @property
     def covers_all(self) -> bool:
         """The requests' query ranges tile [0, actual) (no padding rows to zero)."""
@@ -467,11 +476,13 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
                                    group=group, head_dim=d, device=dev, window=window,
                                    upload_now=False)
             parts += plan.host_parts() + route["index_parts"]
-        cached_rows = None
+        cached_rows, cached_span = None, None
         if not batch.decode_only and (batch.short or batch.long):
-            cached_rows = np.concatenate([np.arange(batch.qsl[i], batch.qsl[i + 1])
-                                          for i in batch.short + batch.long]).astype(np.int64)
-            parts.append(cached_rows)
+            cached_span = batch.span(batch.short + batch.long)
+            if cached_span is None:
+                cached_rows = np.concatenate([np.arange(batch.qsl[i], batch.qsl[i + 1])
+                                              for i in batch.short + batch.long]).astype(np.int64)
+                parts.append(cached_rows)
         dev_parts = ops.upload(parts, dev) if parts else []
         if write_now and stage_mode == STAGE_WRITE:
             store_qsl_dev, store_seqs_dev, dev_parts = dev_parts[0], dev_parts[1], dev_parts[2:]
@@ -516,6 +527,12 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             if route["identity"]:
                 ops.attention_decode(q_rot, k_rot, v_rot, self.key_cache, self.value_cache, table,
                                      plan, self.scale, stage, head_dim=d, out_rot=out_rot, lse=lse)
+            elif route["span"] is not None:
+                i0, i1, a, b = route["span"]
+                cut = (lambda t: None if t is None else t[a:b])
+                ops.attention_decode(cut(q_rot), cut(k_rot), cut(v_rot), self.key_cache,
+                                     self.value_cache, table[i0:i1], plan, self.scale, stage,
+                                     head_dim=d, out_rot=out_rot[a:b], lse=lse[a:b])
             else:
                 ids, req = route["index_dev"]
                 pick = (lambda t: None if t is None else torch.index_select(t, 0, ids))
@@ -533,6 +550,9 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
                                       stage=stage, out=out_rot[a:b], lse=lse[a:b])
         if batch.decode_only:
             ops.rotate(out_rot, rv, transpose=True, out_dtype=query.dtype, out=out3[:actual])
+        elif cached_span is not None:
+            _, _, a, b = cached_span
+            ops.rotate(out_rot[a:b], rv, transpose=True, out_dtype=query.dtype, out=out3[a:b])
         else:
             rows = torch.index_select(out_rot, 0, cached_rows_dev)
             out3.index_copy_(0, cached_rows_dev, ops.rotate(rows, rv, transpose=True, out_dtype=query.dtype))
@@ -544,9 +564,16 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
         """Requests for the split-K decode (the planner cuts chunks of more than 32 rows
         per KV head into sub-requests).  A decode-only batch is planned as it is (the
         plan's request r is metadata request r: no gathers); otherwise the decode
-        requests form a compact batch, gathered by row and block-table row."""
+        requests form a compact batch: the batch's own rows and block-table rows where the
+        decode requests (and empty ones between them) are consecutive, as a decode-first
+        batch order leaves them; gathered by row and block-table row otherwise."""
         if batch.decode_only:
-            return dict(identity=True, qsl=batch.qsl, seqs=batch.seqs, index_parts=[])
+            return dict(identity=True, span=None, qsl=batch.qsl, seqs=batch.seqs, index_parts=[])
+        span = batch.span(batch.short)
+        if span is not None:
+            i0, i1, a, _ = span
+            return dict(identity=False, span=span, qsl=[batch.qsl[i] - a for i in range(i0, i1 + 1)],
+                        seqs=batch.seqs[i0:i1], index_parts=[])
         sub_qsl, sub_seqs, ids, req = [0], [], [], []
         for i in batch.short:
             a, b = batch.qsl[i], batch.qsl[i + 1]
@@ -554,5 +581,5 @@ class OscarAttentionBackendImpl(BaseAttentionImpl):  # type: ignore[misc,valid-t
             req.append(i)
             sub_qsl.append(sub_qsl[-1] + b - a)
             sub_seqs.append(batch.seqs[i])
-        return dict(identity=False, qsl=sub_qsl, seqs=sub_seqs,
+        return dict(identity=False, span=None, qsl=sub_qsl, seqs=sub_seqs,
                     index_parts=[np.asarray(ids, np.int64), np.asarray(req, np.int64)])

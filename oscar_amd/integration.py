@@ -366,7 +366,19 @@ def _allocated(device) -> int | None:
     return torch.cuda.memory_allocated(device)
 
 
-def _reserve_device_scratch(impls, caches_of, max_tokens: int, max_len: int, max_seqs: int) -> int:
+def _warm_gathers(dev) -> None:
+    """torch loads a kernel's code object at the kernel's first launch (about 0.1 s for its
+    indexing kernels): launch the row gathers and scatters of the mixed-batch route (a
+    batch whose decode requests are not consecutive) once at initialization instead."""
+    import torch
+
+    idx = torch.zeros(1, dtype=torch.int64, device=dev)
+    for dt in (torch.float32, torch.bfloat16, torch.float16, torch.int32):
+        t = torch.zeros(1, 1, dtype=dt, device=dev)
+        t.index_copy_(0, idx, torch.index_select(t, 0, idx))
+
+
+def reserve_device_scratch(impls, caches_of, max_tokens: int, max_len: int, max_seqs: int = 0) -> int:
     """Allocate the scratch of the current stream on each layer's device (claim tables,
     epoch, arrival counters) and its workspaces at their planned sizes, so that no
     forward allocates; returns the bytes of the scratch that stays (the workspaces are
@@ -391,6 +403,7 @@ def _reserve_device_scratch(impls, caches_of, max_tokens: int, max_len: int, max
             scratch.prefill_workspace(parts["prefill"])
             scratch.step_workspace(parts["step"])
             ops.DeviceContext.get(dev)
+            _warm_gathers(dev)
     return sum(_nbytes(s.epoch_counter, s.slot_claims, s.seat_claims, s.arrivals) for s in touched.values())
 
 
@@ -424,8 +437,8 @@ def initialize_layers(runner, config, caches) -> dict | None:
         if twin is not caches[name]:
             persistent += _nbytes(*shadow_halves(twin))
     max_tokens, max_len, max_seqs = _limits(runner.vllm_config)
-    persistent += _reserve_device_scratch([m.impl for _, m in bound], [caches[n] for n, _ in bound],
-                                          max_tokens, max_len, max_seqs)
+    persistent += reserve_device_scratch([m.impl for _, m in bound], [caches[n] for n, _ in bound],
+                                         max_tokens, max_len, max_seqs)
     after = _allocated(device)
     plan = getattr(runner, "_oscar_memory_plan", None) or {}
     native_bytes = sum(t.size for t in config.kv_cache_tensors)

@@ -79,13 +79,17 @@ def test_forward_steps_match_oracle(cuda, qdt, ulp):
     assert np.array_equal(caches[1].view(torch.uint8).cpu().numpy(), oracle_layer.v8)
 
 
-@pytest.mark.parametrize("mode", ["mtp_window", "cache_only", "fp16_mtp", "long_chunks", "long_chunks_fresh"])
+@pytest.mark.parametrize("mode", ["mtp_window", "cache_only", "fp16_mtp", "long_chunks", "long_chunks_fresh",
+                                  "fresh_last"])
 def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
     """forward() on decode-shaped batches takes oscar_decode_step_v1 (one native call);
     the same batch through the general Python path (_run) and the oracle agree.
     long_chunks: chunks of 240 and 72 rows per KV head (sub-requests of the plan);
     long_chunks_fresh: the same beside a history-free request, which the native step
-    declines and the general path routes as a compact decode batch plus a prefill."""
+    declines and the general path routes as a compact decode batch (gathered rows and
+    block-table rows, the fresh request lying between decodes) plus a prefill;
+    fresh_last: the fresh request after the decodes (their rows and table rows are a
+    slice of the batch's)."""
     from oscar_amd import backend as B
     from oracle.attention import attention_ref
 
@@ -97,6 +101,8 @@ def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
         lengths = [40, 1, 12, 4]
     if mode == "long_chunks_fresh":
         prefixes, lengths = [3000, 0, 700, 24579], [40, 300, 12, 4]
+    if mode == "fresh_last":
+        prefixes, lengths = [3000, 700, 24579, 0], [40, 12, 4, 300]
     c = cases.make_case(prefixes, lengths, fresh=fresh, seed=77)
     d, hq, hk = 256, 6, 1
     impl = OscarAttentionBackendImplFactory()
@@ -124,7 +130,7 @@ def test_native_decode_step_matches_general_path_and_oracle(cuda, mode):
     calls = {"reads": impl._oscar_stats["reads"]}
     out_native = torch.empty(N, hq * d, dtype=qdt, device=dev)
     native = impl._native_step(layer, tq, tk, tv, caches, md, out_native)
-    assert native == (mode != "long_chunks_fresh")
+    assert native == (mode not in ("long_chunks_fresh", "fresh_last"))
     out_general = torch.empty_like(out_native)
     impl._run(layer, tq, tk, tv, caches, md, out_general, write=True)
     torch.cuda.synchronize()

@@ -250,3 +250,34 @@ def test_staging_struct_checks_the_arena_against_the_cache():
         staging_struct((good[0].transpose(0, 1), good[1], good[2]), kc, 64)
     with pytest.raises(ValueError, match="fp32"):
         staging_struct((good[0].half(), good[1], good[2]), kc, 64)
+
+
+def test_mixed_batch_routes_slice_consecutive_decodes_and_gather_otherwise():
+    """A batch with a continuation chunk or a fresh prefill sends its short requests to the
+    split-K decode: as a slice of the batch's rows and block-table rows when they (and empty
+    requests between them) are consecutive, by gathers otherwise (backend.py:334-393 routing)."""
+    from oscar_amd.backend import _Batch
+
+    impl = make_impl()
+    # continuation of 9256 rows, 16 one-token decodes, a fresh 2048-token prefill
+    qsl = [0, 9256] + [9256 + i for i in range(1, 17)] + [9272 + 2048]
+    seqs = [15360 + 9256] + [8193] * 16 + [2048]
+    b = _Batch.classify(qsl, seqs, qsl[-1], True, 6)
+    assert b.long == [0] and b.short == list(range(1, 17)) and b.fresh == [17]
+    route = impl._decode_route(b)
+    assert route["span"] == (1, 17, 9256, 9272) and route["index_parts"] == []
+    assert route["qsl"] == list(range(17)) and route["seqs"] == [8193] * 16
+    assert b.span(b.short + b.long) == (0, 17, 0, 9272)
+    # an empty request between decodes keeps the slice; a fresh one between them does not
+    qsl2 = [0, 4, 4, 5, 305, 306]
+    seqs2 = [3004, 10, 130, 300, 701]
+    b2 = _Batch.classify(qsl2, seqs2, qsl2[-1], True, 6)
+    assert b2.short == [0, 2, 4] and b2.fresh == [3]
+    route2 = impl._decode_route(b2)
+    assert route2["span"] is None
+    assert route2["qsl"] == [0, 4, 5, 6] and route2["seqs"] == [3004, 130, 701]
+    assert [p.tolist() for p in route2["index_parts"]] == [[0, 1, 2, 3, 4, 305], [0, 2, 4]]
+    b3 = _Batch.classify(qsl2[:5], seqs2[:4], 305, True, 6)
+    assert b3.short == [0, 2] and b3.fresh == [3]
+    assert impl._decode_route(b3)["span"] == (0, 3, 0, 5)
+    assert impl._decode_route(b3)["qsl"] == [0, 4, 4, 5]
