@@ -838,8 +838,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   }
 
   // ---- slow tiles, in value units, one at a time by the whole workgroup: build
-  // (all threads), then the next tile's loads go out while one wave computes
-  if (nslow > 0) load_slow(__builtin_amdgcn_readfirstlane(s_slow[0]));
+  // (all threads), then the next tile's loads go out while one wave computes.  The
+  // build buffers alias every wave's V-code slot of the fast loop, so the first build
+  // waits until all waves are past it (nslow is the same for the whole workgroup).
+  if (nslow > 0) {
+    load_slow(__builtin_amdgcn_readfirstlane(s_slow[0]));
+    __syncthreads();
+  }
 #pragma unroll 1
   for (int k = 0; k < nslow; ++k) {
     const int j = __builtin_amdgcn_readfirstlane(s_slow[k]);
