@@ -128,6 +128,10 @@ typedef struct oscar_store_args_v1 {
 } oscar_store_args_v1;
 
 int64_t oscar_store_workspace_bytes_v1(int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim);
+/* Codes, scales / zeros, slot bytes and owner tags are those of the correctly rounded
+ * fp32 rotation.  FP32 window values are that rotation for calls of <= 64 tokens; larger
+ * calls store the certified MFMA rotation, within 2^-20 ||x|| ||R_:d|| + 2^-22 |y| of it
+ * (bf16 / fp16 inputs; 2^-19 for fp32). */
 int oscar_store_v1(const oscar_store_args_v1* args, void* stream);
 
 /* y[M, D] = x[M, D] @ R[D, D] (or @ R^T when transpose != 0); fp32 accumulate

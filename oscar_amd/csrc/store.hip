@@ -18,8 +18,9 @@
 //   larger calls: store_prep_kernel (last-writer claims, window flags, fp16 planes of R),
 //   store_fused_kernel (MFMA rotation into LDS, then per vector: read-path copy,
 //   certification that every quantizer decision taken on the MFMA result is the one
-//   the exact y takes, quantization), store_exact_kernel (fp64 y for the vectors that
-//   were not certified and for those that keep an FP32 window copy).
+//   the exact y takes, quantization; the FP32 window copies of its vectors are y~ itself,
+//   within the rotation bound e of y), store_exact_kernel (fp64 y for the vectors that
+//   were not certified).
 //
 // Claim epochs live on the device in two int64 words so that a captured graph
 // replays with fresh epochs and no extra launch: the prep kernel uses
@@ -391,9 +392,9 @@ __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, 
 //                        chains of kChainSteps K-steps whose sum is rounded once, into an LDS
 //                        tile of whole vectors.  Then each wave takes vectors from the tile:
 //                        read-path copy, destination, certification, quantization.
-//   store_exact_kernel   the vectors that were not certified or whose FP32 window copy
-//                        needs y itself: y in fp64 (exact products, one final rounding),
-//                        then the same quantizer.
+//   store_exact_kernel   the vectors that were not certified: y in fp64 (exact products,
+//                        one final rounding), then the same quantizer (and their FP32
+//                        window copies from that y).
 //
 // Error of y~ against y: the instruction's products are exact and it rounds C + (the
 // sum of its 16 products) once to fp32 (measured on gfx950), so a chain of kChainSteps
@@ -866,14 +867,26 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
         if (kind == KIND_Q) continue;
         Dest d{};
         if (live) d = s_dest[prv][v];
-        bool exact = d.valid && d.seat_win && d.keep;  // the FP32 window copy is y itself
-        if (d.valid && !exact && d.slot_win) {
+        // the slot's bytes: certified from y~, or left to the exact pass
+        bool exact = false;
+        if (d.valid && d.slot_win) {
           exact = !certify_quant16<D>(p, kind, y, fmaf(cx, s_nx[prv][v], 0x1p-126f), true,
                                       a.cache.k + d.koff, a.cache.v + d.voff);
         }
         if (exact && l == 0) xlist[atomicAdd(&s_xn, 1)] = (int32_t)vec;
-        // a seat this token wins outside the window loses its FP32 copy (backend.py:536-541)
-        if (d.valid && !exact && d.seat_win && kind == KIND_K && l == 0) a.staging.owner[d.seat] = -1;
+        // the seat (an exact-pass vector's is written there, from y): a token in the window
+        // keeps its FP32 copy -- y~ itself, within the rotation bound e of y (the bytes are
+        // exact either way) -- and tags its block; a seat it wins outside the window loses
+        // its FP32 copy (backend.py:513-555)
+        if (d.valid && !exact && d.seat_win) {
+          if (d.keep) {
+            float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) +
+                         (d.seat * hk + (int64_t)((uint32_t)vec % hk32)) * D + l * E;
+#pragma unroll
+            for (int q = 0; q < E; q += 4) *(f32x4*)&dst[q] = *(const f32x4*)&y[q];
+          }
+          if (kind == KIND_K && l == 0) a.staging.owner[d.seat] = d.keep ? d.slot / a.cache.block_size : -1;
+        }
       }
     };
     // the claims are only needed by waves that form before they quantize (tid < TV)

@@ -4,7 +4,7 @@ Config 1  one request: a 1024-token store (fresh prefill through the impl), then
           single-token decode, against the oracle backend (backend.py:249-393).
 Config 2  the store alone: 15360 tokens, 5 % skipped slots, 2 % rewrites, window
           write / standalone invalidation, with and without the serve-default clip;
-          bytes, owner tags and window values bit-exact (store_kernel.py:54-102,
+          bytes and owner tags bit-exact, window values within the rotation bound (store_kernel.py:54-102,
           backend.py:151-198,513-555).
 Config 3  one request, 24576-token history + 4-token MTP: the benchmarked layer step.
 Config 4a 8 x (24576 + 4 MTP): the headline step exactly as bench.py builds and times it
@@ -31,6 +31,7 @@ from oracle import backend as ob
 from oracle import cases, fmt
 from oracle.attention import attention_ref
 from oracle.store import Staging, clip, rotate, store_ref
+from window_check import assert_window_close
 
 pytestmark = pytest.mark.gpu
 
@@ -191,8 +192,8 @@ def test_config2_store_at_full_size(cuda, mode, kclip, vclip):
     assert np.array_equal(got_k, k8), f"K bytes differ at {bad[:5]}"
     assert np.array_equal(got_v, v8), "V bytes differ"
     assert np.array_equal(own.cpu().numpy(), st.owner), "owner tags differ"
-    assert np.array_equal(sk.cpu().numpy(), st.stage_k), "K window differs"
-    assert np.array_equal(sv.cpu().numpy(), st.stage_v), "V window differs"
+    assert_window_close(sk.cpu().numpy(), st.stage_k, [k], rk, "K window")
+    assert_window_close(sv.cpu().numpy(), st.stage_v, [v], rv, "V window")
 
 
 # ---------------------------------------------------------------- impl harness
@@ -257,6 +258,7 @@ def test_config1_store_then_decode_through_forward(cuda):
     oracle_layer = ob.OracleLayer(k8=np.zeros((nb, bs, hk, d), np.uint8),
                                   v8=np.zeros((nb, bs, hk, d), np.uint8), rk=rk, rv=rv, hq=hq,
                                   hk=hk, d=d, scale=d ** -0.5)
+    written_k = []
     for p0, p1 in ((0, 1024), (1024, 1025)):
         n = p1 - p0
         pos = np.arange(p0, p1)
@@ -264,6 +266,7 @@ def test_config1_store_then_decode_through_forward(cuda):
         q = cases.bf16_normal((n, hq, d), cases.BASE_SEED + p0)
         k = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 1 + p0)
         v = cases.kv_outliers(n, hk, d, cases.BASE_SEED + 2 + p0)
+        written_k.append(k)
         md = metadata(dev, slots, [0, n], [p1], table)
         out = torch.empty(n, hq * d, dtype=torch.bfloat16, device=dev)
         tq, tk, tv = (torch.from_numpy(x).to(dev).bfloat16() for x in (q, k, v))
@@ -274,7 +277,7 @@ def test_config1_store_then_decode_through_forward(cuda):
     assert np.array_equal(np_u8(caches[0]), oracle_layer.k8)
     assert np.array_equal(np_u8(caches[1]), oracle_layer.v8)
     assert np.array_equal(layer._oscar_slot_owner.cpu().numpy(), oracle_layer.staging.owner)
-    assert np.array_equal(layer._oscar_stage_k.cpu().numpy(), oracle_layer.staging.stage_k)
+    assert_window_close(layer._oscar_stage_k.cpu().numpy(), oracle_layer.staging.stage_k, written_k, rk, "K window")
 
 
 # ---------------------------------------------------------------- config 5
@@ -351,7 +354,7 @@ def test_config5_batched_forward(cuda):
     assert np.array_equal(np_u8(caches[0]), oracle_layer.k8)
     assert np.array_equal(np_u8(caches[1]), oracle_layer.v8)
     assert np.array_equal(layer._oscar_slot_owner.cpu().numpy(), oracle_layer.staging.owner)
-    assert np.array_equal(layer._oscar_stage_v.cpu().numpy(), oracle_layer.staging.stage_v)
+    assert_window_close(layer._oscar_stage_v.cpu().numpy(), oracle_layer.staging.stage_v, [c["v"]], rv, "V window")
 
 
 # ---------------------------------------------------------------- the reference's probe cases

@@ -1,7 +1,11 @@
 """GPU parity of the INT2 write path (oscar_store_v1) against the CPU oracle.
 
-Bar: bit-exact cache bytes (meta + codes, untouched bytes preserved), owner tags
-and FP32 window values.  Read-path rotated copies: calls of at most 64 tokens
+Bar: bit-exact cache bytes (meta + codes, untouched bytes preserved) and owner
+tags.  FP32 window values: bit-exact for calls of at most 64 tokens (the fp64
+rotation); larger calls keep y~, the MFMA rotation, whose distance from the
+correctly rounded y is bounded by 2^-20 ||x|| ||R_:d|| + 2^-22 |y~| (bf16 / fp16
+inputs; the kernel's certification bound), unless the vector took the exact pass.
+Read-path rotated copies: calls of at most 64 tokens
 round the correctly rounded rotation to the input dtype (bit-exact); larger calls
 round the MFMA rotation, which lies within 2^-20 ||x|| ||R_:d|| of it, so a copy
 is within that bound plus one unit of the dtype, and rarely differs at all (the
@@ -14,6 +18,7 @@ import torch
 
 from oracle import cases, fmt
 from oracle.store import Staging, clip, rotate, rotate_f32gemm, store_ref
+from window_check import assert_window_close
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +57,15 @@ def assert_read_copy(got, x, r, n_tokens, unit=2.0 ** -8):
     tol = 2.0 ** -20 * nx * cn + unit * np.abs(exact)
     assert np.all(np.abs(got.astype(np.float64) - exact) <= tol)
     assert (got != want).mean() < 1e-2, (got != want).mean()
+
+
+def assert_window(got, want, x, r, n_tokens):
+    """FP32 window values: bit-exact for calls of at most 64 tokens, else within the
+    MFMA rotation bound (window_check)."""
+    if n_tokens <= 64:
+        assert np.array_equal(got, want)
+    else:
+        assert_window_close(got, want, [x], r)
 
 
 def run_store(k, v, caches, slots, d, rk, rv, **kw):
@@ -255,8 +269,8 @@ def test_store_window_tags_values_and_rotated_outputs(cuda, qsl, seqs, nb):
     assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
     assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
     assert np.array_equal(own.cpu().numpy(), st.owner)
-    assert np.array_equal(sk.cpu().numpy(), st.stage_k)
-    assert np.array_equal(sv.cpu().numpy(), st.stage_v)
+    assert_window(sk.cpu().numpy(), st.stage_k, k, rk, n)
+    assert_window(sv.cpu().numpy(), st.stage_v, v, rv, n)
     assert_read_copy(q_rot.float().cpu().numpy(), q, rk, n)
     assert_read_copy(k_rot.float().cpu().numpy(), k, rk, n)
     assert_read_copy(v_rot.float().cpu().numpy(), v, rv, n)
