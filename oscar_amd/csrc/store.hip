@@ -238,44 +238,72 @@ __device__ __forceinline__ uint32_t row_or(uint32_t x) {
   return x | (uint32_t)dpp_row_i<kDppMirror>((int)x);
 }
 
+// the median of three (v_med3_u32)
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t x) {
+  x = min(x, (uint32_t)dpp_row_i<kDppXor1>((int)x));
+  x = min(x, (uint32_t)dpp_row_i<kDppXor2>((int)x));
+  x = min(x, (uint32_t)dpp_row_i<kDppHalfMirror>((int)x));
+  return min(x, (uint32_t)dpp_row_i<kDppMirror>((int)x));
+}
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t x) {
+  x = max(x, (uint32_t)dpp_row_i<kDppXor1>((int)x));
+  x = max(x, (uint32_t)dpp_row_i<kDppXor2>((int)x));
+  x = max(x, (uint32_t)dpp_row_i<kDppHalfMirror>((int)x));
+  return max(x, (uint32_t)dpp_row_i<kDppMirror>((int)x));
+}
+
 // idx-th smallest |y| of the row's D values (the sort-clip threshold, backend.py:140-145),
-// bit by bit from the top: the answer is the largest value v with count(|y| < v) <= idx.
-// A row's candidate interval [v, v + 2^w) holds the elements of ranks c_lo .. c_hi - 1;
-// a row whose interval holds exactly one element stops there and takes that element
-// (an OR over the row; every other element contributes 0) instead of its remaining
-// bits.  The loop runs while any row of the wave holds two or more (ties run to bit 0).
+// on the magnitude bits (their order is that of |y|; the row is finite): the answer a is
+// the largest v with count(|y| < v) <= idx, i.e. the (D - idx)-th largest element.
+// Bisection of [lo, hi) with a in [lo, hi): hi = row maximum + 1, lo = the row minimum of
+// each lane's k-th largest, k = 1 while D - idx <= 16, 2 while <= 32 (each of the 16
+// lanes holds k elements >= lo, so at least D - idx do and a >= lo), else 0.  c_lo .. c_hi
+// bound the ranks inside the interval; a row whose interval holds exactly one element
+// stops there and takes that element (an OR over the row; every other element
+// contributes 0), a row whose interval is one value wide takes lo (ties).  The loop runs
+// while any row of the wave is open.
 template <int E>
 __device__ float row_kth_abs(const float* y, int idx) {
+  constexpr int N = 16 * E;
   uint32_t u[E];
+  uint32_t m1 = 0, m2 = 0;  // this lane's largest and second largest
 #pragma unroll
-  for (int j = 0; j < E; ++j) u[j] = __float_as_uint(y[j]) & 0x7fffffffu;  // order of |y| (finite)
-  uint32_t v = 0;
-  int c_lo = 0, c_hi = 16 * E, w = 31;
-  for (int bit = 30; bit >= 0 && __any(c_hi - c_lo > 1); --bit) {
-    const uint32_t cand = v | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) cnt += u[j] < cand;
-    cnt = row_sum(cnt);
-    if (c_hi - c_lo > 1) {  // a settled row keeps its interval
-      if (cnt <= idx) {
-        v = cand;
-        c_lo = cnt;
-      } else {
-        c_hi = cnt;
-      }
-      w = bit;
-    }
+  for (int j = 0; j < E; ++j) {
+    u[j] = __float_as_uint(y[j]) & 0x7fffffffu;
+    m2 = max(m2, min(m1, u[j]));
+    m1 = max(m1, u[j]);
   }
-  if (c_hi - c_lo == 1) {
-    const uint64_t end = (uint64_t)v + (1ull << w);
-    uint32_t m = 0;
+  const int need = N - idx;
+  uint32_t lo = row_min_u32(need <= 16 ? m1 : (need <= 32 ? m2 : 0u));
+  uint32_t hi = row_max_u32(m1) + 1u;  // <= 2^31: every element and candidate is below
+  int c_lo = 0, c_hi = N;  // c_lo: a lower bound of count(|y| < lo) until lo first moves
+  bool open = hi - lo > 1;
+  while (__any(open)) {
+    // an open row has lo < mid < hi: med3(u, mid - 1, mid) is mid - 1 for u < mid and mid
+    // otherwise, so the lane's sum is E (mid - 1) + count(u >= mid) (mod 2^32)
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    uint32_t s = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j)
-      if (u[j] >= v && (uint64_t)u[j] < end) m |= u[j];
-    v = row_or(m);
+    for (int j = 0; j < E; j += 2) s += med3_u32(u[j], mid - 1u, mid) + med3_u32(u[j + 1], mid - 1u, mid);
+    const int cnt = row_sum(E - (int)(s - (uint32_t)E * (mid - 1u)));  // count(|y| < mid)
+    const bool up = open && cnt <= idx, down = open && cnt > idx;
+    lo = up ? mid : lo;
+    c_lo = up ? cnt : c_lo;
+    hi = down ? mid : hi;
+    c_hi = down ? cnt : c_hi;
+    open = hi - lo > 1 && c_hi - c_lo > 1;
   }
-  return __uint_as_float(v);
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < E; ++j)
+    if (u[j] >= lo && u[j] < hi) m |= u[j];
+  m = row_or(m);
+  return __uint_as_float(c_hi - c_lo == 1 ? m : lo);
 }
 
 // Certify and quantize the rows' vectors from y~ (lane: y[E] of its row's vector).  The

@@ -76,46 +76,62 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
 
 // Sort-clip threshold (backend.py:140-145): the idx-th smallest |x| (0-based) of a
 // D-vector held by one wave, lane l < D / 4 holding elements 4l .. 4l + 3 in x4.
-// Selected bit by bit from the top on the magnitude bits (the order of |x|; NaN above
-// inf, as a sort puts it last): the answer is the largest v with count(|x| < v) <= idx,
-// each count four ballots of the wave.  The candidate interval [v, v + 2^(b+1)) holds
-// the elements of ranks c_lo .. c_hi - 1; once it holds exactly one (c_hi - c_lo == 1)
-// that element is the answer, found by a wave minimum over the interval instead of the
-// remaining bits (ties keep the interval at two or more elements and run to bit 0).
+// Selected on the magnitude bits (the order of |x|; NaN above inf, as a sort puts it
+// last): the answer a is the largest v with count(|x| < v) <= idx, the (D - idx)-th
+// largest element, found by bisection of [lo, hi) with a in [lo, hi), each count four
+// ballots of the wave.  hi = the maximum + 1; lo = the minimum over the D / 16 lane
+// quads of each quad's k-th largest, k = 1 while D - idx <= D / 16, 2 while <= D / 8
+// (every quad holds k elements >= lo, so at least D - idx do and a >= lo), else 0.
+// Once the interval holds exactly one element (c_hi - c_lo == 1) that element is the
+// answer, gathered by an OR over the wave; an interval one value wide gives lo (ties).
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x = min(x, (uint32_t)__shfl_xor((int)x, o));
+  return x;
+}
 template <int D>
 __device__ float wave_kth_abs(f32x4 x4, int idx) {
   const bool active = (int)(threadIdx.x & 63) < D / 4;
   uint32_t u[4];
+  uint32_t m1 = 0, m2 = 0;  // this lane's largest and second largest
 #pragma unroll
-  for (int j = 0; j < 4; ++j) u[j] = active ? (__float_as_uint(x4[j]) & 0x7fffffffu) : 0xffffffffu;
-  uint32_t v = 0;
-  int c_lo = 0, c_hi = D, bit = 30;
-  for (; bit >= 0 && c_hi - c_lo > 1; --bit) {  // wave-uniform: one vector per wave
-    const uint32_t cand = v | (1u << bit);
+  for (int j = 0; j < 4; ++j) {
+    u[j] = active ? (__float_as_uint(x4[j]) & 0x7fffffffu) : 0xffffffffu;
+    const uint32_t w = active ? u[j] : 0u;
+    m2 = max(m2, min(m1, w));
+    m1 = max(m1, w);
+  }
+#pragma unroll
+  for (int o = 1; o < 4; o <<= 1) {  // the two largest of the lane quad
+    const uint32_t o1 = (uint32_t)__shfl_xor((int)m1, o), o2 = (uint32_t)__shfl_xor((int)m2, o);
+    m2 = max(min(m1, o1), max(m2, o2));
+    m1 = max(m1, o1);
+  }
+  const int need = D - idx;
+  uint32_t lo = wave_min_u32(active ? (need <= D / 16 ? m1 : (need <= D / 8 ? m2 : 0u)) : 0xffffffffu);
+  uint32_t hi = ~wave_min_u32(~m1) + 1u;  // the maximum + 1 (<= 2^31)
+  int c_lo = 0, c_hi = D;  // c_lo: a lower bound of count(|x| < lo) until lo first moves
+  while (hi - lo > 1 && c_hi - c_lo > 1) {  // wave-uniform: one vector per wave
+    const uint32_t mid = lo + ((hi - lo) >> 1);
     int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot(u[j] < cand));
+    for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot(u[j] < mid));
     if (cnt <= idx) {
-      v = cand;
+      lo = mid;
       c_lo = cnt;
     } else {
+      hi = mid;
       c_hi = cnt;
     }
   }
-  if (c_hi - c_lo == 1) {
-    // the one element in [v, v + 2^(bit + 1)) (bit + 1 <= 31: the span fits 64 bits),
-    // gathered by an OR over the wave (every other element contributes 0; its bits are
-    // kept exactly, NaN payloads included)
-    const uint64_t end = (uint64_t)v + (2ull << bit);
-    uint32_t m = 0;
+  // the one element in [lo, hi), its bits kept exactly (NaN payloads included)
+  uint32_t m = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (u[j] >= v && (uint64_t)u[j] < end) m |= u[j];
+  for (int j = 0; j < 4; ++j)
+    if (u[j] >= lo && u[j] < hi) m |= u[j];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o);
-    v = m;
-  }
-  return __uint_as_float(v);
+  for (int o = 1; o < 64; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o);
+  return __uint_as_float(c_hi - c_lo == 1 ? m : lo);
 }
 
 // Where one vector (kind K or V of token t) goes: slot, seat, whether this token is
