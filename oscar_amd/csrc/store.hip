@@ -315,12 +315,15 @@ __device__ float row_kth_abs(const float* y, int idx) {
 // over the interval means y gives the same bytes.  Certified rows with write != 0 store
 // their codes and meta (K slot kslot + 32 / V slot vslot); the function returns whether
 // this lane's row was certified.
-template <int D>
+// CLIP false: the kind's sort clip is off (known at compile time, so that the common
+// unclipped case carries no per-element clamps); true: tested at run time
+template <int D, bool CLIP>
 __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, float ex,
                                 bool write, uint8_t* kslot, uint8_t* vslot) {
   constexpr int E = D / 16;
   const int l = threadIdx.x & 15;
   const float clip = kind == KIND_K ? p.a.k_clip_ratio : p.a.v_clip_ratio;
+  const bool clipping = CLIP && clip > 0.f;
   // row extremes with NaN-propagating minimum / maximum: a NaN or inf anywhere makes eb
   // NaN or inf, and the row goes to the exact pass (which reproduces the reference)
   float vmin = y[0], vmax = y[0];
@@ -334,7 +337,7 @@ __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, 
   const float eb = ex + __builtin_elementwise_maximum(fabsf(vmin), fabsf(vmax)) * 0x1p-22f;
   if (!row_all(eb <= 0x1.fffffep127f)) return false;
   float t_lo = INFINITY, t_hi = INFINITY;
-  if (clip > 0.f) {
+  if (clipping) {
     int idx = (int)(clip * (float)D);
     if (idx > D - 1) idx = D - 1;
     const float t = row_kth_abs<E>(y, idx);
@@ -345,8 +348,8 @@ __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, 
   // the ends of an element's interval, clipped like the values themselves: lower ends
   // into [-t_hi, t_lo], upper ends into [-t_lo, t_hi]; clipping and rounding are
   // monotone, so the row extremes of the ends are the ends of the row extremes
-  auto lo_of = [&](float v) { return clip > 0.f ? fminf(fmaxf(v - eb, -t_hi), t_lo) : v - eb; };
-  auto hi_of = [&](float v) { return clip > 0.f ? fminf(fmaxf(v + eb, -t_lo), t_hi) : v + eb; };
+  auto lo_of = [&](float v) { return clipping ? fminf(fmaxf(v - eb, -t_hi), t_lo) : v - eb; };
+  auto hi_of = [&](float v) { return clipping ? fminf(fmaxf(v + eb, -t_lo), t_hi) : v + eb; };
   const float vmin_lo = lo_of(vmin), vmin_hi = hi_of(vmin), vmax_lo = lo_of(vmax), vmax_hi = hi_of(vmax);
   const unsigned short s_a = scale_bits_of(vmax_lo, vmin_hi), s_b = scale_bits_of(vmax_hi, vmin_lo);
   const unsigned short z_a = f32_to_f16_bits(vmin_lo), z_b = f32_to_f16_bits(vmin_hi);
@@ -362,10 +365,10 @@ __device__ bool certify_quant16(const StoreParams& p, int kind, const float* y, 
   // RN(RN(x - z) / s) + 0.5 for any x there is within w = ew (1 / s) + 2^-19 max(|q|, 1)
   // of t = fma(yc - z, 1 / s, 0.5) (a few ulp of rounding, and 1 / s within one ulp), so
   // where t is farther than w from every integer, all of them share floor(t)'s code.
-  const float tc = clip > 0.f ? 0.5f * (t_lo + t_hi) : INFINITY;
-  const float ew = clip > 0.f ? eb + (0.5f * (t_hi - t_lo) + tc * 0x1p-22f) * (1.f + 0x1p-20f) : eb;
+  const float tc = clipping ? 0.5f * (t_lo + t_hi) : INFINITY;
+  const float ew = clipping ? eb + (0.5f * (t_hi - t_lo) + tc * 0x1p-22f) * (1.f + 0x1p-20f) : eb;
   const float w = ew * inv * (1.f + 0x1p-20f) + 0x1p-19f * qm;
-  auto center = [&](int j) { return fmaf((clip > 0.f ? fminf(fmaxf(y[j], -tc), tc) : y[j]) - z16, inv, 0.5f); };
+  auto center = [&](int j) { return fmaf((clipping ? fminf(fmaxf(y[j], -tc), tc) : y[j]) - z16, inv, 0.5f); };
   auto code_at = [&](float t) {  // floor(t) clamped to [0, 3] (t truncated: equal after clamping)
     const int c = (int)t;
     return c < 0 ? 0 : (c > 3 ? 3 : c);
@@ -679,6 +682,7 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   void* rot_out = kind == KIND_K ? a.key_rot : (kind == KIND_V ? a.value_rot : a.query_rot);
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const int64_t epoch = a.epoch_counter[1];
+  const bool clipped = (kind == KIND_K ? a.k_clip_ratio : a.v_clip_ratio) > 0.f;  // this workgroup's kind
 
   const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -765,11 +769,15 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
       // ---- stage x: exponent, norm, fp16 planes in MFMA A order
       float f[16];
       xc.to_float(f);
-      const bool live = base + sv < nvec;
+      // the last round's vectors past the end stage zeros (rounds that end inside the
+      // call skip the test: workgroup-uniform)
+      if (base + TV > nvec && base + sv >= nvec) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) f[j] = 0.f;
+      }
       float mx = 0.f, ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        if (!live) f[j] = 0.f;
         mx = fmaxf(mx, fabsf(f[j]));
         ss = fmaf(f[j], f[j], ss);
       }
@@ -898,8 +906,9 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
         // the slot's bytes: certified from y~, or left to the exact pass
         bool exact = false;
         if (d.valid && d.slot_win) {
-          exact = !certify_quant16<D>(p, kind, y, fmaf(cx, s_nx[prv][v], 0x1p-126f), true,
-                                      a.cache.k + d.koff, a.cache.v + d.voff);
+          const float ex = fmaf(cx, s_nx[prv][v], 0x1p-126f);
+          exact = !(clipped ? certify_quant16<D, true>(p, kind, y, ex, true, a.cache.k + d.koff, a.cache.v + d.voff)
+                            : certify_quant16<D, false>(p, kind, y, ex, true, a.cache.k + d.koff, a.cache.v + d.voff));
         }
         if (exact && l == 0) xlist[atomicAdd(&s_xn, 1)] = (int32_t)vec;
         // the seat (an exact-pass vector's is written there, from y): a token in the window
