@@ -228,6 +228,48 @@ def test_store_clip_bit_exact(cuda, d, hk, n):
     assert np.array_equal(got_v, v8)
 
 
+def tie_heavy(n, hk, d, seed):
+    """Rows whose rotated values tie often: +-1 and +-2 (exact in bf16; no zeros before
+    the rotation); every 4th token has one lane's
+    whole span of a 16-lane row (elements 2E .. 3E - 1) at a large equal value, so that
+    its largest magnitudes all sit in one lane; every 5th token is all zeros (every
+    magnitude ties, a zero scale and zero)."""
+    g = cases.rng(seed)
+    x = g.choice(np.array([-2.0, -1.0, 1.0, 2.0], dtype=np.float32), (n, hk, d))
+    e = d // 16
+    x[::4, :, 2 * e:3 * e] = 7.0
+    x[1::5] = 0.0
+    return x
+
+
+# The sort-clip threshold (the (D - idx)-th largest magnitude) by bisection from a
+# lower bound: the one-launch path (<= 64 tokens, one wave per vector) and the large
+# path (16-lane rows in the fused launch, the exact pass for the rows it leaves), at
+# ratios whose bound is a lane's largest (need <= D / 16), its second largest, or 0
+# (need > D / 8), and at need = 1.  (A threshold of exactly 0 over a row with values of
+# both signs clips them to -0 and +0, and the sign of their minimum -- the zero point --
+# is then whatever the min reduction gives, in the reference's torch amin as here: the
+# Hadamard rotations of these rows hold up to 9.4% exact zeros, so the smallest ratio
+# here is 0.125.)
+@pytest.mark.parametrize("clips", [(0.96, 0.92), (0.5, 0.999), (0.125, 0.5)])
+@pytest.mark.parametrize("rot", ["identity", "hadamard"])
+@pytest.mark.parametrize("n", [23, 300])
+@pytest.mark.parametrize("d,hk", [(256, 1), (128, 2)])
+def test_store_clip_threshold_ties_and_bounds(cuda, d, hk, n, rot, clips):
+    bs, nb = 128, 4
+    k, v = tie_heavy(n, hk, d, 41), tie_heavy(n, hk, d, 42)
+    r = cases.hadamard_rotation(d, 43) if rot == "hadamard" else None
+    eye = np.eye(d, dtype=np.float32)
+    slots = slot_mapping(n, nb * bs, 44)
+    k8, v8 = cases.empty_caches(nb, bs, hk, d)
+    kc_, vc_ = clips
+    got_k, got_v = run_store(k, v, (k8, v8), slots, d, r, r, k_clip=kc_, v_clip=vc_)
+    rr = r if r is not None else eye
+    store_ref(clip(rotate(k, rr), kc_), clip(rotate(v, rr), vc_), k8, v8, slots)
+    assert np.array_equal(got_k, k8), f"K bytes differ at {np.argwhere(got_k != k8)[:5]}"
+    assert np.array_equal(got_v, v8), f"V bytes differ at {np.argwhere(got_v != v8)[:5]}"
+
+
 # the last request of each case is empty; with 100 blocks over 64 staging rows,
 # blocks b and b + 64 share seats (collisions resolved by the last writer)
 @pytest.mark.parametrize("qsl,seqs,nb", [([0, 700, 705, 1200, 1200], [700, 2000, 496, 10], 32),
