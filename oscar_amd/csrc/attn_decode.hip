@@ -934,7 +934,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnParams
     if (!S.deferred || v >= 2 * nkv) return;
     const int kind = v < nkv ? KIND_K : KIND_V;
     const int64_t vw = kind == KIND_K ? v : v - nkv;
-    const int64_t t = vw / hk, h = vw % hk;
+    const int64_t t = fdiv((uint32_t)vw, S.div_hk), h = vw - t * hk;
     const DestLoads dl = dest_loads(S, t);
     const f32x4 x4 = *(const f32x4*)(S.y + ((int64_t)kind * nkv + vw) * D + 4 * (lane < D / 4 ? lane : 0));
     const Dest dest = dest_finish(S, kind, t, dl);

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
   const int64_t gy = blockIdx.y;
   const int kind = gy < gkv ? KIND_K : (gy < 2 * gkv ? KIND_V : KIND_Q);
   const int64_t grp = kind == KIND_K ? gy : (kind == KIND_V ? gy - gkv : gy - 2 * gkv);
-  const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
+  const FastDiv& dh = kind == KIND_Q ? p.div_hq : p.div_hk;  // vector -> token, head
   const int64_t count = kind == KIND_Q ? nq : nkv;
   const int64_t v0 = grp * kSmallVecs;  // first vector (token * heads + head) of the group
   const int nv = count - v0 < kSmallVecs ? (int)(count - v0) : kSmallVecs;
@@ -105,15 +105,16 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
     const int v = e / (D / 8), k8 = (e % (D / 8)) * 8;
     float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (v < nv) {
-      const int64_t vi = v0 + v;
-      load8<XT>(src, (vi / heads) * src_stride + (vi % heads) * D + k8, xv);
+      const uint32_t vi = (uint32_t)(v0 + v), t = fdiv(vi, dh);
+      load8<XT>(src, (int64_t)t * src_stride + (int64_t)(vi - t * dh.d) * D + k8, xv);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) s_x[v][k8 + j] = (double)xv[j];
   }
   // the destination loads of this wave's K / V vector (the token of vector v0 +
   // wave): out with the operands, used after the products
-  const int64_t vw = v0 + wave, t = vw / hk, h = vw % hk;
+  const uint32_t vw = (uint32_t)(v0 + wave);
+  const int64_t t = fdiv(vw, p.div_hk), h = vw - (uint32_t)t * p.div_hk.d;
   DestLoads dl{};
   if (kv && !p.deferred && wave < nv) dl = dest_loads(p, t);
   __syncthreads();
@@ -162,9 +163,8 @@ __global__ __launch_bounds__(kSmallThreads) void store_small_kernel(StoreParams 
     // the seats of the call's valid tokens get the pending tag; the quantization
     // writes their final tags (every such seat has a last writer among the tokens)
     if (kind == KIND_K && blockIdx.x == 0 && tid < nv && a.stage_mode != OSCAR_STAGE_NONE) {
-      const int64_t slot = a.slot_mapping[(v0 + tid) / hk];
-      if (slot >= 0 && slot < p.capacity)
-        a.staging.owner[seat_of(slot, a.cache.block_size, a.staging.rows)] = kPendingTag;
+      const int64_t slot = a.slot_mapping[fdiv((uint32_t)(v0 + tid), p.div_hk)];
+      if (slot >= 0 && slot < p.capacity) a.staging.owner[seat_of(p, slot)] = kPendingTag;
     }
     return;
   }
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(256) void store_prep_kernel(StoreParams p) {
   if (slot < 0 || slot >= p.capacity) return;
   atomicMax((unsigned long long*)&a.slot_claims[slot], (unsigned long long)claim_value(epoch, t));
   if (a.stage_mode == OSCAR_STAGE_NONE) return;
-  const int64_t seat = seat_of(slot, a.cache.block_size, a.staging.rows);
+  const int64_t seat = seat_of(p, slot);
   if (a.stage_mode == OSCAR_STAGE_INVALIDATE) a.staging.owner[seat] = -1;
   else atomicMax((unsigned long long*)&a.seat_claims[seat], (unsigned long long)claim_value(epoch, t));
 }
@@ -581,7 +581,7 @@ __device__ __forceinline__ Dest claimed_dest(const StoreParams& p, int64_t t, in
   if (!d.valid) return d;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const long long mine = claim_value(epoch, t);
-  d.seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, a.cache.block_size, a.staging.rows) : 0;
+  d.seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(p, slot) : 0;
   d.slot_win = (long long)a.slot_claims[slot] == mine;
   d.seat_win = window && (long long)a.seat_claims[d.seat] == mine;
   d.keep = window && (flag & 1);
@@ -671,7 +671,6 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   const int64_t wg = kind == KIND_K ? b : (kind == KIND_V ? b - gkv : b - 2 * gkv);
   const int64_t nwg = kind == KIND_Q ? (int64_t)gridDim.x - 2 * gkv : gkv;
   const int64_t nvec = kind == KIND_Q ? q_vec : kv_vec;
-  const int64_t heads = kind == KIND_Q ? a.num_q_heads : hk;
   const int64_t rounds = (nvec + TV - 1) / TV;
   const int64_t per = (rounds + nwg - 1) / nwg;
   const int64_t it0 = wg * per, it1 = it0 + per < rounds ? it0 + per : rounds;
@@ -703,12 +702,13 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   // every load below is issued unconditionally (indexes clamped into range, results
   // masked at use), so the waits before their uses count exactly the loads issued since
   const int sv = tid / TPV, sq = tid % TPV;  // staging: vector, 16-element chunk
-  // vector indexes fit in 31 bits (checked on the host): 32-bit division
-  const uint32_t heads32 = (uint32_t)heads, hk32 = (uint32_t)hk;
+  // vector indexes fit in 31 bits (checked on the host): division by the call's fixed
+  // head counts
+  const FastDiv& dh = kind == KIND_Q ? p.div_hq : p.div_hk;
   auto load_x = [&](int64_t it, XChunk<XT>& xc) {
     const int64_t vec = it * TV + sv;
-    const uint32_t vc = (uint32_t)(vec < nvec ? vec : nvec - 1);
-    xc.load(src, (int64_t)(vc / heads32) * stride + (vc % heads32) * D + 16 * sq);
+    const uint32_t vc = (uint32_t)(vec < nvec ? vec : nvec - 1), t = fdiv(vc, dh);
+    xc.load(src, (int64_t)t * stride + (int64_t)(vc - t * dh.d) * D + 16 * sq);
   };
   // destination inputs of vector tid (< TV) of a K / V round, loaded one round ahead:
   // slot and window flag; the claims follow at the start of the round
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   int32_t flag_n = 0;
   auto load_slot = [&](int64_t it) {
     const int64_t vec = it * TV + tid;
-    const uint32_t t = (tid < TV && vec < kv_vec) ? (uint32_t)vec / hk32 : 0u;
+    const uint32_t t = (tid < TV && vec < kv_vec) ? fdiv((uint32_t)vec, p.div_hk) : 0u;
     slot_n = a.slot_mapping[t];
     if (window) flag_n = p.flags[t];
   };
@@ -750,7 +750,6 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
   if (rg == 0 && g == 0) s_cn[col] = cn;
   float cx = 0.f;  // the rotation term of the certification bound per unit ||x|| (first round)
   int32_t* xlist = exact_list(p, kind == KIND_V ? 1 : 0, kv_vec) + it0 * TV;  // K / V: this run's segment
-  const int seat_rows = a.staging.rows;
 
   // Rounds in a two-stage pipeline: each pass of the loop stages round it's x, then forms
   // round it's y~ (MFMA) and quantizes round it - 1.  The two waves that share a SIMD
@@ -808,7 +807,7 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
         flag = flag_n;
         const int64_t cs = slot >= 0 && slot < p.capacity ? slot : 0;
         c_slot = (long long)a.slot_claims[cs];
-        if (a.stage_mode != OSCAR_STAGE_NONE) seat = seat_of(cs, a.cache.block_size, seat_rows);
+        if (a.stage_mode != OSCAR_STAGE_NONE) seat = seat_of(p, cs);
         if (window) c_seat = (long long)a.seat_claims[seat];
       }
     }
@@ -832,15 +831,16 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
       if (kind != KIND_Q && tid < TV) {
         Dest d{};
         if (slot >= 0 && slot < p.capacity) {
-          const long long mine = claim_value(epoch, (uint32_t)(base + tid) / hk32);
+          const uint32_t t = fdiv((uint32_t)(base + tid), p.div_hk);
+          const long long mine = claim_value(epoch, t);
           d.slot = slot;
           d.seat = seat;
           d.valid = true;
           d.slot_win = c_slot == mine;
           d.seat_win = window && c_seat == mine;
           d.keep = window && (flag & 1);
-          const int64_t h = (uint32_t)(base + tid) % hk32, blk = slot / a.cache.block_size,
-                        off = slot % a.cache.block_size;
+          const int64_t h = (uint32_t)(base + tid) - t * p.div_hk.d, blk = block_of(p, slot),
+                        off = slot - blk * a.cache.block_size;
           d.koff = blk * a.cache.k_stride[0] + off * a.cache.k_stride[1] + h * a.cache.k_stride[2];
           d.voff = blk * a.cache.v_stride[0] + off * a.cache.v_stride[1] + h * a.cache.v_stride[2];
         }
@@ -918,11 +918,11 @@ __global__ __launch_bounds__(kFusedThreads) void store_fused_kernel(StoreParams 
         if (d.valid && !exact && d.seat_win) {
           if (d.keep) {
             float* dst = (kind == KIND_K ? a.staging.stage_k : a.staging.stage_v) +
-                         (d.seat * hk + (int64_t)((uint32_t)vec % hk32)) * D + l * E;
+                         (d.seat * hk + (int64_t)fmod((uint32_t)vec, p.div_hk)) * D + l * E;
 #pragma unroll
             for (int q = 0; q < E; q += 4) *(f32x4*)&dst[q] = *(const f32x4*)&y[q];
           }
-          if (kind == KIND_K && l == 0) a.staging.owner[d.seat] = d.keep ? d.slot / a.cache.block_size : -1;
+          if (kind == KIND_K && l == 0) a.staging.owner[d.seat] = d.keep ? block_of(p, d.slot) : -1;
         }
       }
     };
@@ -1016,6 +1016,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   // y of the group's vectors, rounded to fp32
   __shared__ __attribute__((aligned(16))) float s_y[G][D];
   __shared__ int32_t s_id[G];
+  __shared__ int64_t s_src[G];               // element offset of each vector in the input
   __shared__ Dest s_dst[G];
   for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
     // R's batches 0 (ra) and 1 (rb1), independent of the group: in flight during the
@@ -1024,17 +1025,36 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     load_rows(0, ra);
     if (RB < RS) load_rows(RB, rb1);
     // ---- the group's entries: each list position g0 .. g0 + G - 1 below count lies in
-    // exactly one workgroup's segment; the thread owning that workgroup fills it
+    // exactly one workgroup's segment; the thread owning that workgroup fills it (all of
+    // its reads issued before the first is used: one round trip)
     {
+      int32_t at[G];  // list index of group position j (below nvec), or -1 where another thread has it
+      int32_t e[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) at[j] = -1;
       int pre = before;
 #pragma unroll
       for (int i = 0; i < PT; ++i) {
-        const int w = PT * tid + i;
-        const int lo = pre > g0 ? pre : g0, hi = pre + cnt[i] < g0 + G ? pre + cnt[i] : g0 + G;
-        for (int q = lo; q < hi; ++q) s_id[q - g0] = list[w * seg + (q - pre)];
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+          if (g0 + j >= pre && g0 + j < pre + cnt[i]) at[j] = (int32_t)((PT * tid + i) * seg + (g0 + j - pre));
         pre += cnt[i];
       }
-      if (tid < G && g0 + tid >= count) s_id[tid] = -1;
+#pragma unroll
+      for (int j = 0; j < G; ++j)
+        if (at[j] >= 0) e[j] = list[at[j]];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (at[j] >= 0) {
+          const uint32_t id = (uint32_t)e[j];
+          s_id[j] = (int32_t)id;
+          s_src[j] = (int64_t)fdiv(id, p.div_hk) * stride + (int64_t)fmod(id, p.div_hk) * D;
+        }
+      }
+      if (tid < G && g0 + tid >= count) {
+        s_id[tid] = -1;
+        s_src[tid] = -1;
+      }
     }
     __syncthreads();
     // destination inputs of vector tid < G: slot and window flag now, the claims after
@@ -1042,14 +1062,26 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     int64_t d_slot = -1, d_t = 0;
     int32_t d_flag = 0;
     if (tid < G && s_id[tid] >= 0) {
-      d_t = s_id[tid] / hk;
+      d_t = fdiv((uint32_t)s_id[tid], p.div_hk);
       d_slot = a.slot_mapping[d_t];
       if (window) d_flag = p.flags[d_t];
     }
-    for (int i = tid; i < G * D; i += kExactThreads) {
-      const int v = i / D, k = i % D;
-      const int32_t id = s_id[v];
-      s_xd[k][v] = id >= 0 ? (double)load_elem(src, XT, (id / hk) * stride + (id % hk) * D + k) : 0.0;
+    {  // x of the group: every element's read issued before the first is used (the
+       // entries past count read element k of vector 0, masked)
+      constexpr int NI = G * D / kExactThreads;
+      static_assert(NI * kExactThreads == G * D, "exact staging shape");
+      float xs[NI];
+#pragma unroll
+      for (int r = 0; r < NI; ++r) {
+        const int i = tid + r * kExactThreads, v = i / D, k = i % D;
+        const int64_t off = s_src[v];
+        xs[r] = load_elem(src, XT, (off >= 0 ? off : 0) + k);
+      }
+#pragma unroll
+      for (int r = 0; r < NI; ++r) {
+        const int i = tid + r * kExactThreads, v = i / D, k = i % D;
+        s_xd[k][v] = s_src[v] >= 0 ? (double)xs[r] : 0.0;
+      }
     }
     __syncthreads();
     long long d_cs = -1, d_cseat = -1;
@@ -1057,7 +1089,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     const bool d_valid = d_slot >= 0 && d_slot < p.capacity;
     if (tid < G && d_valid) {
       d_cs = (long long)a.slot_claims[d_slot];
-      if (a.stage_mode != OSCAR_STAGE_NONE) d_seat = seat_of(d_slot, a.cache.block_size, a.staging.rows);
+      if (a.stage_mode != OSCAR_STAGE_NONE) d_seat = seat_of(p, d_slot);
       if (window) d_cseat = (long long)a.seat_claims[d_seat];
     }
     double acc[G][4];
@@ -1128,7 +1160,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       const int32_t id = s_id[v];
       if (id < 0) continue;
       const f32x4 y4 = *(const f32x4*)&s_y[v][4 * (lane < D / 4 ? lane : 0)];
-      quant_vector<D>(p, kind, id / hk, id % hk, s_dst[v], y4);
+      quant_vector<D>(p, kind, fdiv((uint32_t)id, p.div_hk), fmod((uint32_t)id, p.div_hk), s_dst[v], y4);
     }
     __syncthreads();  // s_id, s_xd, s_part, s_y, s_dst are rewritten by the next group
   }
@@ -1290,6 +1322,11 @@ int oscar::store_launch(const oscar_store_args_v1* args, void* stream, bool defe
       (a.query_rot != nullptr && a.num_tokens * a.num_q_heads >= (1ll << 31)))
     return fail(-22, "%s: num_tokens x heads too large for one call", fn);
   StoreParams p{a, (float*)a.workspace, a.cache.num_blocks * a.cache.block_size};
+  p.slots31 = p.capacity < (1ll << 31);
+  p.div_hk = FastDiv::of(a.cache.num_kv_heads);
+  p.div_hq = FastDiv::of(a.num_q_heads);
+  p.div_bs = FastDiv::of(a.cache.block_size);
+  p.div_rows = FastDiv::of(a.staging.rows);
   uint8_t* ws = (uint8_t*)a.workspace;
   p.exact = (int32_t*)ws;
   p.flags = (int32_t*)(ws + store_ws_list_bytes(a.num_tokens, a.cache.num_kv_heads));

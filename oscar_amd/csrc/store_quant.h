@@ -16,6 +16,23 @@ typedef float __attribute__((ext_vector_type(2))) f32x2;
 // workgroups of the fused launch per kind at most (bounds the per-workgroup exact counts)
 constexpr int kMaxFusedGroups = 1024;
 
+// Division of numerators below 2^31 by a divisor fixed for the call, as a multiply-high
+// and a shift (Granlund and Montgomery, "Division by Invariant Integers using
+// Multiplication", PLDI 1994, section 4): for 2^(l-1) < d <= 2^l and
+// m = floor(2^32 (2^l - d) / d) + 1 (below 2^32), floor(n / d) = (mulhi(m, n) + n) >> l
+// for every n < 2^32; the sum is formed in 32 bits, exact for n < 2^31 (mulhi(m, n) < n).
+struct FastDiv {
+  uint32_t d, m, l;
+  static FastDiv of(int64_t divisor) {  // divisors outside [1, 2^31) give a placeholder
+    const uint32_t d = divisor >= 1 && divisor < (1ll << 31) ? (uint32_t)divisor : 1u;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    return {d, (uint32_t)((((1ull << l) - d) << 32) / d + 1), l};
+  }
+};
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(f.m, n) + n) >> f.l; }
+__device__ __forceinline__ uint32_t fmod(uint32_t n, const FastDiv& f) { return n - fdiv(n, f) * f.d; }
+
 struct StoreParams {
   oscar_store_args_v1 a;
   float* y;          // small calls: workspace [2][num_tokens][num_kv_heads][D] fp32 (K then V)
@@ -32,6 +49,8 @@ struct StoreParams {
   int32_t deferred;  // small calls of oscar_decode_write_v1: store_small_kernel rotates only
                      // (read-path copies, rotated K / V in y, pending tags); the merge launch
                      // of the decode quantizes (quant_deferred)
+  int32_t slots31;   // capacity < 2^31: slots split into block and offset by div_bs
+  FastDiv div_hk, div_hq, div_bs, div_rows;  // num_kv_heads, num_q_heads, block_size, staging rows
 };
 
 // Owner tag of a seat that a deferred small call rewrites, from its rotation launch to
@@ -55,6 +74,17 @@ constexpr int64_t kMaxEpoch = (1ll << 39) - 1;
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, int64_t bs, int64_t rows) {
   return ((slot / bs) % rows) * bs + slot % bs;
+}
+// the same for a slot in [0, capacity), by the call's fixed divisors where they apply
+__device__ __forceinline__ int64_t seat_of(const StoreParams& p, int64_t slot) {
+  if (p.slots31) {
+    const uint32_t s = (uint32_t)slot, blk = fdiv(s, p.div_bs);
+    return (int64_t)fmod(blk, p.div_rows) * p.div_bs.d + (s - blk * p.div_bs.d);
+  }
+  return seat_of(slot, p.a.cache.block_size, p.a.staging.rows);
+}
+__device__ __forceinline__ int64_t block_of(const StoreParams& p, int64_t slot) {
+  return p.slots31 ? (int64_t)fdiv((uint32_t)slot, p.div_bs) : slot / p.a.cache.block_size;
 }
 
 // 4 floats to dtype DT at element i (8 or 16 bytes, aligned)
@@ -207,14 +237,14 @@ __device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, co
   d.keep = window && in_window(a, t, seq, end);
   d.valid = slot >= 0 && slot < p.capacity;
   if (!d.valid) return d;
-  const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(slot, bs, a.staging.rows) : 0;
+  const int64_t seat = a.stage_mode != OSCAR_STAGE_NONE ? seat_of(p, slot) : 0;
   d.seat = seat;
   // last writer: no later valid token of the call has the same slot / seat
   {
     const int64_t t2 = lane, s2 = l.s2;
     const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
     const bool later_slot = later && s2 == slot;
-    const bool later_seat = window && later && seat_of(s2 < 0 ? 0 : s2, bs, a.staging.rows) == seat;
+    const bool later_seat = window && later && seat_of(p, s2) == seat;
     d.slot_win = !__any(later_slot);
     d.seat_win = window && !__any(later_seat);
     // standalone KV update: every written seat loses its window copy
@@ -238,7 +268,7 @@ __device__ void quant_vector(const StoreParams& p, int kind, int64_t t, int64_t 
   if (!d.valid) return;
   const int64_t slot = d.slot, seat = d.seat;
   const bool slot_win = d.slot_win, seat_win = d.seat_win;
-  const int64_t blk = slot / bs, off = slot % bs;
+  const int64_t blk = block_of(p, slot), off = slot - blk * bs;
 
   if (window && seat_win) {
     const bool keep = d.keep;

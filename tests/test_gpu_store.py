@@ -318,6 +318,54 @@ def test_store_window_tags_values_and_rotated_outputs(cuda, qsl, seqs, nb):
     assert_read_copy(v_rot.float().cpu().numpy(), v, rv, n)
 
 
+@pytest.mark.parametrize("qsl,seqs", [([0, 700, 705, 1500, 1500], [700, 2000, 1000, 10]),
+                                      ([0, 100, 105, 300, 300], [100, 2000, 400, 10]),
+                                      ([0, 4, 8, 23, 23], [700, 2000, 496, 10])])
+def test_store_window_odd_geometry(cuda, qsl, seqs):
+    """Block size, head counts and staging rows that are not powers of two (the
+    kernels divide slots, vector indexes and block numbers by them): 48-slot blocks,
+    3 KV heads, 5 query heads, 50 blocks over 21 staging rows."""
+    from oscar_amd import ops
+    from oscar_amd._lib import STAGE_WRITE
+
+    d, hk, hq, bs, nb = 128, 3, 5, 48, 50
+    n = qsl[-1]
+    k = cases.kv_outliers(n, hk, d, 51)
+    v = cases.kv_outliers(n, hk, d, 52)
+    q = cases.bf16_normal((n, hq, d), 53)
+    rk, rv = cases.qr_rotation(d, 54), cases.hadamard_rotation(d, 55)
+    slots = slot_mapping(n, nb * bs, 56)
+    st = Staging(bs, hk, d, 96, 200, 1000)
+    assert st.rows == 21
+    st.owner[:] = np.arange(st.rows)[:, None]
+    st.stage_k[:] = 7.0
+    k8, v8 = cases.empty_caches(nb, bs, hk, d)
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
+    q_rot = torch.empty(n, hq, d, dtype=torch.bfloat16, device="cuda")
+    k_rot = torch.empty(n, hk, d, dtype=torch.bfloat16, device="cuda")
+    v_rot = torch.empty_like(k_rot)
+    ops.store(to_dev(k), to_dev(v), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+              rk=torch.from_numpy(rk).cuda(), rv=torch.from_numpy(rv).cuda(),
+              stage=(sk, sv, own), stage_mode=STAGE_WRITE,
+              qsl_dev=torch.tensor(qsl, dtype=torch.int32, device="cuda"),
+              seqs_dev=torch.tensor(seqs, dtype=torch.int32, device="cuda"), num_reqs=len(seqs),
+              recent_tokens=200, sink_tokens_eff=st.sink_eff, query=to_dev(q),
+              query_rot=q_rot, key_rot=k_rot, value_rot=v_rot)
+    torch.cuda.synchronize()
+    kr, vr = rotate(k, rk), rotate(v, rv)
+    store_ref(kr, vr, k8, v8, slots)
+    st.write(kr, vr, slots, qsl, seqs)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
+    assert np.array_equal(own.cpu().numpy(), st.owner)
+    assert_window(sk.cpu().numpy(), st.stage_k, k, rk, n)
+    assert_window(sv.cpu().numpy(), st.stage_v, v, rv, n)
+    assert_read_copy(q_rot.float().cpu().numpy(), q, rk, n)
+    assert_read_copy(k_rot.float().cpu().numpy(), k, rk, n)
+    assert_read_copy(v_rot.float().cpu().numpy(), v, rv, n)
+
+
 def test_standalone_update_invalidates_written_seats(cuda):
     from oscar_amd import ops
     from oscar_amd._lib import STAGE_INVALIDATE
