@@ -103,17 +103,29 @@ __device__ __forceinline__ float swap_halves(float x) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-// all-lane max / min of a full wave: four DPP steps inside each 16-lane row, then
-// the rows (lane l ^ 16, then l ^ 32).  max / min are exact, so the order is free.
-template <bool MAX>
-__device__ __forceinline__ float wave_extreme(float x) {
-  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); };
+// x of lane l ^ 16 (ds_swizzle bit mode: and mask 0x1f, xor mask 0x10; the pattern is
+// an immediate, so no lane-address register stays live across loops)
+__device__ __forceinline__ float swizzle_xor16(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
+
+// all-lane reduction of a full wave under a commutative, associative op: xor 1, xor 2
+// within each quad, the half mirror (quad pairs) and the mirror (8-lane halves) within
+// each 16-lane row, then lane l ^ 16 and l ^ 32
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
   x = op(x, dpp_row<kDppXor1>(x));
   x = op(x, dpp_row<kDppXor2>(x));
   x = op(x, dpp_row<kDppHalfMirror>(x));
   x = op(x, dpp_row<kDppMirror>(x));
-  x = op(x, __shfl_xor(x, 16));
+  x = op(x, swizzle_xor16(x));
   return op(x, swap_halves(x));
+}
+
+// all-lane max / min of a full wave (exact, so the order is free)
+template <bool MAX>
+__device__ __forceinline__ float wave_extreme(float x) {
+  return wave_reduce(x, [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); });
 }
 __device__ __forceinline__ float wave_max(float x) { return wave_extreme<true>(x); }
 __device__ __forceinline__ float wave_min(float x) { return wave_extreme<false>(x); }

@@ -27,6 +27,7 @@
 // E = word0 + 1 and stores E in word1; the fused kernel reads word1 and copies it
 // to word0 for the next call.
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "store_quant.h"
@@ -1018,13 +1019,17 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   __shared__ int32_t s_id[G];
   __shared__ int64_t s_src[G];               // element offset of each vector in the input
   __shared__ Dest s_dst[G];
-  for (int g0 = blockIdx.x * G; g0 < count; g0 += gridDim.x * G) {
+  // group size: the fewest vectors (even, at most G) that give every workgroup at most
+  // one group when the grid allows, so the products shrink with the count
+  const int per_wg = (int)((count + gridDim.x - 1) / gridDim.x);
+  const int ge = __builtin_amdgcn_readfirstlane(per_wg > G - 2 ? G : (per_wg <= 2 ? 2 : (per_wg + 1) & ~1));
+  for (int g0 = blockIdx.x * ge; g0 < count; g0 += gridDim.x * ge) {
     // R's batches 0 (ra) and 1 (rb1), independent of the group: in flight during the
     // list reads and the staging; batch b + 2 is issued when batch b's products start
     f32x4 ra[RB], rb1[RB];
     load_rows(0, ra);
     if (RB < RS) load_rows(RB, rb1);
-    // ---- the group's entries: each list position g0 .. g0 + G - 1 below count lies in
+    // ---- the group's entries: each list position g0 .. g0 + ge - 1 below count lies in
     // exactly one workgroup's segment; the thread owning that workgroup fills it (all of
     // its reads issued before the first is used: one round trip)
     {
@@ -1037,7 +1042,8 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       for (int i = 0; i < PT; ++i) {
 #pragma unroll
         for (int j = 0; j < G; ++j)
-          if (g0 + j >= pre && g0 + j < pre + cnt[i]) at[j] = (int32_t)((PT * tid + i) * seg + (g0 + j - pre));
+          if (j < ge && g0 + j >= pre && g0 + j < pre + cnt[i])
+            at[j] = (int32_t)((PT * tid + i) * seg + (g0 + j - pre));
         pre += cnt[i];
       }
 #pragma unroll
@@ -1051,7 +1057,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
           s_src[j] = (int64_t)fdiv(id, p.div_hk) * stride + (int64_t)fmod(id, p.div_hk) * D;
         }
       }
-      if (tid < G && g0 + tid >= count) {
+      if (tid < G && (tid >= ge || g0 + tid >= count)) {
         s_id[tid] = -1;
         s_src[tid] = -1;
       }
@@ -1092,41 +1098,50 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       if (a.stage_mode != OSCAR_STAGE_NONE) d_seat = seat_of(p, d_slot);
       if (window) d_cseat = (long long)a.seat_claims[d_seat];
     }
-    double acc[G][4];
+    // the products of the group's first GE vectors (the group size, a multiple of 2)
+    auto products = [&](auto ge_c) {
+      constexpr int GE = decltype(ge_c)::value;
+      double acc[GE][4];
 #pragma unroll
-    for (int v = 0; v < G; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0;
+      for (int v = 0; v < GE; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0;
 #pragma unroll 1
-    for (int kb = 0; kb < RS; kb += RB) {
-      f32x4 rn[RB];
-      if (kb + 2 * RB < RS) load_rows(kb + 2 * RB, rn);
+      for (int kb = 0; kb < RS; kb += RB) {
+        f32x4 rn[RB];
+        if (kb + 2 * RB < RS) load_rows(kb + 2 * RB, rn);
 #pragma unroll
-      for (int j = 0; j < RB; ++j) {
-        const int k = k0 + kb + j;
-        const double r0 = ra[j][0], r1 = ra[j][1], r2 = ra[j][2], r3 = ra[j][3];
+        for (int j = 0; j < RB; ++j) {
+          const int k = k0 + kb + j;
+          const double r0 = ra[j][0], r1 = ra[j][1], r2 = ra[j][2], r3 = ra[j][3];
 #pragma unroll
-        for (int v = 0; v < G; v += 2) {
-          const double2 xv = *(const double2*)&s_xd[k][v];
-          acc[v][0] = fma(xv.x, r0, acc[v][0]);
-          acc[v][1] = fma(xv.x, r1, acc[v][1]);
-          acc[v][2] = fma(xv.x, r2, acc[v][2]);
-          acc[v][3] = fma(xv.x, r3, acc[v][3]);
-          acc[v + 1][0] = fma(xv.y, r0, acc[v + 1][0]);
-          acc[v + 1][1] = fma(xv.y, r1, acc[v + 1][1]);
-          acc[v + 1][2] = fma(xv.y, r2, acc[v + 1][2]);
-          acc[v + 1][3] = fma(xv.y, r3, acc[v + 1][3]);
+          for (int v = 0; v < GE; v += 2) {
+            const double2 xv = *(const double2*)&s_xd[k][v];
+            acc[v][0] = fma(xv.x, r0, acc[v][0]);
+            acc[v][1] = fma(xv.x, r1, acc[v][1]);
+            acc[v][2] = fma(xv.x, r2, acc[v][2]);
+            acc[v][3] = fma(xv.x, r3, acc[v][3]);
+            acc[v + 1][0] = fma(xv.y, r0, acc[v + 1][0]);
+            acc[v + 1][1] = fma(xv.y, r1, acc[v + 1][1]);
+            acc[v + 1][2] = fma(xv.y, r2, acc[v + 1][2]);
+            acc[v + 1][3] = fma(xv.y, r3, acc[v + 1][3]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          ra[j] = rb1[j];
+          rb1[j] = rn[j];
         }
       }
 #pragma unroll
-      for (int j = 0; j < RB; ++j) {
-        ra[j] = rb1[j];
-        rb1[j] = rn[j];
+      for (int v = 0; v < GE; ++v) {
+        s_part[sl][v][0][cq] = double2{acc[v][0], acc[v][1]};
+        s_part[sl][v][1][cq] = double2{acc[v][2], acc[v][3]};
       }
-    }
-#pragma unroll
-    for (int v = 0; v < G; ++v) {
-      s_part[sl][v][0][cq] = double2{acc[v][0], acc[v][1]};
-      s_part[sl][v][1][cq] = double2{acc[v][2], acc[v][3]};
-    }
+    };
+    static_assert(G == 8, "group sizes 2, 4, 6, 8");
+    if (ge > 6) products(std::integral_constant<int, 8>{});
+    else if (ge > 4) products(std::integral_constant<int, 6>{});
+    else if (ge > 2) products(std::integral_constant<int, 4>{});
+    else products(std::integral_constant<int, 2>{});
     if (tid < G) {  // the destination of vector tid, from its claims
       Dest d{};
       d.slot = d_slot;
@@ -1143,6 +1158,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     __syncthreads();
     for (int i = tid; i < G * NQ; i += kExactThreads) {  // four columns of one vector each
       const int v = i / NQ, q = i % NQ;
+      if (v >= ge) continue;
       double y0 = 0.0, y1 = 0.0, y2 = 0.0, y3 = 0.0;
 #pragma unroll 4
       for (int s = 0; s < S; ++s) {

@@ -115,9 +115,9 @@ __device__ __forceinline__ void store4(void* base, int64_t i, const float* y) {
 // Once the interval holds exactly one element (c_hi - c_lo == 1) that element is the
 // answer, gathered by an OR over the wave; an interval one value wide gives lo (ties).
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) x = min(x, (uint32_t)__shfl_xor((int)x, o));
-  return x;
+  return __float_as_uint(wave_reduce(__uint_as_float(x), [](float a, float b) {
+    return __uint_as_float(min(__float_as_uint(a), __float_as_uint(b)));
+  }));
 }
 template <int D>
 __device__ float wave_kth_abs(f32x4 x4, int idx) {
@@ -131,12 +131,12 @@ __device__ float wave_kth_abs(f32x4 x4, int idx) {
     m2 = max(m2, min(m1, w));
     m1 = max(m1, w);
   }
-#pragma unroll
-  for (int o = 1; o < 4; o <<= 1) {  // the two largest of the lane quad
-    const uint32_t o1 = (uint32_t)__shfl_xor((int)m1, o), o2 = (uint32_t)__shfl_xor((int)m2, o);
+  auto quad_top2 = [&](uint32_t o1, uint32_t o2) {  // merge another lane's two largest
     m2 = max(min(m1, o1), max(m2, o2));
     m1 = max(m1, o1);
-  }
+  };
+  quad_top2(__float_as_uint(dpp_row<kDppXor1>(__uint_as_float(m1))), __float_as_uint(dpp_row<kDppXor1>(__uint_as_float(m2))));
+  quad_top2(__float_as_uint(dpp_row<kDppXor2>(__uint_as_float(m1))), __float_as_uint(dpp_row<kDppXor2>(__uint_as_float(m2))));
   const int need = D - idx;
   uint32_t lo = wave_min_u32(active ? (need <= D / 16 ? m1 : (need <= D / 8 ? m2 : 0u)) : 0xffffffffu);
   uint32_t hi = ~wave_min_u32(~m1) + 1u;  // the maximum + 1 (<= 2^31)
@@ -159,8 +159,9 @@ __device__ float wave_kth_abs(f32x4 x4, int idx) {
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     if (u[j] >= lo && u[j] < hi) m |= u[j];
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o);
+  m = __float_as_uint(wave_reduce(__uint_as_float(m), [](float a, float b) {
+    return __uint_as_float(__float_as_uint(a) | __float_as_uint(b));
+  }));
   return __uint_as_float(c_hi - c_lo == 1 ? m : lo);
 }
 
