@@ -971,12 +971,16 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   const int cq = tid % NQ, sl = tid / NQ;    // column quad, row slice
   const int k0 = sl * RS;
-  auto load_rows = [&](int kb, f32x4* r) {   // R[k][4 cq ..], k = k0 + kb + j (identity for NULL)
+  // R[k][4 cq ..], k = k0 + kb + j; the identity for a NULL R (IDENT, a separate copy of
+  // the group loop, so the loads carry no branch that would make the compiler wait)
+  auto load_rows = [&](auto ident, int kb, f32x4* r) {
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int k = k0 + kb + j, o = k - 4 * cq;
-      if (R != nullptr) r[j] = *(const f32x4*)(R + (int64_t)k * D + 4 * cq);
-      else r[j] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
+      if constexpr (decltype(ident)::value)
+        r[j] = f32x4{o == 0 ? 1.f : 0.f, o == 1 ? 1.f : 0.f, o == 2 ? 1.f : 0.f, o == 3 ? 1.f : 0.f};
+      else
+        r[j] = *(const f32x4*)(R + (int64_t)k * D + 4 * cq);
     }
   };
 
@@ -1023,12 +1027,13 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
   // one group when the grid allows, so the products shrink with the count
   const int per_wg = (int)((count + gridDim.x - 1) / gridDim.x);
   const int ge = __builtin_amdgcn_readfirstlane(per_wg > G - 2 ? G : (per_wg <= 2 ? 2 : (per_wg + 1) & ~1));
+  auto group_loop = [&](auto ident) {
   for (int g0 = blockIdx.x * ge; g0 < count; g0 += gridDim.x * ge) {
     // R's batches 0 (ra) and 1 (rb1), independent of the group: in flight during the
     // list reads and the staging; batch b + 2 is issued when batch b's products start
     f32x4 ra[RB], rb1[RB];
-    load_rows(0, ra);
-    if (RB < RS) load_rows(RB, rb1);
+    load_rows(ident, 0, ra);
+    if (RB < RS) load_rows(ident, RB, rb1);
     // ---- the group's entries: each list position g0 .. g0 + ge - 1 below count lies in
     // exactly one workgroup's segment; the thread owning that workgroup fills it (all of
     // its reads issued before the first is used: one round trip)
@@ -1064,14 +1069,13 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     }
     __syncthreads();
     // destination inputs of vector tid < G: slot and window flag now, the claims after
-    // the staging (in flight during the products)
-    int64_t d_slot = -1, d_t = 0;
-    int32_t d_flag = 0;
-    if (tid < G && s_id[tid] >= 0) {
-      d_t = fdiv((uint32_t)s_id[tid], p.div_hk);
-      d_slot = a.slot_mapping[d_t];
-      if (window) d_flag = p.flags[d_t];
-    }
+    // the staging (in flight during the products).  Every thread reads them (token 0
+    // where it has no vector), with no branch: nothing then waits for these reads
+    // before the staging's reads go out.
+    const int32_t d_id = tid < G ? s_id[tid] : -1;
+    const int64_t d_t = fdiv((uint32_t)(d_id >= 0 ? d_id : 0), p.div_hk);
+    const int64_t d_slot_in = a.slot_mapping[d_t];
+    const int32_t d_flag = p.flags[d_t];
     {  // x of the group: every element's read issued before the first is used (the
        // entries past count read element k of vector 0, masked)
       constexpr int NI = G * D / kExactThreads;
@@ -1092,6 +1096,7 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     __syncthreads();
     long long d_cs = -1, d_cseat = -1;
     int64_t d_seat = 0;
+    const int64_t d_slot = d_id >= 0 ? d_slot_in : -1;
     const bool d_valid = d_slot >= 0 && d_slot < p.capacity;
     if (tid < G && d_valid) {
       d_cs = (long long)a.slot_claims[d_slot];
@@ -1104,14 +1109,15 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
       double acc[GE][4];
 #pragma unroll
       for (int v = 0; v < GE; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0;
-#pragma unroll 1
-      for (int kb = 0; kb < RS; kb += RB) {
-        f32x4 rn[RB];
-        if (kb + 2 * RB < RS) load_rows(kb + 2 * RB, rn);
+      // batches by parity in two fixed register sets (ra: even, rb1: odd), each refilled
+      // two batches ahead as soon as its products are issued, unconditionally (the last
+      // two refills re-read the last batch, just fetched): no register copies and no
+      // merges of loaded and unloaded values, so the waits count exactly
+      auto batch = [&](int b, const f32x4* r) {
 #pragma unroll
         for (int j = 0; j < RB; ++j) {
-          const int k = k0 + kb + j;
-          const double r0 = ra[j][0], r1 = ra[j][1], r2 = ra[j][2], r3 = ra[j][3];
+          const int k = k0 + b * RB + j;
+          const double r0 = r[j][0], r1 = r[j][1], r2 = r[j][2], r3 = r[j][3];
 #pragma unroll
           for (int v = 0; v < GE; v += 2) {
             const double2 xv = *(const double2*)&s_xd[k][v];
@@ -1125,10 +1131,20 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
             acc[v + 1][3] = fma(xv.y, r3, acc[v + 1][3]);
           }
         }
-#pragma unroll
-        for (int j = 0; j < RB; ++j) {
-          ra[j] = rb1[j];
-          rb1[j] = rn[j];
+      };
+      constexpr int NB = RS / RB;  // batches
+      static_assert(NB == 1 || NB % 2 == 0, "batches in pairs");
+      if constexpr (NB == 1) {
+        batch(0, ra);
+      } else {
+#pragma unroll 1
+        for (int b = 0; b < NB; b += 2) {
+          batch(b, ra);
+          load_rows(ident, (b + 2 < NB ? b + 2 : NB - 1) * RB, ra);
+          __builtin_amdgcn_sched_barrier(0);  // the refill stays ahead of the odd batch
+          batch(b + 1, rb1);
+          load_rows(ident, (b + 3 < NB ? b + 3 : NB - 1) * RB, rb1);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
@@ -1180,6 +1196,9 @@ __global__ __launch_bounds__(kExactThreads) void store_exact_kernel(StoreParams 
     }
     __syncthreads();  // s_id, s_xd, s_part, s_y, s_dst are rewritten by the next group
   }
+  };
+  if (R != nullptr) group_loop(std::false_type{});
+  else group_loop(std::true_type{});
 }
 
 template <int D, int XT>
