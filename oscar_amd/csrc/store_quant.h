@@ -186,29 +186,35 @@ __device__ __forceinline__ bool in_window(const oscar_store_args_v1& a, int64_t 
 // load (the token's slot, lane l's request-table entry and lane l's slot of the
 // call), dest_finish decides.  A call has at most kFusedTokens (64) tokens, so one
 // slot per lane covers it; requests past the first 64 are read in dest_finish.
+// The raw reads, all issued at once and without a branch (lanes with nothing to read
+// read entry 0 of a valid array); dest_finish masks them.  A select or widening right
+// after a read would make the compiler wait for each read in turn.
 struct DestLoads {
-  int64_t slot;     // slot_mapping[t]
-  int64_t s2;       // slot_mapping[lane] (-1 past the call)
-  int64_t st, nx, sq;  // query_start_loc[lane], [lane + 1], seq_lens[lane]
+  int64_t slot;        // slot_mapping[t]
+  int64_t s2;          // slot_mapping[lane] (lanes past the call: entry 0)
+  int32_t st, nx, sq;  // query_start_loc[lane], [lane + 1], seq_lens[lane] (lanes past the
+                       // requests, or no window: entries 0 and 1 of slot_mapping's words)
 };
 
 __device__ __forceinline__ DestLoads dest_loads(const StoreParams& p, int64_t t) {
   const oscar_store_args_v1& a = p.a;
   const int lane = threadIdx.x & 63;
+  const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
+  const int32_t* qsl = window ? a.query_start_loc : reinterpret_cast<const int32_t*>(a.slot_mapping);
+  const int32_t* sql = window ? a.seq_lens : reinterpret_cast<const int32_t*>(a.slot_mapping);
+  const int r = window && lane < a.num_reqs ? lane : 0;
   DestLoads l;
   l.slot = a.slot_mapping[t];
-  l.s2 = lane < a.num_tokens ? a.slot_mapping[lane] : -1;
-  const bool in = lane < a.num_reqs && a.stage_mode == OSCAR_STAGE_WRITE;
-  l.st = in ? a.query_start_loc[lane] : a.num_tokens;
-  l.nx = in ? a.query_start_loc[lane + 1] : a.num_tokens;
-  l.sq = in ? a.seq_lens[lane] : 0;
+  l.s2 = a.slot_mapping[lane < a.num_tokens ? lane : 0];
+  l.st = qsl[r];
+  l.nx = qsl[r + 1];
+  l.sq = sql[r];
   return l;
 }
 
 __device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, const DestLoads& l) {
   const oscar_store_args_v1& a = p.a;
   const int lane = threadIdx.x & 63;
-  const int64_t bs = a.cache.block_size;
   const bool window = a.stage_mode == OSCAR_STAGE_WRITE;
   Dest d{};
   const int64_t slot = l.slot;
@@ -219,18 +225,21 @@ __device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, co
     for (int c0 = 0; c0 < a.num_reqs; c0 += 64) {
       const int r = c0 + lane;
       const bool in = r < a.num_reqs;
-      int64_t st = l.st, nx = l.nx, sq = l.sq;
+      int64_t st = in ? l.st : a.num_tokens, nx = in ? l.nx : a.num_tokens, sq = in ? l.sq : 0;
       if (c0 > 0) {
         st = in ? a.query_start_loc[r] : a.num_tokens;
         nx = in ? a.query_start_loc[r + 1] : a.num_tokens;
         sq = in ? a.seq_lens[r] : 0;
       }
       const int64_t start = st < a.num_tokens ? st : a.num_tokens;
+      // the shuffles run whatever the ballot (so the reads stay where dest_loads issued
+      // them instead of sinking into the taken branch)
       const uint64_t bal = __ballot(in && start <= t);
+      const int last = bal ? 63 - __builtin_clzll(bal) : 0;
+      const int64_t sq_last = __shfl(sq, last), nx_last = __shfl(nx, last);
       if (bal) {
-        const int last = 63 - __builtin_clzll(bal);
-        seq = __shfl(sq, last);
-        end = __shfl(nx, last);
+        seq = sq_last;
+        end = nx_last;
       }
     }
   }
@@ -242,7 +251,7 @@ __device__ inline Dest dest_finish(const StoreParams& p, int kind, int64_t t, co
   d.seat = seat;
   // last writer: no later valid token of the call has the same slot / seat
   {
-    const int64_t t2 = lane, s2 = l.s2;
+    const int64_t t2 = lane, s2 = lane < a.num_tokens ? l.s2 : -1;
     const bool later = t2 > t && s2 >= 0 && s2 < p.capacity;
     const bool later_slot = later && s2 == slot;
     const bool later_seat = window && later && seat_of(p, s2) == seat;
