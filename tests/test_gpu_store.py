@@ -366,6 +366,59 @@ def test_store_window_odd_geometry(cuda, qsl, seqs):
     assert_read_copy(v_rot.float().cpu().numpy(), v, rv, n)
 
 
+@pytest.mark.parametrize("n", [23, 1500])  # one-launch path / three launches
+def test_store_capacity_past_31_bits(cuda, n):
+    """A cache of 2^31 + 2048 slots, where the kernels split slots into block and offset
+    with 64-bit division: every block aliases one real block (block stride 0) and the
+    tokens' slots lie at distinct offsets of far blocks, so the bytes land in the real
+    block at those offsets; seats and owner tags follow the far blocks."""
+    import ctypes as C
+
+    from oscar_amd import _lib, ops
+    from oscar_amd._lib import STAGE_WRITE
+
+    d, hk, bs = 256, 1, 2048
+    nb = (1 << 31) // bs + 1
+    g = cases.rng(61)
+    offs = g.permutation(bs)[:n].astype(np.int64)
+    blocks = (nb - 1 - g.integers(0, 5000, n)).astype(np.int64)
+    blocks[::3] = nb - 1  # slots at and past 2^31
+    slots = blocks * bs + offs
+    slots[g.random(n) < 0.05] = -1
+    assert slots.max() >= 1 << 31
+    k = cases.kv_outliers(n, hk, d, 62)
+    v = cases.kv_outliers(n, hk, d, 63)
+    rk, rv = cases.hadamard_rotation(d, 64), cases.qr_rotation(d, 65)
+    st = Staging(bs, hk, d, 0, 256, 4 * bs)
+    qsl, seqs = [0, n], [n + 100]
+    k8, v8 = cases.empty_caches(1, bs, hk, d)
+    kc, vc = cache_dev(k8), cache_dev(v8)
+    sk, sv, own = (torch.from_numpy(a.copy()).cuda() for a in st.arrays())
+    args, keep = ops.store_args(
+        to_dev(k), to_dev(v), kc, vc, torch.from_numpy(slots).cuda(), head_dim=d,
+        rk=torch.from_numpy(rk).cuda(), rv=torch.from_numpy(rv).cuda(), stage=(sk, sv, own),
+        stage_mode=STAGE_WRITE, qsl_dev=torch.tensor(qsl, dtype=torch.int32, device="cuda"),
+        seqs_dev=torch.tensor(seqs, dtype=torch.int32, device="cuda"), num_reqs=1,
+        recent_tokens=256, sink_tokens_eff=0)
+    args.cache.num_blocks = nb
+    args.cache.k_stride[0] = 0
+    args.cache.v_stride[0] = 0
+    claims = torch.zeros(nb * bs, dtype=torch.int64, device="cuda")  # 16 GiB, one per slot
+    args.slot_claims = claims.data_ptr()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.load().oscar_store_v1(C.byref(args), stream), "oscar_store_v1")
+    torch.cuda.synchronize()
+    del claims, keep
+    kr, vr = rotate(k, rk), rotate(v, rv)
+    store_ref(kr, vr, k8, v8, np.where(slots >= 0, slots % bs, -1))
+    st.write(kr, vr, slots, qsl, seqs)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
+    assert np.array_equal(own.cpu().numpy(), st.owner)
+    assert_window(sk.cpu().numpy(), st.stage_k, k, rk, n)
+    assert_window(sv.cpu().numpy(), st.stage_v, v, rv, n)
+
+
 def test_standalone_update_invalidates_written_seats(cuda):
     from oscar_amd import ops
     from oscar_amd._lib import STAGE_INVALIDATE
