@@ -318,13 +318,15 @@ def test_store_window_tags_values_and_rotated_outputs(cuda, qsl, seqs, nb):
     assert_read_copy(v_rot.float().cpu().numpy(), v, rv, n)
 
 
+@pytest.mark.parametrize("clips", [(0.0, 0.0), (0.96, 0.92)])
 @pytest.mark.parametrize("qsl,seqs", [([0, 700, 705, 1500, 1500], [700, 2000, 1000, 10]),
                                       ([0, 100, 105, 300, 300], [100, 2000, 400, 10]),
                                       ([0, 4, 8, 23, 23], [700, 2000, 496, 10])])
-def test_store_window_odd_geometry(cuda, qsl, seqs):
+def test_store_window_odd_geometry(cuda, qsl, seqs, clips):
     """Block size, head counts and staging rows that are not powers of two (the
     kernels divide slots, vector indexes and block numbers by them): 48-slot blocks,
-    3 KV heads, 5 query heads, 50 blocks over 21 staging rows."""
+    3 KV heads, 5 query heads, 50 blocks over 21 staging rows; with and without the
+    serve defaults' sort clip (the bytes of clipped values, the window unclipped)."""
     from oscar_amd import ops
     from oscar_amd._lib import STAGE_WRITE
 
@@ -351,10 +353,10 @@ def test_store_window_odd_geometry(cuda, qsl, seqs):
               qsl_dev=torch.tensor(qsl, dtype=torch.int32, device="cuda"),
               seqs_dev=torch.tensor(seqs, dtype=torch.int32, device="cuda"), num_reqs=len(seqs),
               recent_tokens=200, sink_tokens_eff=st.sink_eff, query=to_dev(q),
-              query_rot=q_rot, key_rot=k_rot, value_rot=v_rot)
+              query_rot=q_rot, key_rot=k_rot, value_rot=v_rot, k_clip=clips[0], v_clip=clips[1])
     torch.cuda.synchronize()
     kr, vr = rotate(k, rk), rotate(v, rv)
-    store_ref(kr, vr, k8, v8, slots)
+    store_ref(clip(kr, clips[0]), clip(vr, clips[1]), k8, v8, slots)
     st.write(kr, vr, slots, qsl, seqs)
     assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), k8)
     assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), v8)
