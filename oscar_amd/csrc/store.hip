@@ -232,13 +232,6 @@ __device__ __forceinline__ bool row_all(bool pred) {
   return ((m >> (threadIdx.x & 48)) & 0xffffull) == 0xffffull;
 }
 
-__device__ __forceinline__ uint32_t row_or(uint32_t x) {
-  x |= (uint32_t)dpp_row_i<kDppXor1>((int)x);
-  x |= (uint32_t)dpp_row_i<kDppXor2>((int)x);
-  x |= (uint32_t)dpp_row_i<kDppHalfMirror>((int)x);
-  return x | (uint32_t)dpp_row_i<kDppMirror>((int)x);
-}
-
 // the median of three (v_med3_u32)
 __device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
   uint32_t r;
@@ -265,9 +258,9 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t x) {
 // each lane's k-th largest, k = 1 while D - idx <= 16, 2 while <= 32 (each of the 16
 // lanes holds k elements >= lo, so at least D - idx do and a >= lo), else 0.  c_lo .. c_hi
 // bound the ranks inside the interval; a row whose interval holds exactly one element
-// stops there and takes that element (an OR over the row; every other element
-// contributes 0), a row whose interval is one value wide takes lo (ties).  The loop runs
-// while any row of the wave is open.
+// stops there and takes that element (the row's smallest element at or above lo), a row
+// whose interval is one value wide takes lo (ties).  The loop runs while any row of the
+// wave is open.
 template <int E>
 __device__ float row_kth_abs(const float* y, int idx) {
   constexpr int N = 16 * E;
@@ -284,7 +277,7 @@ __device__ float row_kth_abs(const float* y, int idx) {
   uint32_t hi = row_max_u32(m1) + 1u;  // <= 2^31: every element and candidate is below
   int c_lo = 0, c_hi = N;  // c_lo: a lower bound of count(|y| < lo) until lo first moves
   bool open = hi - lo > 1;
-  while (__any(open)) {
+  auto bisect = [&]() {
     // an open row has lo < mid < hi: med3(u, mid - 1, mid) is mid - 1 for u < mid and mid
     // otherwise, so the lane's sum is E (mid - 1) + count(u >= mid) (mod 2^32)
     const uint32_t mid = lo + ((hi - lo) >> 1);
@@ -298,13 +291,19 @@ __device__ float row_kth_abs(const float* y, int idx) {
     hi = down ? mid : hi;
     c_hi = down ? cnt : c_hi;
     open = hi - lo > 1 && c_hi - c_lo > 1;
+  };
+  // two steps per test of the wave (a closed row's step changes nothing)
+  while (__any(open)) {
+    bisect();
+    bisect();
   }
-  uint32_t m = 0;
+  // the one element of [lo, hi) when c_hi - c_lo == 1 is the row's smallest element at or
+  // above lo (u - lo wraps past 2^31 for the elements below lo)
+  uint32_t dmin = 0xffffffffu;
 #pragma unroll
-  for (int j = 0; j < E; ++j)
-    if (u[j] >= lo && u[j] < hi) m |= u[j];
-  m = row_or(m);
-  return __uint_as_float(c_hi - c_lo == 1 ? m : lo);
+  for (int j = 0; j < E; ++j) dmin = min(dmin, u[j] - lo);
+  dmin = row_min_u32(dmin);
+  return __uint_as_float(c_hi - c_lo == 1 ? lo + dmin : lo);
 }
 
 // Certify and quantize the rows' vectors from y~ (lane: y[E] of its row's vector).  The
