@@ -76,7 +76,7 @@ extern "C" int oscar_context_create_v1(int32_t device, oscar_context_v1** out) {
   for (int i = 0; !rc && i < kRingSlots; ++i)
     if (hipEventCreateWithFlags(&c->done[i], hipEventDisableTiming) != hipSuccess)
       rc = fail(-12, "oscar_context_create_v1: event creation failed");
-  hipSetDevice(prev);
+  (void)hipSetDevice(prev);  // restore the caller's device (best effort)
   if (rc) {
     oscar_context_destroy_v1(c);
     return rc;
@@ -87,18 +87,19 @@ extern "C" int oscar_context_create_v1(int32_t device, oscar_context_v1** out) {
 
 extern "C" int oscar_context_destroy_v1(oscar_context_v1* c) {
   if (!c) return 0;
+  // teardown is best effort: a failing call leaves nothing more to release
   int prev = -1;
-  hipGetDevice(&prev);
-  hipSetDevice(c->device);
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(c->device);
   for (int i = 0; i < kRingSlots; ++i) {
     if (c->done[i]) {
-      hipEventSynchronize(c->done[i]);
-      hipEventDestroy(c->done[i]);
+      (void)hipEventSynchronize(c->done[i]);
+      (void)hipEventDestroy(c->done[i]);
     }
   }
-  if (c->dev_ring) hipFree(c->dev_ring);
-  if (c->host_ring) hipHostFree(c->host_ring);
-  hipSetDevice(prev);
+  if (c->dev_ring) (void)hipFree(c->dev_ring);
+  if (c->host_ring) (void)hipHostFree(c->host_ring);
+  (void)hipSetDevice(prev);
   delete c;
   return 0;
 }
