@@ -87,6 +87,9 @@ DECODE_CASES = [
     ("chunk_d128_hk2", [1500, 40], [20, 9], {"d": 128, "hk": 2, "group": 4}),
     ("chunk_no_window", [2000], [33], {"window": False, "target": 16}),
     ("cache_only_long", [2000, 100], [12, 20], {"fresh": False}),
+    # items of one tile each, history and window tiles alike: wave 0's state is the
+    # item's partial (no cross-wave merge)
+    ("one_tile_items", [4000, 40], [1, 3], {"fresh": False, "target": 200, "hint": (0, 0), "one_tile": True}),
 ]
 
 
@@ -98,7 +101,10 @@ def test_decode_matches_oracle(cuda, name, prefixes, lengths, opts):
     c = cases.make_case(prefixes, lengths, d=d, hk=hk, group=group, bs=opts.get("bs", 128),
                         fresh=opts.get("fresh", True), window=opts.get("window", True),
                         key_ramp=opts.get("key_ramp", 0.0), legacy=opts.get("legacy", False))
-    out, lse, _ = run_decode(c, d, hk, group, opts.get("target", 256), opts.get("hint"))
+    out, lse, plan = run_decode(c, d, hk, group, opts.get("target", 256), opts.get("hint"))
+    if opts.get("one_tile"):
+        counts = plan.host_items.reshape(plan.num_items, -1)[:, 4]  # tiles per item (record word 4)
+        assert (counts == 1).sum() >= 100, f"{name}: {(counts == 1).sum()} one-tile items"
     ref_out, ref_lse = attention_ref(c["q"], c["k"], c["v"], c["k8"], c["v8"], c["bt"], c["qsl"],
                                      c["seqs"], c["scale"], c["stage"], d=d)
     check(out, lse, ref_out, ref_lse, name)
