@@ -875,26 +875,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
   f32x4* po = (f32x4*)(P.part_o + (int64_t)part * 32 * D);
   // only the item's rows move through LDS (lane l and thread t hold row l % 32 / t % 32)
   const bool my_row = (lane & 31) < nrows;
-  if (count == 1) {
-    // an item of one tile (a slow one, typically): wave 0 ran it and the other waves
-    // hold O = 0, m = -inf, so wave 0's scaled state is the partial; f32x4 (bb, q, lane)
-    // of its round rb is index 2 rb * kThreads + (4 bb + q) 64 + lane, as below
-    if (wave == 0 && my_row) {
-#pragma unroll
-      for (int rb = 0; rb < C::MBLK / 4; ++rb)
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x16& Ob = O[4 * rb + bb];
-            store_through(po, 2 * rb * kThreads + (4 * bb + q) * 64 + lane,
-                          f32x4{Ob[4 * q] * fw, Ob[4 * q + 1] * fw, Ob[4 * q + 2] * fw, Ob[4 * q + 3] * fw});
-          }
-    }
-  } else {
+  // an item of one tile (a slow one, typically): wave 0 ran it and the other waves hold
+  // O = 0, m = -inf, so only wave 0 writes and each thread reads wave 0's value alone
+  const bool one = count == 1;
 #pragma unroll
   for (int rb = 0; rb < C::MBLK / 4; ++rb) {
-    if (my_row) {
+    if (my_row && (!one || wave == 0)) {
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
@@ -911,13 +897,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_main_kernel(AttnParams P) {
       for (int h = 0; h < 2; ++h) {
         const int e = h * kThreads + tid;
         f32x4 acc = buf[e];
+        if (!one) {
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) acc += buf[w * 2 * kThreads + e];
+          for (int w = 1; w < kWaves; ++w) acc += buf[w * 2 * kThreads + e];
+        }
         store_through(po, 2 * rb * kThreads + e, acc);
       }
     }
     __syncthreads();
-  }
   }
   if (tid < 32) {
     float lse = (L > 0.f && M != -INFINITY) ? (M + log2f(L)) * kLn2 : -INFINITY;
